@@ -1,0 +1,110 @@
+/* qw35_hip.h — C ABI of the MI355X (gfx950) quantized matvec/matmul engine.
+ *
+ * Drop-in for the projection path behind the qw35-server engine-side kernel
+ * API.  Conventions follow the reference FFI (qw35-server/src/metal/bridge/Qw35FFI.h:1-4):
+ *   - every function reports failure by returning 0 (or NULL) and writing a
+ *     NUL-terminated message into the caller-provided `err` buffer; success is 1;
+ *   - nothing throws across the ABI; GPU execution is asynchronous on the
+ *     caller's stream and device-side faults surface at the next
+ *     qw35_hip_sync (as they surface at the next wait in the reference,
+ *     Qw35FFI.h:87-88).
+ * Pointers marked "device" are HBM addresses (hipMalloc'd or offsets into an
+ * uploaded model image).  `stream` is a hipStream_t (NULL = default stream).
+ * Calls on one stream are ordered; the library keeps no global mutable state
+ * except its plans, which are single-threaded objects (like MetalRuntime,
+ * `Send` but not `Sync`, qw35-server/src/metal/bridge.rs:257).
+ *
+ * Weight formats are the reference's raw GGUF tensor bytes (no repacking):
+ *   type 100  GF4   8 elems / 4 B   (tools/gguf_custom_types.py:26-30)
+ *   type   8  q8_0 32 elems / 34 B  (qw35-server/src/loader/tensors.rs:144)
+ *   type  12  Q4_K 256 elems / 144 B (qw35-server/src/loader/tensors.rs:148)
+ * Shape limits of this build: k % 256 == 0 and 256 <= k <= 12288 (every
+ * Qwen3.5-9B projection has k = 4096 or 12288), rows >= 1, n_batch 1..8.
+ */
+#ifndef QW35_HIP_H
+#define QW35_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QW35_HIP_TYPE_Q8_0 8u
+#define QW35_HIP_TYPE_Q4_K 12u
+#define QW35_HIP_TYPE_GF4 100u
+#define QW35_HIP_MAX_BATCH 8u
+
+/* GGUF tensor descriptor; field-for-field the reference's
+ * qw35_metal_tensor_desc (qw35-server/src/metal/bridge/Qw35MetalTypes.h:18-27),
+ * so the Rust #[repr(C)] mirror in bridge.rs is reused unchanged. */
+typedef struct {
+    const uint8_t *name;
+    uintptr_t name_len;
+    uint64_t dims[4]; /* dims[0] = k (columns), dims[1] = rows */
+    uint32_t n_dims;
+    uint32_t type_id;
+    uint64_t abs_offset; /* byte offset of the tensor data in the model image */
+    uint64_t bytes;
+    uint64_t elements;
+} qw35_hip_tensor_desc;
+
+/* A weight matrix resident in device memory (raw GGUF bytes, row-major). */
+typedef struct {
+    const void *data; /* device, 16-byte aligned */
+    uint64_t k;       /* columns = dims[0] */
+    uint64_t rows;    /* dims[1] */
+    uint64_t bytes;   /* rows * row_bytes(type, k) */
+    uint32_t type_id; /* QW35_HIP_TYPE_* */
+    uint32_t reserved;
+} qw35_hip_weight;
+
+/* 1 if a HIP device is present.  Replaces qw35_metal_has_device (Qw35FFI.h:18-19). */
+int qw35_hip_has_device(void);
+
+/* Validate a GGUF tensor descriptor and build the device view
+ * data = device_base + desc->abs_offset.  Replaces the no-copy tensor view
+ * creation of Qw35TensorStore (Qw35TensorStore.m:58-153) plus the per-type
+ * byte-size rule of tensor_nbytes (qw35-server/src/loader/tensors.rs:123-172). */
+int qw35_hip_weight_view(const qw35_hip_tensor_desc *desc, const void *device_base, qw35_hip_weight *out,
+                         char *err, uintptr_t err_len);
+
+/* Decode GEMV, batch 1..8:
+ *   dst[b][r] (+)= sum_k W[r][k] * awq[k] * x[b][k]    (awq == NULL: 1)
+ * x: device fp32 [n_batch][k] (16-byte aligned rows); dst: device fp32
+ * [n_batch][rows]; residual != 0 adds into dst.  Replaces
+ * encodeDecodeMatvecTensor:weight:input:inputOffset:dst:residual:
+ * (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:184-256); the input
+ * offset of the reference is folded into `x`.  awq is the explicit form of
+ * the AWQ per-input-channel scale that the reference folds into the norm
+ * weight (tools/cook_qw35_awq_gf4.py:112-114). */
+int qw35_hip_decode_matvec(const qw35_hip_weight *w, const float *x, const float *awq, float *dst,
+                           uint32_t n_batch, int residual, void *stream, char *err, uintptr_t err_len);
+
+/* Fused gate/up GEMV + SwiGLU, batch 1..8:
+ *   dst[b][r] = silu(gate[r] . (awq*x[b])) * (up[r] . (awq*x[b])),  silu(v) = v / (1 + exp(-v))
+ * gate and up share type and shape.  Replaces encodeGf4FusedFfn
+ * (Qw35MetalRuntime+FFN.m:13-35) / qw35_ffn_gate_up_swiglu_gf4_f32
+ * (qw35-server/src/metal/qw35_gf4.metal:62-96), for every supported codec. */
+int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weight *up, const float *x,
+                                const float *awq, float *dst, uint32_t n_batch, void *stream, char *err,
+                                uintptr_t err_len);
+
+/* fp32 dequantisation (bit-exact statement of each format).  row_ids == NULL:
+ * all rows, dst fp32 [rows][k]; otherwise dst[i] = row row_ids[i] (device
+ * uint32 [n_rows]; an id >= rows gives a row of zeros), which is the
+ * embedding gather of qw35_get_row(s)_{q8_0,q4_k}_f32
+ * (qw35-server/src/metal/qw35_matvec.metal:100-169). */
+int qw35_hip_dequantize(const qw35_hip_weight *w, const uint32_t *row_ids, uint32_t n_rows, float *dst,
+                        void *stream, char *err, uintptr_t err_len);
+
+/* Wait for the stream and report any asynchronous device error.  Replaces
+ * qw35_metal_runtime_sync (Qw35FFI.h:71-72). */
+int qw35_hip_sync(void *stream, char *err, uintptr_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QW35_HIP_H */

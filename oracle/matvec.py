@@ -1,0 +1,120 @@
+"""fp64 matvec / matmul oracle on dequantised weights.  Test infrastructure only.
+
+The quantity every kernel is checked against is the fp64 product of the
+oracle-dequantised weights with the activations the kernel was given:
+
+* decode GEMV (``qw35_gf4.metal:99-136``, ``qw35_matvec.metal:171-261,630-654``):
+  ``y[b, r] = sum_k W[r, k] * (a[k] * x[b, k])`` (``a`` = 1 when no AWQ vector),
+  ``y += ...`` for the residual variants (``qw35_gf4.metal:209-246``);
+* fused gate/up/SwiGLU (``qw35_gf4.metal:62-96``):
+  ``silu(gate . x) * (up . x)`` with ``silu(v) = v / (1 + exp(-v))``
+  (``qw35_types.metal:40-42``);
+* prefill dequant-matmul (``qw35_tiled_mm.metal:36-198``; output layout
+  ``dst[token * rows + row]`` at ``:157-165``): the kernel consumes
+  ``A' = bf16_rne(a * A)`` (fp32 product, one rounding) and returns
+  ``bf16_rne(sum_k A'[m, k] * W[n, k])``; the oracle accumulates the same bf16
+  operands in fp64.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import gf4, q4_k, q8_0
+
+TYPE_GF4 = gf4.GF4_TYPE_ID
+TYPE_Q8_0 = q8_0.Q8_0_TYPE_ID
+TYPE_Q4_K = q4_k.Q4_K_TYPE_ID
+
+
+def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
+    """Byte size of a rows x k tensor (``qw35-server/src/loader/tensors.rs:123-172``)."""
+    if type_id == TYPE_GF4:
+        return gf4.gf4_nbytes(rows, k)
+    if type_id == TYPE_Q8_0:
+        return q8_0.q8_0_nbytes(rows, k)
+    if type_id == TYPE_Q4_K:
+        return q4_k.q4_k_nbytes(rows, k)
+    raise ValueError(f"unsupported type id {type_id}")
+
+
+def quantize(type_id: int, w: np.ndarray) -> np.ndarray:
+    """fp32 [R, K] -> raw tensor bytes as uint8 [R, row_bytes]."""
+    if type_id == TYPE_GF4:
+        return gf4.gf4_pack(w).view(np.uint8).reshape(w.shape[0], -1)
+    if type_id == TYPE_Q8_0:
+        return q8_0.q8_0_quantize(w)
+    if type_id == TYPE_Q4_K:
+        return q4_k.q4_k_quantize(w)
+    raise ValueError(f"unsupported type id {type_id}")
+
+
+def dequant(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """Raw tensor bytes (any shape, rows*row_bytes total) -> fp32 [rows, k]."""
+    raw = np.ascontiguousarray(raw).view(np.uint8).reshape(rows, -1)
+    if type_id == TYPE_GF4:
+        return gf4.gf4_dequant(raw.view("<u4"))
+    if type_id == TYPE_Q8_0:
+        return q8_0.q8_0_dequant(raw)
+    if type_id == TYPE_Q4_K:
+        return q4_k.q4_k_dequant(raw)
+    raise ValueError(f"unsupported type id {type_id}")
+
+
+def matvec_f64(w: np.ndarray, x: np.ndarray, awq: np.ndarray | None = None) -> np.ndarray:
+    """fp64 ``y[b] = W @ (a * x[b])`` for x of shape [K] or [B, K]."""
+    w64 = np.asarray(w, dtype=np.float64)
+    x64 = np.atleast_2d(np.asarray(x, dtype=np.float64))
+    if awq is not None:
+        x64 = x64 * np.asarray(awq, dtype=np.float64)[None, :]
+    y = x64 @ w64.T
+    return y if np.ndim(x) == 2 else y[0]
+
+
+def silu_f64(v: np.ndarray) -> np.ndarray:
+    v = np.asarray(v, dtype=np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+def swiglu_f64(w_gate, w_up, x, awq=None):
+    return silu_f64(matvec_f64(w_gate, x, awq)) * matvec_f64(w_up, x, awq)
+
+
+def rel_l2(got: np.ndarray, want: np.ndarray) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    den = np.linalg.norm(want)
+    return float(np.linalg.norm(got - want) / (den if den > 0 else 1.0))
+
+
+# -- bf16 helpers -----------------------------------------------------------
+
+def f32_to_bf16_bits(v: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round-to-nearest-even (NaN kept quiet)."""
+    bits = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32)
+    lsb = (bits >> np.uint32(16)) & np.uint32(1)
+    rounded = (bits + np.uint32(0x7FFF) + lsb) >> np.uint32(16)
+    nan = np.isnan(np.asarray(v, dtype=np.float32))
+    rounded = np.where(nan, (bits >> np.uint32(16)) | np.uint32(0x40), rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def bf16_round(v: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(v))
+
+
+def prefill_operand(a_bits: np.ndarray, awq: np.ndarray | None) -> np.ndarray:
+    """The activation tile the prefill kernel contracts: ``bf16_rne(fp32(A) * a)`` as fp32."""
+    a32 = bf16_bits_to_f32(a_bits)
+    if awq is None:
+        return a32
+    return bf16_round(a32 * np.asarray(awq, dtype=np.float32)[None, :])
+
+
+def prefill_f64(w: np.ndarray, a_bits: np.ndarray, awq: np.ndarray | None = None) -> np.ndarray:
+    """fp64 C[M, rows] = A' @ W^T on the exact bf16 operands the kernel consumes."""
+    a_eff = prefill_operand(a_bits, awq).astype(np.float64)
+    return a_eff @ np.asarray(w, dtype=np.float64).T

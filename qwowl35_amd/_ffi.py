@@ -1,0 +1,105 @@
+"""ctypes binding of ``include/qw35_hip.h`` (the library's C ABI).
+
+The prototypes here are the ones a Rust/C host binds; tests and the benchmark
+call the library only through them.  Loading fails loudly when the built
+library is missing: there is no CPU fallback anywhere in the package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libqw35_hip.so"
+
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_GF4 = 100
+MAX_BATCH = 8
+
+
+class TensorDesc(C.Structure):
+    """``qw35_hip_tensor_desc`` == ``qw35_metal_tensor_desc`` (Qw35MetalTypes.h:18-27)."""
+
+    _fields_ = [
+        ("name", C.c_void_p),
+        ("name_len", C.c_size_t),
+        ("dims", C.c_uint64 * 4),
+        ("n_dims", C.c_uint32),
+        ("type_id", C.c_uint32),
+        ("abs_offset", C.c_uint64),
+        ("bytes", C.c_uint64),
+        ("elements", C.c_uint64),
+    ]
+
+
+class Weight(C.Structure):
+    """``qw35_hip_weight``."""
+
+    _fields_ = [
+        ("data", C.c_void_p),
+        ("k", C.c_uint64),
+        ("rows", C.c_uint64),
+        ("bytes", C.c_uint64),
+        ("type_id", C.c_uint32),
+        ("reserved", C.c_uint32),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/qw35_hip.h.
+PROTOTYPES: dict[str, tuple] = {
+    "qw35_hip_has_device": (C.c_int, []),
+    "qw35_hip_weight_view": (C.c_int, [C.POINTER(TensorDesc), C.c_void_p, C.POINTER(Weight), C.c_char_p, C.c_size_t]),
+    "qw35_hip_decode_matvec": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_void_p, C.c_char_p,
+         C.c_size_t],
+    ),
+    "qw35_hip_ffn_gate_up_swiglu": (
+        C.c_int,
+        [C.POINTER(Weight), C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
+         C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_dequantize": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_sync": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+class Qw35Error(RuntimeError):
+    """A C-ABI call returned 0; the message is the library's err buffer."""
+
+
+def load(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Load ``libqw35_hip.so`` and bind every prototype (raises if missing)."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise Qw35Error(
+            f"{p} is not built; run `python -m qwowl35_amd.build` (the HIP library is required, "
+            "there is no fallback)"
+        )
+    lib = C.CDLL(str(p))
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def call(name: str, *args) -> int:
+    """Call ``name(*args, err, err_len)`` and raise ``Qw35Error`` on a 0 return."""
+    lib = load()
+    err = C.create_string_buffer(512)
+    rc = getattr(lib, name)(*args, err, C.sizeof(err))
+    if rc == 0:
+        raise Qw35Error(f"{name}: {err.value.decode(errors='replace')}")
+    return rc

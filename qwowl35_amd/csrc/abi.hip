@@ -1,0 +1,242 @@
+// extern "C" entry points of include/qw35_hip.h: argument validation, the
+// type-id -> kernel dispatch of encodeDecodeMatvecTensor
+// (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:184-256) and the
+// 0 + err[err_len] error convention of Qw35FFI.m:15-22.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/qw35_hip.h"
+#include "qw35_kernels.h"
+
+namespace {
+
+void set_err(char* err, uintptr_t err_len, const char* fmt, ...) {
+    if (!err || err_len == 0) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, (size_t)err_len, fmt, ap);
+    va_end(ap);
+}
+
+bool type_supported(uint32_t t) {
+    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K;
+}
+
+uint64_t row_bytes(uint32_t t, uint64_t k) {
+    switch (t) {
+        case qw35::kTypeGF4: return (k + 7) / 8 * 4;
+        case qw35::kTypeQ8_0: return (k + 31) / 32 * 34;
+        case qw35::kTypeQ4_K: return (k + 255) / 256 * 144;
+        default: return 0;
+    }
+}
+
+const char* type_name(uint32_t t) {
+    switch (t) {
+        case qw35::kTypeGF4: return "gf4";
+        case qw35::kTypeQ8_0: return "q8_0";
+        case qw35::kTypeQ4_K: return "q4_k";
+        default: return "unsupported";
+    }
+}
+
+constexpr uint64_t kMaxK = 12288;
+
+bool check_weight(const qw35_hip_weight* w, const char* what, char* err, uintptr_t err_len) {
+    if (!w) {
+        set_err(err, err_len, "%s: null weight", what);
+        return false;
+    }
+    if (!type_supported(w->type_id)) {
+        set_err(err, err_len, "%s: unsupported tensor type %u", what, w->type_id);
+        return false;
+    }
+    if (!w->data) {
+        set_err(err, err_len, "%s: null weight data", what);
+        return false;
+    }
+    if (((uintptr_t)w->data & 15u) != 0) {
+        set_err(err, err_len, "%s: weight data must be 16-byte aligned", what);
+        return false;
+    }
+    if (w->k == 0 || w->k % 256 != 0 || w->k > kMaxK) {
+        set_err(err, err_len, "%s: k=%llu must be a positive multiple of 256 and <= %llu", what,
+                (unsigned long long)w->k, (unsigned long long)kMaxK);
+        return false;
+    }
+    if (w->rows == 0 || w->rows > 0x7fffffffull) {
+        set_err(err, err_len, "%s: rows=%llu out of range", what, (unsigned long long)w->rows);
+        return false;
+    }
+    const uint64_t want = row_bytes(w->type_id, w->k) * w->rows;
+    if (w->bytes != want) {
+        set_err(err, err_len, "%s: %s tensor %llux%llu must be %llu bytes, got %llu", what, type_name(w->type_id),
+                (unsigned long long)w->rows, (unsigned long long)w->k, (unsigned long long)want,
+                (unsigned long long)w->bytes);
+        return false;
+    }
+    return true;
+}
+
+bool check_hip(hipError_t e, const char* what, char* err, uintptr_t err_len) {
+    if (e == hipSuccess) return true;
+    set_err(err, err_len, "%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+hipError_t dispatch_gemv(uint32_t type_id, const qw35::GemvArgs& a, hipStream_t s) {
+    switch (type_id) {
+        case qw35::kTypeGF4: return qw35::launch_gf4_gemv(a, s);
+        case qw35::kTypeQ8_0: return qw35::launch_q8_0_gemv(a, s);
+        default: return qw35::launch_q4_k_gemv(a, s);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qw35_hip_has_device(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n > 0 ? 1 : 0;
+}
+
+int qw35_hip_weight_view(const qw35_hip_tensor_desc* desc, const void* device_base, qw35_hip_weight* out, char* err,
+                         uintptr_t err_len) {
+    if (!desc || !out) {
+        set_err(err, err_len, "weight_view: null descriptor or output");
+        return 0;
+    }
+    if (!device_base) {
+        set_err(err, err_len, "weight_view: null device base");
+        return 0;
+    }
+    if (desc->n_dims < 2) {
+        set_err(err, err_len, "weight_view: tensor is not a matrix (n_dims=%u)", desc->n_dims);
+        return 0;
+    }
+    for (uint32_t i = 2; i < desc->n_dims && i < 4; ++i) {
+        if (desc->dims[i] != 1) {
+            set_err(err, err_len, "weight_view: dims[%u]=%llu, only 2-D weights are supported", i,
+                    (unsigned long long)desc->dims[i]);
+            return 0;
+        }
+    }
+    if (desc->elements != desc->dims[0] * desc->dims[1]) {
+        set_err(err, err_len, "weight_view: elements=%llu != dims[0]*dims[1]", (unsigned long long)desc->elements);
+        return 0;
+    }
+    qw35_hip_weight w;
+    w.data = static_cast<const uint8_t*>(device_base) + desc->abs_offset;
+    w.k = desc->dims[0];
+    w.rows = desc->dims[1];
+    w.bytes = desc->bytes;
+    w.type_id = desc->type_id;
+    w.reserved = 0;
+    if (!check_weight(&w, "weight_view", err, err_len)) return 0;
+    *out = w;
+    return 1;
+}
+
+int qw35_hip_decode_matvec(const qw35_hip_weight* w, const float* x, const float* awq, float* dst,
+                           uint32_t n_batch, int residual, void* stream, char* err, uintptr_t err_len) {
+    if (!check_weight(w, "decode_matvec", err, err_len)) return 0;
+    if (!x || !dst) {
+        set_err(err, err_len, "decode_matvec: null input or output");
+        return 0;
+    }
+    if (((uintptr_t)x & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)dst & 3u)) {
+        set_err(err, err_len, "decode_matvec: x/awq must be 16-byte aligned and dst 4-byte aligned");
+        return 0;
+    }
+    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
+        set_err(err, err_len, "decode_matvec: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);
+        return 0;
+    }
+    qw35::GemvArgs a{};
+    a.w = w->data;
+    a.x = x;
+    a.awq = awq;
+    a.y = dst;
+    a.w_up = nullptr;
+    a.rows = (int)w->rows;
+    a.k = (int)w->k;
+    a.n_batch = (int)n_batch;
+    a.residual = residual ? 1 : 0;
+    return check_hip(dispatch_gemv(w->type_id, a, static_cast<hipStream_t>(stream)), "decode_matvec", err, err_len)
+               ? 1
+               : 0;
+}
+
+int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight* gate, const qw35_hip_weight* up, const float* x,
+                                const float* awq, float* dst, uint32_t n_batch, void* stream, char* err,
+                                uintptr_t err_len) {
+    if (!check_weight(gate, "ffn_gate_up_swiglu(gate)", err, err_len)) return 0;
+    if (!check_weight(up, "ffn_gate_up_swiglu(up)", err, err_len)) return 0;
+    if (gate->type_id != up->type_id || gate->k != up->k || gate->rows != up->rows) {
+        set_err(err, err_len, "ffn_gate_up_swiglu: gate and up must share type and shape");
+        return 0;
+    }
+    if (!x || !dst) {
+        set_err(err, err_len, "ffn_gate_up_swiglu: null input or output");
+        return 0;
+    }
+    if (((uintptr_t)x & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)dst & 3u)) {
+        set_err(err, err_len, "ffn_gate_up_swiglu: x/awq must be 16-byte aligned and dst 4-byte aligned");
+        return 0;
+    }
+    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
+        set_err(err, err_len, "ffn_gate_up_swiglu: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);
+        return 0;
+    }
+    qw35::GemvArgs a{};
+    a.w = gate->data;
+    a.w_up = up->data;
+    a.x = x;
+    a.awq = awq;
+    a.y = dst;
+    a.rows = (int)gate->rows;
+    a.k = (int)gate->k;
+    a.n_batch = (int)n_batch;
+    a.residual = 0;
+    return check_hip(dispatch_gemv(gate->type_id, a, static_cast<hipStream_t>(stream)), "ffn_gate_up_swiglu", err,
+                     err_len)
+               ? 1
+               : 0;
+}
+
+int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint32_t n_rows, float* dst, void* stream,
+                        char* err, uintptr_t err_len) {
+    if (!check_weight(w, "dequantize", err, err_len)) return 0;
+    if (!dst) {
+        set_err(err, err_len, "dequantize: null output");
+        return 0;
+    }
+    if ((uintptr_t)dst & 15u) {
+        set_err(err, err_len, "dequantize: dst must be 16-byte aligned");
+        return 0;
+    }
+    const int out_rows = row_ids ? (int)n_rows : (int)w->rows;
+    if (row_ids && n_rows > 0x7fffffffu) {
+        set_err(err, err_len, "dequantize: n_rows out of range");
+        return 0;
+    }
+    return check_hip(qw35::launch_dequant(w->type_id, w->data, (int)w->rows, (int)w->k, row_ids, out_rows, dst,
+                                          static_cast<hipStream_t>(stream)),
+                     "dequantize", err, err_len)
+               ? 1
+               : 0;
+}
+
+int qw35_hip_sync(void* stream, char* err, uintptr_t err_len) {
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipGetLastError();
+    return check_hip(e, "sync", err, err_len) ? 1 : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,94 @@
+// fp32 dequantisation of GF4 / q8_0 / Q4_K tensors, optionally gathering rows.
+//
+// This is the library's bit-exact statement of each format (every weight of
+// all three codecs is exact in fp32, so results are compared bit-for-bit with
+// the CPU oracle).  With a row list it is the embedding row gather of
+// qw35_get_row(s)_{q8_0,q4_k}_f32 (qw35-server/src/metal/qw35_matvec.metal:100-169).
+//
+//   GF4  (tools/qw35_cook_common.py:79):  w = (4 - (c ^ 4)) * 0.25 * s, s = fp16(b << 8)
+//   q8_0 (qw35_types.metal:24-36):        w = fp32(d) * qs[i]
+//   Q4_K (qw35_matvec.metal:2-12):        w = d * sc_j * q - dmin * m_j
+#include "qw35_device.h"
+#include "qw35_kernels.h"
+
+namespace qw35 {
+namespace {
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// One thread per output group of 8 columns.
+// A gathered row id >= rows yields a row of zeros (no out-of-bounds read).
+__global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const uint8_t* __restrict__ w, int rows,
+                                                      int k, const uint32_t* __restrict__ row_ids, int n_out_rows,
+                                                      float* __restrict__ dst) {
+    const int groups = k >> 3;
+    const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (size_t)n_out_rows * groups) return;
+    const int out_row = (int)(gid / groups);
+    const int g = (int)(gid % groups);
+    const size_t src_row = row_ids ? (size_t)row_ids[out_row] : (size_t)out_row;
+    float v[8];
+    if (src_row >= (size_t)rows) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    } else if (type_id == kTypeGF4) {
+        const uint32_t word = reinterpret_cast<const uint32_t*>(w)[src_row * groups + g];
+        const float s = f16_to_f32((word & 0xFFu) << 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = ((word >> (8 + 3 * i)) & 7u) ^ 4u;
+            v[i] = (4.0f - (float)q) * 0.25f * s;
+        }
+    } else if (type_id == kTypeQ8_0) {
+        const uint8_t* row = w + src_row * (size_t)(k >> 5) * 34;
+        const int col = 8 * g;
+        const uint8_t* blk = row + (size_t)(col >> 5) * 34;
+        const float d = f16_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = d * (float)(int8_t)blk[2 + (col & 31) + i];
+    } else {  // Q4_K
+        const uint8_t* row = w + src_row * (size_t)(k >> 8) * 144;
+        const int col = 8 * g;
+        const uint8_t* blk = row + (size_t)(col >> 8) * 144;
+        const int e = col & 255;
+        const int j = e >> 5;
+        const uint8_t* sc = blk + 4;
+        uint32_t s6, m6;
+        if (j < 4) {
+            s6 = sc[j] & 63;
+            m6 = sc[j + 4] & 63;
+        } else {
+            s6 = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4);
+            m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+        }
+        const float d = f16_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const float dmin = f16_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+        const float dsc = d * (float)s6;
+        const float mm = dmin * (float)m6;
+        const uint8_t* qs = blk + 16 + (j >> 1) * 32 + (e & 31);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 0x0F);
+            v[i] = dsc * (float)q - mm;
+        }
+    }
+    float* o = dst + (size_t)out_row * k + 8 * g;
+    *reinterpret_cast<float4_t*>(o) = float4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<float4_t*>(o + 4) = float4_t{v[4], v[5], v[6], v[7]};
+}
+
+}  // namespace
+
+hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, const uint32_t* row_ids,
+                          int n_out_rows, float* dst, hipStream_t stream) {
+    const size_t total = (size_t)n_out_rows * (size_t)(k >> 3);
+    if (total == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(dequant_kernel, dim3(grid), dim3(256), 0, stream, type_id, static_cast<const uint8_t*>(w), rows, k,
+                       row_ids, n_out_rows, dst);
+    return hipGetLastError();
+}
+
+}  // namespace qw35

@@ -1,0 +1,457 @@
+// GF4 decode GEMV / fused gate-up-SwiGLU for gfx950, batch 1..8, on MFMA.
+//
+//   y[b][r] (+)= sum_k W[r][k] * a[k] * x[b][k]
+//
+// Weight format (GGUF type 100): one uint32 per 8 columns, bits 0..7 an e5m2
+// scale byte, bits 8+3i..10+3i the code c_i = q_i ^ 4 of column 8g+i; the
+// weight is (4 - q_i) * s / 4 (tools/qw35_cook_common.py:67-80,115-119).
+// Reference kernels replaced: qw35_decode_matmul_gf4_2row{,_residual}_f32 and
+// qw35_ffn_gate_up_swiglu_gf4_f32 (qw35-server/src/metal/qw35_gf4.metal:62-136,209-246).
+//
+// Mapping onto v_mfma_f32_16x16x32_f16 (D[16x16] += A[16x32] * B[32x16]):
+//   * B = weights: lane l holds 8 consecutive k of weight row n = l % 16, i.e.
+//     exactly one GF4 word, decoded in registers to exact fp16 values;
+//   * A = activations: row m = 2b holds fp16(x_b) ("hi"), row 2b+1 holds
+//     fp16(x_b - hi) ("lo"), so batch 1..8 fill the 16 A rows and the fp16
+//     split keeps ~22 bits of each fp32 activation;
+//   * D: lane l holds D[4*(l/16)+j][l%16]; y[b][n] = D[2b][n] + D[2b+1][n].
+//
+// Word -> 8 exact fp16 weights, 17 VALU ops:
+//   t  = w ^ 0x92492400                  (q_i = c_i ^ 4 for the eight codes)
+//   t1 = t >> 4, t2 = t >> 10
+//   P0 = (t1 & 0x00070070) | 0x64005400  fp16 pair (64 + q0, 1024 + q4)
+//   P1 = (t1 & 0x00380380) | 0x58004800  fp16 pair ( 8 + q1,  128 + q5)
+//   P2 = (t2 & 0x00070070) | 0x64005400  fp16 pair (64 + q2, 1024 + q6)
+//   P3 = (t2 & 0x00380380) | 0x58004800  fp16 pair ( 8 + q3,  128 + q7)
+//   E_j = P_j - (base + 4)               exact small integers q - 4
+//   B_j = E_j * (-s/4)                   exact: |q-4| <= 4 and s has 3 significant bits
+// The pairs hold columns (0,4) (1,5) (2,6) (3,7); A is stored in LDS in the
+// same order, which the MFMA's sum over k does not see.
+//
+// Activations are staged once per workgroup in LDS, scaled per batch row by a
+// power of two that puts max|a*x| in [2^13, 2^14) (no fp16 overflow for any
+// input magnitude); the factor is divided out exactly at the end.
+//
+// Launch: one workgroup per 16-row tile, KS waves splitting K, each wave
+// covering CPW chunks of 256 columns (two 16-byte loads per lane per chunk).
+// Every x load is issued before the weight loads, so waiting for x never waits
+// on the weight stream (vector loads complete in order); the weights are then
+// consumed in issue order as they arrive.
+#include "qw35_device.h"
+#include "qw35_kernels.h"
+
+#include <type_traits>
+
+namespace qw35 {
+namespace {
+
+constexpr uint32_t kFlip = 0x92492400u;
+constexpr uint32_t kMaskA = 0x00070070u;
+constexpr uint32_t kMaskB = 0x00380380u;
+constexpr uint32_t kMagicA = 0x64005400u;
+constexpr uint32_t kMagicB = 0x58004800u;
+
+__device__ __forceinline__ half2_t h2(float lo, float hi) {
+    half2_t r;
+    r.x = (_Float16)lo;
+    r.y = (_Float16)hi;
+    return r;
+}
+
+// Loop-invariant operands of the decode, held in VGPRs so that the VOP3 forms
+// (v_bitop3_b32, v_pk_fma_f16) take them without literals.
+struct Gf4Consts {
+    uint32_t mask_a, mask_b, magic_a, magic_b;
+    half2_t quarter_neg, off_a, off_b;
+};
+
+// (t & mask) ^ magic' = ((t ^ flip) & mask) | magic: the code flip q = c ^ 4
+// (bit 2 of every field) is folded into the magic constants.
+constexpr uint32_t kMagicFlipA = kMagicA ^ ((kFlip >> 4) & kMaskA);  // == ((kFlip >> 10) & kMaskA) ^ kMagicA
+constexpr uint32_t kMagicFlipB = kMagicB ^ ((kFlip >> 4) & kMaskB);
+static_assert(((kFlip >> 4) & kMaskA) == ((kFlip >> 10) & kMaskA), "flip bits agree for both shifts");
+static_assert(((kFlip >> 4) & kMaskB) == ((kFlip >> 10) & kMaskB), "flip bits agree for both shifts");
+
+__device__ __forceinline__ Gf4Consts gf4_consts() {
+    Gf4Consts c;
+    c.mask_a = kMaskA;
+    c.mask_b = kMaskB;
+    c.magic_a = kMagicFlipA;
+    c.magic_b = kMagicFlipB;
+    c.quarter_neg = h2(-0.25f, -0.25f);
+    c.off_a = h2(68.0f / 4.0f, 1028.0f / 4.0f);
+    c.off_b = h2(12.0f / 4.0f, 132.0f / 4.0f);
+    return c;
+}
+
+// v_bitop3_b32 with truth table 0x6a: (a & b) ^ c.
+__device__ __forceinline__ uint32_t and_xor(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+    return r;
+}
+
+// One GF4 word -> MFMA B operand: 8 exact fp16 weights in column order
+// 0,4,1,5,2,6,3,7 (15 VALU ops).
+//   E_j = P_j * (-1/4) + (base + 4)/4 = (4 - q)/4   (exact)
+//   B_j = E_j * s                                   (exact, |B| <= |s|)
+__device__ __forceinline__ half8_t gf4_word_to_b(uint32_t w, const Gf4Consts& c) {
+    const uint32_t t1 = w >> 4;
+    const uint32_t t2 = w >> 10;
+    const half2_t p0 = as_half2(and_xor(t1, c.mask_a, c.magic_a));
+    const half2_t p1 = as_half2(and_xor(t1, c.mask_b, c.magic_b));
+    const half2_t p2 = as_half2(and_xor(t2, c.mask_a, c.magic_a));
+    const half2_t p3 = as_half2(and_xor(t2, c.mask_b, c.magic_b));
+    const half2_t e0 = __builtin_elementwise_fma(p0, c.quarter_neg, c.off_a);
+    const half2_t e1 = __builtin_elementwise_fma(p1, c.quarter_neg, c.off_b);
+    const half2_t e2 = __builtin_elementwise_fma(p2, c.quarter_neg, c.off_a);
+    const half2_t e3 = __builtin_elementwise_fma(p3, c.quarter_neg, c.off_b);
+    // (b << 24) | (b << 8): the e5m2 byte as the high byte of both halves = (s, s).
+    const half2_t s2 = as_half2(__builtin_amdgcn_perm(w, w, 0x000C000Cu));
+    const uint4_t u = {as_u32(e0 * s2), as_u32(e1 * s2), as_u32(e2 * s2), as_u32(e3 * s2)};
+    return __builtin_bit_cast(half8_t, u);
+}
+
+// s_waitcnt encoding (gfx9): wait until at most `n` vector-memory operations
+// of this wave are outstanding; expcnt and lgkmcnt are left unconstrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Per-wave LDS block:
+//   xpose    2 x 2 KB transpose buffers (16 rows x 128 bytes = one 256-column
+//            chunk of a 16-row tile).  Global loads read full 128-byte lines
+//            (lane l of instruction h: row 8h + l/8, 16-byte segment l%8); each
+//            lane stores its segment s of row r at r*128 + 16*(s ^ ((r>>1)&7)),
+//            and the MFMA-layout reads (row n, segments 2kq and 2kq+1) then hit
+//            16 distinct bank groups per 16 lanes.
+//   acts     2*NB rows (hi, lo of each batch row) x (CPW*256 + 8) halves, each
+//            group of 8 columns stored as x0 x4 x1 x5 x2 x6 x3 x7.
+//   zeros    64 halves (the A operand of rows past the batch).
+// After the KS blocks: the per-wave partial outputs.
+template <int NB, int CPW>
+struct WaveLds {
+    static constexpr int kXposeBytes = 2 * 2048;
+    static constexpr int kStride = CPW * 256 + 8;  // halves per activation row
+    static constexpr int kActBytes = 2 * NB * kStride * 2;
+    static constexpr int kBytes = kXposeBytes + kActBytes + 128;
+};
+
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+// Workgroup = KS waves covering 16*RT rows x all k.  Wave w owns the K-slice
+// [w*CPW*256, (w+1)*CPW*256) of all RT row tiles; its weight loads are issued
+// up front in the order (chunk, tile, matrix, half) and consumed in that order.
+template <int NB, int RT, int KS, int CPW, bool SWIGLU, bool HAS_AWQ>
+__global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int NM = SWIGLU ? 2 : 1;
+    using L = WaveLds<NB, CPW>;
+    constexpr int STRIDE = L::kStride;
+    constexpr int GPL = (CPW * 32 + 63) / 64;  // activation groups per lane per batch row
+    constexpr int NTC = CPW * RT * NM;         // tile-chunks per wave
+    constexpr int NLOADS = 2 * NTC;
+    static_assert(NLOADS <= 48, "vmcnt budget");
+    const int k = args.k;
+    const int rows = args.rows;
+    const int n_batch = args.n_batch;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 15;
+    const int kq = lane >> 4;
+    const int row0 = blockIdx.x * 16 * RT;
+    const int words_per_row = k >> 3;
+    const int col0 = wave * CPW * 256;
+    const int slice_groups = min(CPW * 32, max(0, (k - col0) >> 3));
+
+    uint8_t* wblk = smem + (size_t)wave * L::kBytes;
+    _Float16* xs = reinterpret_cast<_Float16*>(wblk + L::kXposeBytes);
+    _Float16* zrow = xs + 2 * NB * STRIDE;
+    float* part = reinterpret_cast<float*>(smem + (size_t)KS * L::kBytes);  // [KS][RT][NM][NB][16]
+    if (lane < 32) reinterpret_cast<uint32_t*>(zrow)[lane] = 0u;
+
+    // 1. Activation slice (and AWQ) into registers, clamped, unused until step 3.
+    float4_t xv[NB][GPL][2];
+    float4_t av[GPL][2];
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+        int g = lane + 64 * j;
+        g = g < slice_groups ? g : 0;
+        const int col = col0 + 8 * g;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int bb = b < n_batch ? b : 0;
+            const float* src = args.x + (size_t)bb * k + col;
+            xv[b][j][0] = *reinterpret_cast<const float4_t*>(src);
+            xv[b][j][1] = *reinterpret_cast<const float4_t*>(src + 4);
+        }
+        if (HAS_AWQ) {
+            av[j][0] = *reinterpret_cast<const float4_t*>(args.awq + col);
+            av[j][1] = *reinterpret_cast<const float4_t*>(args.awq + col + 4);
+        }
+    }
+
+    // Keep the scheduler from sinking the activation loads below the weight
+    // loads: vector loads complete in order, so waiting for x must not wait
+    // for the weight stream.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. Weight loads, full 128-byte lines per 8 lanes.  Rows past the end are
+    //    clamped (computed on a duplicate row, never stored).
+    uint4_t wv[NTC][2];
+    const int lrow = lane >> 3;  // row within the half tile
+    const int lseg = lane & 7;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        int chunk = wave * CPW + c;
+        chunk = chunk * 256 < k ? chunk : 0;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const uint32_t* wbase = static_cast<const uint32_t*>(m == 0 ? args.w : args.w_up);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    int r = row0 + 16 * t + 8 * h + lrow;
+                    r = r < rows ? r : rows - 1;
+                    wv[(c * RT + t) * NM + m][h] =
+                        load_stream16(wbase + (size_t)r * words_per_row + chunk * 32 + 4 * lseg);
+                }
+            }
+        }
+    }
+
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. Wave-private fp16 hi/lo activations with a per-wave power-of-two scale.
+    wait_vmcnt<NLOADS>();
+    float inv_scale[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GPL; ++j) {
+            if (HAS_AWQ) {
+                xv[b][j][0] *= av[j][0];
+                xv[b][j][1] *= av[j][1];
+            }
+            if (lane + 64 * j < slice_groups) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fmaxf(fabsf(xv[b][j][0][e]), fabsf(xv[b][j][1][e])));
+            }
+        }
+        const float sc = fp16_range_scale(wave_max_abs(mx));
+        inv_scale[b] = 1.0f / sc;
+#pragma unroll
+        for (int j = 0; j < GPL; ++j) {
+            const int g = lane + 64 * j;
+            if (g < slice_groups) {
+                const float4_t v0 = xv[b][j][0] * sc;
+                const float4_t v1 = xv[b][j][1] * sc;
+                const float e[8] = {v0[0], v1[0], v0[1], v1[1], v0[2], v1[2], v0[3], v1[3]};
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const half2_t hh = h2(e[2 * q], e[2 * q + 1]);
+                    hi[q] = as_u32(hh);
+                    lo[q] = as_u32(h2(e[2 * q] - (float)hh.x, e[2 * q + 1] - (float)hh.y));
+                }
+                *reinterpret_cast<uint4_t*>(xs + (size_t)(2 * b) * STRIDE + 8 * g) = uint4_t{hi[0], hi[1], hi[2], hi[3]};
+                *reinterpret_cast<uint4_t*>(xs + (size_t)(2 * b + 1) * STRIDE + 8 * g) =
+                    uint4_t{lo[0], lo[1], lo[2], lo[3]};
+            }
+        }
+    }
+
+    // 4. Per tile-chunk: transpose through LDS, decode, MFMA.  All LDS data
+    //    here is private to the wave and LDS operations of one wave execute in
+    //    order, so no workgroup barrier is needed before the compute.
+    const int mrow = lane & 15;
+    const bool a_live = mrow < 2 * n_batch;
+    const _Float16* arow = xs + (size_t)mrow * STRIDE + 64 * kq;
+    const int swz_r = (n >> 1) & 7;
+    const int rd0 = n * 128 + 16 * ((2 * kq) ^ swz_r);
+    const int rd1 = n * 128 + 16 * ((2 * kq + 1) ^ swz_r);
+    const int wr0 = lrow * 128 + 16 * (lseg ^ ((lrow >> 1) & 7));              // h = 0: rows 0..7
+    const int wr1 = (8 + lrow) * 128 + 16 * (lseg ^ (((8 + lrow) >> 1) & 7));  // h = 1: rows 8..15
+    const Gf4Consts cst = gf4_consts();
+    float4_t acc[RT][NM];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[t][m] = float4_t{0.f, 0.f, 0.f, 0.f};
+    half8_t a[8];
+
+    static_for<NTC>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        constexpr int c = i / (RT * NM);
+        constexpr int t = (i / NM) % RT;
+        constexpr int m = i % NM;
+        if ((wave * CPW + c) * 256 < k) {
+            if constexpr (t == 0 && m == 0) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const _Float16* ap = a_live ? arow + c * 256 : zrow;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) a[q] = *reinterpret_cast<const half8_t*>(ap + 8 * q);
+            }
+            wait_vmcnt<NLOADS - 2 * (i + 1)>();
+            uint8_t* xb = wblk + (i & 1) * 2048;
+            *reinterpret_cast<uint4_t*>(xb + wr0) = wv[i][0];
+            *reinterpret_cast<uint4_t*>(xb + wr1) = wv[i][1];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint4_t w0 = *reinterpret_cast<const uint4_t*>(xb + rd0);
+            const uint4_t w1 = *reinterpret_cast<const uint4_t*>(xb + rd1);
+            const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], gf4_word_to_b(ww[q], cst), acc[t][m], 0, 0, 0);
+        }
+    });
+
+    // 5. y[b][n] = (D[2b][n] + D[2b+1][n]) / scale of this wave, summed over the
+    //    KS waves; lane group kq holds batches 2kq and 2kq+1.
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int b = 2 * kq + jj;
+                float isc = 1.0f;
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb)
+                    if (bb == b) isc = inv_scale[bb];
+                if (b < NB)
+                    part[(((wave * RT + t) * NM + m) * NB + b) * 16 + n] =
+                        (acc[t][m][2 * jj] + acc[t][m][2 * jj + 1]) * isc;
+            }
+        }
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < RT * NB * 16; o += 64 * KS) {
+        const int t = o / (NB * 16);
+        const int b = (o / 16) % NB;
+        const int nn = o & 15;
+        const int r = row0 + 16 * t + nn;
+        float tot[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < KS; ++w) sum += part[(((w * RT + t) * NM + m) * NB + b) * 16 + nn];
+            tot[m] = sum;
+        }
+        if (r < rows && b < n_batch) {
+            float* yp = args.y + (size_t)b * rows + r;
+            float v = SWIGLU ? silu(tot[0]) * tot[NM - 1] : tot[0];
+            if (args.residual) v += *yp;
+            *yp = v;
+        }
+    }
+}
+
+template <int NB, int RT, int KS, int CPW, bool SWIGLU>
+size_t lds_bytes() {
+    constexpr int NM = SWIGLU ? 2 : 1;
+    return (size_t)KS * WaveLds<NB, CPW>::kBytes + (size_t)KS * RT * NM * NB * 16 * 4;
+}
+
+template <int NB, int RT, int KS, int CPW, bool SWIGLU>
+hipError_t launch_cfg(const GemvArgs& a, hipStream_t stream) {
+    const size_t lds = lds_bytes<NB, RT, KS, CPW, SWIGLU>();
+    if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+    const int grid = (a.rows + 16 * RT - 1) / (16 * RT);
+    if (a.awq) {
+        hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds, stream, a);
+    } else {
+        hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, false>), dim3(grid), dim3(64 * KS), lds, stream, a);
+    }
+    return hipGetLastError();
+}
+
+// Launch plan for a shape: KS waves per workgroup, CPW 256-column chunks per
+// wave (KS*CPW*256 >= k), RT 16-row tiles per workgroup.  RT is raised for
+// tall matrices so that one workgroup per CU re-reads the activations once
+// for 48 rows instead of 16.
+struct Gf4Plan {
+    int rt, ks, cpw;
+};
+
+Gf4Plan plan_gf4(int nb, int rows, int k, bool swiglu) {
+    (void)nb;
+    (void)swiglu;
+    const int chunks = k / 256;
+    const int tiles = (rows + 15) / 16;
+    if (chunks <= 4) return {1, 4, 1};
+    if (chunks <= 8) return {1, 4, 2};
+    if (chunks <= 16) {
+        if (tiles >= 768) return {3, 8, 2};
+        if (tiles >= 512) return {2, 8, 2};
+        return {1, 8, 2};
+    }
+    if (chunks <= 32) return {1, 8, 4};
+    return {1, 8, 6};
+}
+
+size_t plan_lds(const Gf4Plan& p, int nb, bool swiglu) {
+    const int nm = swiglu ? 2 : 1;
+    const size_t per_wave = 4096 + (size_t)2 * nb * (p.cpw * 256 + 8) * 2 + 128;
+    return (size_t)p.ks * per_wave + (size_t)p.ks * p.rt * nm * nb * 16 * 4;
+}
+
+template <int NB, bool SWIGLU>
+hipError_t launch_nb(const GemvArgs& a, hipStream_t stream) {
+    const Gf4Plan p = plan_gf4(NB, a.rows, a.k, SWIGLU);
+#define QW35_GF4_PLAN(RT, KS, CPW) \
+    if (p.rt == RT && p.ks == KS && p.cpw == CPW) return launch_cfg<NB, RT, KS, CPW, SWIGLU>(a, stream);
+    QW35_GF4_PLAN(1, 4, 1)
+    QW35_GF4_PLAN(1, 4, 2)
+    QW35_GF4_PLAN(1, 8, 2)
+    QW35_GF4_PLAN(2, 8, 2)
+    QW35_GF4_PLAN(3, 8, 2)
+    if constexpr (NB <= 4) { QW35_GF4_PLAN(1, 8, 4) }
+    if constexpr (NB <= 2) { QW35_GF4_PLAN(1, 8, 6) }
+#undef QW35_GF4_PLAN
+    return hipErrorInvalidValue;
+}
+
+template <bool SWIGLU>
+hipError_t launch_gf4_any(const GemvArgs& a, hipStream_t stream) {
+    // Largest batch slice (8, 4, 2, 1 rows) whose plan fits the 160 KiB LDS.
+    int slice = 8;
+    while (slice > 1 && plan_lds(plan_gf4(slice, a.rows, a.k, SWIGLU), slice, SWIGLU) > 160 * 1024) slice >>= 1;
+    if (plan_lds(plan_gf4(1, a.rows, a.k, SWIGLU), 1, SWIGLU) > 160 * 1024) return hipErrorInvalidValue;
+    for (int b0 = 0; b0 < a.n_batch; b0 += slice) {
+        GemvArgs s = a;
+        s.n_batch = a.n_batch - b0 < slice ? a.n_batch - b0 : slice;
+        s.x = a.x + (size_t)b0 * a.k;
+        s.y = a.y + (size_t)b0 * a.rows;
+        hipError_t e;
+        if (s.n_batch == 1) e = launch_nb<1, SWIGLU>(s, stream);
+        else if (s.n_batch == 2) e = launch_nb<2, SWIGLU>(s, stream);
+        else if (s.n_batch <= 4) e = launch_nb<4, SWIGLU>(s, stream);
+        else e = launch_nb<8, SWIGLU>(s, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? launch_gf4_any<true>(a, stream) : launch_gf4_any<false>(a, stream);
+}
+
+}  // namespace qw35

@@ -1,0 +1,93 @@
+// Device-side helpers shared by the qw35 HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qw35 {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; the total is valid in lane 63.
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    v += dpp_f32<kDppQuadXor2>(v);
+    v += dpp_f32<kDppRowHalfMirror>(v);
+    v += dpp_f32<kDppRowMirror>(v);
+    v += dpp_f32<kDppRowBcast15, 0xA>(v);
+    v += dpp_f32<kDppRowBcast31, 0xC>(v);
+    return v;
+}
+
+// Sum over the 64 lanes, broadcast to every lane (through lane 63).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = wave_sum_to_lane63(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_max_abs(float v) {
+    v = fabsf(v);
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppRowMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppRowBcast15, 0xA>(v));
+    v = fmaxf(v, dpp_f32<kDppRowBcast31, 0xC>(v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+__device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// fp32 -> fp16 round-to-nearest-even, packed.
+__device__ __forceinline__ half2_t pack_half2(float lo, float hi) {
+    half2_t r;
+    r.x = (_Float16)lo;
+    r.y = (_Float16)hi;
+    return r;
+}
+
+// Streaming 16-byte load of weights that are read exactly once.
+__device__ __forceinline__ uint4_t load_stream16(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint4_t*>(p));
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+// Power-of-two factor 2^e that brings max_abs to at most 2^14, so that every
+// scaled activation fits fp16 (max 65504) with headroom; 1 for zero input.
+__device__ __forceinline__ float fp16_range_scale(float max_abs) {
+    if (!(max_abs > 0.0f) || !(max_abs < 3.0e38f)) return 1.0f;
+    int e;
+    (void)frexpf(max_abs, &e);  // max_abs in [2^(e-1), 2^e)
+    int shift = 14 - e;         // max_abs * 2^shift < 2^14
+    if (shift > 24) shift = 24;
+    if (shift < -24) shift = -24;
+    return ldexpf(1.0f, shift);
+}
+
+}  // namespace qw35

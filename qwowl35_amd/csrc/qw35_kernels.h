@@ -1,0 +1,44 @@
+// Host-side launch interface of the qw35 HIP kernels (internal to the library;
+// the public C ABI is include/qw35_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qw35 {
+
+// GGUF tensor type-ids handled by this library.
+constexpr uint32_t kTypeQ8_0 = 8;
+constexpr uint32_t kTypeQ4_K = 12;
+constexpr uint32_t kTypeGF4 = 100;
+
+// Largest decode batch of the GEMV kernels.
+constexpr int kMaxDecodeBatch = 8;
+
+struct GemvArgs {
+    const void* w;        // raw tensor bytes, row-major, rows x row_bytes
+    const float* x;       // [n_batch][k]
+    const float* awq;     // [k] or nullptr
+    float* y;             // [n_batch][rows]
+    const void* w_up;     // second matrix of the fused gate/up/SwiGLU kernel, else nullptr
+    int rows;
+    int k;
+    int n_batch;
+    int residual;         // y += result instead of y = result
+};
+
+// Each launcher validates nothing (the C ABI does) and returns the launch status.
+hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream);
+hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream);
+hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream);
+
+// Full or row-gathered fp32 dequantisation (row_ids == nullptr: all rows).
+hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, const uint32_t* row_ids,
+                          int n_out_rows, float* dst, hipStream_t stream);
+
+// GF4 prefill dequant-matmul on bf16 MFMA: C[m][n] = sum_k bf16(a_k * A[m][k]) * W[n][k].
+// out_f32 != 0 writes fp32, otherwise bf16 (RNE).
+hipError_t launch_gf4_prefill(const void* w, int rows, int k, const uint16_t* a_bf16, const float* awq,
+                              void* c, int m, int out_f32, hipStream_t stream);
+
+}  // namespace qw35

@@ -1,0 +1,149 @@
+"""Host-side mirror of the reference's per-op encoder API, over the C ABI.
+
+Names and argument meaning follow the reference runtime's encoders
+(qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m):
+
+* ``decode_matvec``       <- ``encodeDecodeMatvecTensor:weight:input:inputOffset:dst:residual:`` (:184-256)
+* ``ffn_gate_up_swiglu``  <- ``encodeGf4FusedFfn`` / ``qw35_ffn_gate_up_swiglu_gf4_f32`` (:13-35)
+* ``matvec_batch``        <- ``encodeMatvecBatch`` for 1..8 tokens (:260-306)
+* ``dequantize``          <- the per-codec dequant helpers / ``qw35_get_rows_*`` gathers
+
+Device memory and streams come from torch (plumbing only); every computation
+is a call into ``libqw35_hip.so``.  Errors raise ``Qw35Error`` with the
+library's message, the Python form of the reference's 0 + err-buffer return.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _ffi
+from ._ffi import Qw35Error, TYPE_GF4, TYPE_Q4_K, TYPE_Q8_0  # noqa: F401
+
+_ROW_BYTES = {
+    TYPE_GF4: lambda k: (k + 7) // 8 * 4,
+    TYPE_Q8_0: lambda k: (k + 31) // 32 * 34,
+    TYPE_Q4_K: lambda k: (k + 255) // 256 * 144,
+}
+
+
+def row_bytes(type_id: int, k: int) -> int:
+    try:
+        return _ROW_BYTES[type_id](k)
+    except KeyError:
+        raise Qw35Error(f"unsupported tensor type {type_id}") from None
+
+
+@dataclass
+class HipWeight:
+    """A weight tensor in HBM plus its C-ABI view (``qw35_hip_weight``)."""
+
+    storage: torch.Tensor  # uint8 device tensor holding the raw GGUF bytes
+    view: _ffi.Weight
+
+    @property
+    def type_id(self) -> int:
+        return int(self.view.type_id)
+
+    @property
+    def rows(self) -> int:
+        return int(self.view.rows)
+
+    @property
+    def k(self) -> int:
+        return int(self.view.k)
+
+    @classmethod
+    def upload(cls, raw, type_id: int, rows: int, k: int, device="cuda") -> "HipWeight":
+        """Copy raw tensor bytes (numpy / torch, any shape) into HBM and validate."""
+        t = torch.as_tensor(raw).reshape(-1).view(torch.uint8)
+        dev = torch.empty(t.numel(), dtype=torch.uint8, device=device)
+        dev.copy_(t)
+        return cls.from_device(dev, type_id, rows, k)
+
+    @classmethod
+    def from_device(cls, storage: torch.Tensor, type_id: int, rows: int, k: int, offset: int = 0,
+                    nbytes: int | None = None) -> "HipWeight":
+        """View ``nbytes`` at ``offset`` of a device byte buffer as a rows x k tensor
+        through ``qw35_hip_weight_view`` (the descriptor path a GGUF loader uses)."""
+        desc = _ffi.TensorDesc()
+        desc.name = None
+        desc.name_len = 0
+        desc.dims[0] = k
+        desc.dims[1] = rows
+        desc.dims[2] = 1
+        desc.dims[3] = 1
+        desc.n_dims = 2
+        desc.type_id = type_id
+        desc.abs_offset = offset
+        desc.bytes = nbytes if nbytes is not None else rows * row_bytes(type_id, k)
+        desc.elements = rows * k
+        w = _ffi.Weight()
+        _ffi.call("qw35_hip_weight_view", C.byref(desc), C.c_void_p(storage.data_ptr()), C.byref(w))
+        return cls(storage, w)
+
+
+def _ptr(t: torch.Tensor | None) -> C.c_void_p:
+    return C.c_void_p(t.data_ptr() if t is not None else None)
+
+
+def _stream(stream) -> C.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream)
+
+
+def _check_act(x: torch.Tensor, k: int, name: str) -> int:
+    if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous():
+        raise Qw35Error(f"{name} must be a contiguous fp32 device tensor")
+    if x.shape[-1] != k:
+        raise Qw35Error(f"{name} last dim {x.shape[-1]} != k={k}")
+    return 1 if x.dim() == 1 else int(x.shape[0])
+
+
+def decode_matvec(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, residual: bool = False,
+                  awq: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """``dst (+)= W @ (awq * x)`` for x [k] or [n_batch, k] (n_batch <= 8)."""
+    nb = _check_act(x, w.k, "x")
+    if dst is None:
+        dst = torch.zeros((nb, w.rows) if x.dim() == 2 else (w.rows,), dtype=torch.float32, device=x.device)
+    _ffi.call("qw35_hip_decode_matvec", C.byref(w.view), _ptr(x), _ptr(awq), _ptr(dst), nb, int(bool(residual)),
+              _stream(stream))
+    return dst
+
+
+def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None,
+                       awq: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """``dst = silu(gate @ (awq*x)) * (up @ (awq*x))``."""
+    nb = _check_act(x, gate.k, "x")
+    if dst is None:
+        dst = torch.empty((nb, gate.rows) if x.dim() == 2 else (gate.rows,), dtype=torch.float32, device=x.device)
+    _ffi.call("qw35_hip_ffn_gate_up_swiglu", C.byref(gate.view), C.byref(up.view), _ptr(x), _ptr(awq), _ptr(dst),
+              nb, _stream(stream))
+    return dst
+
+
+def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Multi-token matvec (``encodeMatvecBatch``) for 1..8 tokens of fp32 activations."""
+    if x.dim() != 2 or x.shape[0] > _ffi.MAX_BATCH:
+        raise Qw35Error("matvec_batch takes 1..8 tokens; use the prefill matmul for larger chunks")
+    return decode_matvec(w, x, dst, residual=False, stream=stream)
+
+
+def dequantize(w: HipWeight, row_ids: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """fp32 weights [rows, k], or the gathered rows ``row_ids`` (uint32/int32 device)."""
+    if row_ids is not None:
+        if row_ids.dtype not in (torch.int32,) or not row_ids.is_cuda:
+            raise Qw35Error("row_ids must be an int32 device tensor (read as uint32)")
+        n = int(row_ids.numel())
+    else:
+        n = w.rows
+    dst = torch.empty((n, w.k), dtype=torch.float32, device=w.storage.device)
+    _ffi.call("qw35_hip_dequantize", C.byref(w.view), _ptr(row_ids), n, _ptr(dst), _stream(stream))
+    return dst
+
+
+def sync(stream=None) -> None:
+    _ffi.call("qw35_hip_sync", _stream(stream))

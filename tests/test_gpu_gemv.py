@@ -1,0 +1,139 @@
+"""GPU parity of the decode GEMVs and the dequantiser, through the C ABI.
+
+Bars: dequantisation bit-exact against the oracle; GEMV outputs within
+GEMV_REL_L2 (1e-3) relative L2 of the fp64 matvec on the oracle-dequantised
+weights.  Shapes run from tiny/ragged cases to the Qwen3.5-9B projections.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import gf4 as ogf4
+from oracle import matvec as om
+from tests.helpers import GEMV_REL_L2, TYPES, activations, awq_scales, make_weight, random_gf4_words
+
+pytestmark = pytest.mark.gpu
+
+
+def _rt():
+    from qwowl35_amd import runtime
+
+    return runtime
+
+
+def _upload(raw, type_id, rows, k):
+    return _rt().HipWeight.upload(raw, type_id, rows, k)
+
+
+def _t(a, cuda):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    same = a.view(np.uint32) == b.view(np.uint32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(same | both_nan))
+
+
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("rows,k", [(3, 256), (64, 4096), (37, 12288)])
+def test_dequant_bit_exact(cuda, name, rows, k):
+    type_id = TYPES[name]
+    raw, deq = make_weight(type_id, rows, k, seed=rows * 7 + k)
+    w = _upload(raw, type_id, rows, k)
+    got = _rt().dequantize(w).cpu().numpy()
+    assert _bits_equal(got, deq)
+
+
+def test_dequant_gf4_arbitrary_words(cuda):
+    rng = np.random.default_rng(11)
+    words = random_gf4_words(rng, (256, 512))
+    w = _upload(words.view(np.uint8), om.TYPE_GF4, 256, 4096)
+    got = _rt().dequantize(w).cpu().numpy()
+    assert _bits_equal(got, ogf4.gf4_dequant(words))
+
+
+def test_dequant_row_gather(cuda):
+    import torch
+
+    raw, deq = make_weight(om.TYPE_Q8_0, 50, 512, seed=3)
+    w = _upload(raw, om.TYPE_Q8_0, 50, 512)
+    ids = np.array([7, 0, 49, 7, 1000], dtype=np.int32)  # 1000 is out of range -> zeros
+    got = _rt().dequantize(w, torch.from_numpy(ids).to(cuda)).cpu().numpy()
+    want = np.concatenate([deq[[7, 0, 49, 7]], np.zeros((1, 512), np.float32)])
+    assert _bits_equal(got, want)
+
+
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("rows,k", [(1, 256), (37, 4096), (130, 12288), (5, 8192), (64, 1024)])
+@pytest.mark.parametrize("nb", [1, 2, 3, 8])
+def test_gemv_parity(cuda, name, rows, k, nb):
+    type_id = TYPES[name]
+    rng = np.random.default_rng(rows + k + nb)
+    raw, deq = make_weight(type_id, rows, k, seed=rows * 31 + k)
+    x = activations(rng, nb, k)
+    w = _upload(raw, type_id, rows, k)
+    y = _rt().decode_matvec(w, _t(x, cuda)).cpu().numpy()
+    want = om.matvec_f64(deq, x)
+    assert om.rel_l2(y, want) <= GEMV_REL_L2
+
+
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+def test_gemv_awq_and_residual(cuda, name):
+    import torch
+
+    type_id = TYPES[name]
+    rows, k, nb = 96, 4096, 2
+    rng = np.random.default_rng(5)
+    raw, deq = make_weight(type_id, rows, k, seed=9)
+    x = activations(rng, nb, k)
+    a = awq_scales(rng, k)
+    base = rng.standard_normal((nb, rows)).astype(np.float32)
+    w = _upload(raw, type_id, rows, k)
+    dst = torch.from_numpy(base.copy()).to(cuda)
+    _rt().decode_matvec(w, _t(x, cuda), dst=dst, residual=True, awq=_t(a, cuda))
+    want = base.astype(np.float64) + om.matvec_f64(deq, x, a)
+    assert om.rel_l2(dst.cpu().numpy(), want) <= GEMV_REL_L2
+
+
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("nb", [1, 4])
+def test_swiglu_parity(cuda, name, nb):
+    type_id = TYPES[name]
+    rows, k = 200, 4096
+    rng = np.random.default_rng(21 + nb)
+    rg, dg = make_weight(type_id, rows, k, seed=1, std=0.05)
+    ru, du = make_weight(type_id, rows, k, seed=2, std=0.05)
+    x = activations(rng, nb, k)
+    a = awq_scales(rng, k)
+    g = _upload(rg, type_id, rows, k)
+    u = _upload(ru, type_id, rows, k)
+    y = _rt().ffn_gate_up_swiglu(g, u, _t(x, cuda), awq=_t(a, cuda)).cpu().numpy()
+    want = om.swiglu_f64(dg, du, x, a)
+    assert om.rel_l2(y, want) <= GEMV_REL_L2
+
+
+def test_gemv_extreme_activation_scale(cuda):
+    """fp16 staging of GF4 activations must not overflow or flush: |x| ~ 1e6 and ~ 1e-6."""
+    rows, k = 64, 4096
+    raw, deq = make_weight(om.TYPE_GF4, rows, k, seed=4)
+    w = _upload(raw, om.TYPE_GF4, rows, k)
+    rng = np.random.default_rng(8)
+    for mag in (1e6, 1e-6):
+        x = activations(rng, 2, k) * np.float32(mag)
+        y = _rt().decode_matvec(w, _t(x, cuda)).cpu().numpy()
+        assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
+
+
+def test_gemv_config1_full_size(cuda):
+    """Config 1: GF4 12288x4096, batch 1, W = bf16(0.02 N(0,1)), x = N(0,1)."""
+    raw, deq = make_weight(om.TYPE_GF4, 12288, 4096, seed=1)
+    w = _upload(raw, om.TYPE_GF4, 12288, 4096)
+    x = activations(np.random.default_rng(2), 1, 4096)
+    y = _rt().decode_matvec(w, _t(x, cuda)).cpu().numpy()
+    assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
