@@ -1,0 +1,137 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol that
+include/qw35_hip.h declares, its structs match the ctypes mirrors, and the
+host-side validation rejects bad calls with a message (the 0 + err-buffer
+convention of qw35-server/src/metal/bridge/Qw35FFI.h:1-4)."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from qwowl35_amd import _ffi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qw35_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qw35_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _ffi.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    syms = declared_symbols()
+    assert syms, "no declarations parsed"
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert set(syms) == set(_ffi.PROTOTYPES), "ctypes prototypes must cover exactly the header"
+
+
+def test_struct_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "qw35_hip.h"\n'
+        "int main(void){\n"
+        'printf("%zu %zu %zu %zu %zu\\n", sizeof(qw35_hip_tensor_desc), offsetof(qw35_hip_tensor_desc, dims),'
+        " offsetof(qw35_hip_tensor_desc, type_id), offsetof(qw35_hip_tensor_desc, abs_offset),"
+        " offsetof(qw35_hip_tensor_desc, elements));\n"
+        'printf("%zu %zu %zu %zu\\n", sizeof(qw35_hip_weight), offsetof(qw35_hip_weight, rows),'
+        " offsetof(qw35_hip_weight, bytes), offsetof(qw35_hip_weight, type_id));\n"
+        "return 0;}\n"
+    )
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    a, b = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")[:2]
+    td = _ffi.TensorDesc
+    assert [int(v) for v in a.split()] == [C.sizeof(td), td.dims.offset, td.type_id.offset, td.abs_offset.offset,
+                                           td.elements.offset]
+    w = _ffi.Weight
+    assert [int(v) for v in b.split()] == [C.sizeof(w), w.rows.offset, w.bytes.offset, w.type_id.offset]
+
+
+def _weight(type_id=100, k=4096, rows=16, data=4096, nbytes=None):
+    w = _ffi.Weight()
+    w.data = data
+    w.k = k
+    w.rows = rows
+    rb = {100: k // 8 * 4, 8: k // 32 * 34, 12: k // 256 * 144}.get(type_id, 0)
+    w.bytes = nbytes if nbytes is not None else rb * rows
+    w.type_id = type_id
+    return w
+
+
+def _call_matvec(w, x=4096, dst=4096, nb=1, awq=None):
+    return _ffi.call("qw35_hip_decode_matvec", C.byref(w), C.c_void_p(x), C.c_void_p(awq), C.c_void_p(dst), nb, 0,
+                     None)
+
+
+@pytest.mark.parametrize(
+    "kwargs,needle",
+    [
+        (dict(type_id=14), "unsupported tensor type 14"),
+        (dict(k=100), "multiple of 256"),
+        (dict(k=16384), "<= 12288"),
+        (dict(rows=0), "rows=0"),
+        (dict(nbytes=5), "must be 32768 bytes, got 5"),
+        (dict(data=4097), "16-byte aligned"),
+    ],
+)
+def test_decode_matvec_rejects_bad_weights(lib, kwargs, needle):
+    with pytest.raises(_ffi.Qw35Error, match=re.escape(needle)):
+        _call_matvec(_weight(**kwargs))
+
+
+def test_decode_matvec_rejects_bad_batch_and_pointers(lib):
+    w = _weight()
+    with pytest.raises(_ffi.Qw35Error, match="n_batch=0"):
+        _call_matvec(w, nb=0)
+    with pytest.raises(_ffi.Qw35Error, match="n_batch=9"):
+        _call_matvec(w, nb=9)
+    with pytest.raises(_ffi.Qw35Error, match="null input"):
+        _call_matvec(w, x=0)
+    with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
+        _call_matvec(w, x=4100)
+
+
+def test_swiglu_rejects_mismatched_pair(lib):
+    g = _weight()
+    u = _weight(k=8192)
+    with pytest.raises(_ffi.Qw35Error, match="share type and shape"):
+        _ffi.call("qw35_hip_ffn_gate_up_swiglu", C.byref(g), C.byref(u), C.c_void_p(4096), None, C.c_void_p(4096), 1,
+                  None)
+
+
+def test_weight_view_validates_descriptor(lib):
+    d = _ffi.TensorDesc()
+    d.dims[0], d.dims[1], d.dims[2], d.dims[3] = 4096, 8, 1, 1
+    d.n_dims = 2
+    d.type_id = 100
+    d.abs_offset = 256
+    d.bytes = 8 * 2048
+    d.elements = 4096 * 8
+    out = _ffi.Weight()
+    _ffi.call("qw35_hip_weight_view", C.byref(d), C.c_void_p(1 << 20), C.byref(out))
+    assert out.data == (1 << 20) + 256 and out.k == 4096 and out.rows == 8 and out.type_id == 100
+    d.elements = 7
+    with pytest.raises(_ffi.Qw35Error, match="elements"):
+        _ffi.call("qw35_hip_weight_view", C.byref(d), C.c_void_p(1 << 20), C.byref(out))
+    d.elements = 4096 * 8
+    d.n_dims = 1
+    with pytest.raises(_ffi.Qw35Error, match="not a matrix"):
+        _ffi.call("qw35_hip_weight_view", C.byref(d), C.c_void_p(1 << 20), C.byref(out))
+
+
+def test_error_buffer_truncates_safely(lib):
+    w = _weight(type_id=14)
+    err = C.create_string_buffer(8)
+    rc = lib.qw35_hip_decode_matvec(C.byref(w), C.c_void_p(4096), None, C.c_void_p(4096), 1, 0, None, err, 8)
+    assert rc == 0 and len(err.value) == 7

@@ -137,3 +137,20 @@ def test_gemv_config1_full_size(cuda):
     x = activations(np.random.default_rng(2), 1, 4096)
     y = _rt().decode_matvec(w, _t(x, cuda)).cpu().numpy()
     assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
+
+
+def test_golden_fixtures(cuda):
+    """The library reproduces the committed fixtures (tests/golden/gemv_golden.npz)."""
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "gemv_golden.npz"), allow_pickle=False)
+    x = _t(g["x"], cuda)
+    a = _t(g["awq"], cuda)
+    for name, raw_key, rows in (("gf4", "gf4_words", 32), ("q8_0", "q8_0_raw", 16), ("q4_k", "q4_k_raw", 16)):
+        type_id = TYPES[name]
+        w = _upload(np.ascontiguousarray(g[raw_key]).view(np.uint8), type_id, rows, 512)
+        assert _bits_equal(_rt().dequantize(w).cpu().numpy(), g[f"{name}_deq"]), name
+        y = _rt().decode_matvec(w, x, awq=a).cpu().numpy()
+        assert om.rel_l2(y, g[f"{name}_y"]) <= GEMV_REL_L2, name
+    w = _upload(g["gf4_any_words"].view(np.uint8), om.TYPE_GF4, 8, 512)
+    assert _bits_equal(_rt().dequantize(w).cpu().numpy(), g["gf4_any_deq"])
