@@ -2,21 +2,26 @@
 """Benchmark of the quantized GEMV path on one MI355X.
 
 Headline (BASELINE.json metric, config 1): GF4 decode GEMV, batch 1, W 12288x4096
-(bf16 N(0,0.02) packed by the GF4 packer), x fp32 N(0,1).  One "step" is one
-GEMV launch over one weight copy; the launches rotate over enough distinct
-weight copies (> 600 MB) that every step streams its weights from HBM rather
-than the 256 MB Infinity Cache.  Inputs are resident in HBM before timing.
+= GF4 pack of bf16(0.02 N(0,1)), x fp32 N(0,1).  One "step" is one GEMV launch
+over one weight copy; the launches rotate over 32 distinct weight copies
+(805 MB > the 256 MB Infinity Cache) so every step streams its weights from HBM.
+Weights and activations are made on the GPU (torch's seeded generator, the
+library's own GF4 / q8_0 / Q4_K encoders) and are resident before timing.
 
-Printed: one JSON line with the driver's contract fields plus
-``roofline`` (dominant kernel, from per-launch HIP events on the launch stream)
-and ``cpu_baseline`` (the numpy oracle dequant + matvec on the host cores).
-Further configs are reported under ``extra``.
+Launches are captured into a hipGraph and replayed; HIP events on the replay
+stream bracket the timed replays.  Printed: one JSON line with the driver's
+contract fields plus ``roofline`` (dominant kernel) and ``cpu_baseline`` (the
+numpy oracle GF4 dequant + matvec on this host's cores), and under ``extra``
+the other decode configs: GF4 batches 2..8 and the transposed shape, the q8_0
+layer set (config 2) and the Q4_K down / LM-head GEMVs at batch 1 and 8
+(config 3).  ``--gpus`` above 1 is refused: this build measures one GPU.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -26,124 +31,220 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gf4_gemv_b1_12288x4096_traffic.md")
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def gf4_weight(rows: int, k: int, seed: int) -> np.ndarray:
-    """Config-1 weights: bf16_RNE(0.02 N(0,1)) packed to GF4 words (uint8 view)."""
+class Bench:
+    def __init__(self, torch, runtime, seed: int = 1):
+        self.torch = torch
+        self.rt = runtime
+        self.dev = torch.device("cuda:0")
+        self.gen = torch.Generator(device=self.dev)
+        self.gen.manual_seed(seed)
+        self.stream = torch.cuda.Stream()
+
+    def normal(self, shape, std=1.0, bf16=False):
+        t = self.torch.randn(shape, generator=self.gen, device=self.dev, dtype=self.torch.float32)
+        if std != 1.0:
+            t.mul_(std)
+        if bf16:
+            t = t.to(self.torch.bfloat16).to(self.torch.float32)
+        return t
+
+    def weight(self, type_id, rows, k, std=0.02, tile_rows=None):
+        """Encoded N(0, std) weight.  tile_rows: encode that many distinct rows and
+        repeat them (the LM head, whose 1.0e9 fp32 source would not be worth making)."""
+        if tile_rows is None or tile_rows >= rows:
+            src = self.normal((rows, k), std, bf16=(type_id == self.rt.TYPE_GF4))
+            hw = self.rt.quantize_weight(src, type_id)
+            del src
+            return hw
+        src = self.normal((tile_rows, k), std)
+        part = self.rt.quantize(src, type_id)
+        rb = self.rt.row_bytes(type_id, k)
+        full = self.torch.empty(rows * rb, dtype=self.torch.uint8, device=self.dev)
+        for r0 in range(0, rows, tile_rows):
+            n = min(tile_rows, rows - r0)
+            full[r0 * rb:(r0 + n) * rb].copy_(part[:n * rb])
+        return self.rt.HipWeight.from_device(full, type_id, rows, k)
+
+    def time_calls(self, calls, steps: int, warmup: int):
+        """Graph-capture ``calls`` (one launch each) and replay; returns
+        (ms per launch, ms per graph, launches timed)."""
+        torch = self.torch
+        n = len(calls)
+        with torch.cuda.stream(self.stream):
+            for c in calls:  # first-touch and code-object load outside the capture
+                c(self.stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=self.stream):
+            for c in calls:
+                c(self.stream)
+        reps_w = max(1, warmup // n)
+        reps = max(1, steps // n)
+        with torch.cuda.stream(self.stream):
+            for _ in range(reps_w):
+                graph.replay()
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.stream):  # replays and events on the same stream
+            ev0.record(self.stream)
+            for _ in range(reps):
+                graph.replay()
+            ev1.record(self.stream)
+        torch.cuda.synchronize()
+        total = ev0.elapsed_time(ev1)
+        return total / (reps * n), total / reps, reps * n
+
+
+def gemv_calls(rt, weights, x, y):
+    return [lambda s, w=w: rt.decode_matvec(w, x, y, stream=s) for w in weights]
+
+
+def gemv_bytes(type_id, rows, k, nb, rt):
+    return rows * rt.row_bytes(type_id, k) + 4 * nb * (k + rows)
+
+
+def read_traffic(kernel_hint: str):
+    """HBM bytes per launch from the committed PMC summary, if it names this kernel."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None, None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
+    k = re.search(r"kernel:\s*`([^`]+)`", text)
+    if not m or not k or kernel_hint not in k.group(1):
+        return None, None
+    return int(m.group(1)), k.group(1)
+
+
+def cpu_baseline_gf4(rows: int, k: int, seed: int, reps: int):
+    """numpy oracle on the host: GF4 dequant (vectorised numpy) + fp32 W @ x (BLAS)."""
+    from threadpoolctl import threadpool_info
+
     from oracle import gf4 as ogf4
     from oracle import matvec as om
 
     rng = np.random.default_rng(seed)
     w = om.bf16_round(rng.standard_normal((rows, k), dtype=np.float32) * np.float32(0.02))
-    return ogf4.gf4_pack(w).view(np.uint8).reshape(rows, -1)
-
-
-def time_gemv(weights, x, y, steps: int, warmup: int, torch, runtime, awq=None, residual=False):
-    """Time `steps` GEMV launches rotating over `weights` (list of HipWeight).
-
-    The launches are captured once into a hipGraph (one launch per weight copy)
-    and the graph is replayed, so the host launch rate does not limit the GPU.
-    HIP events bracket the replays on the capture/replay stream.  Returns
-    (ms_per_step, kernel_us) where kernel_us is the average per-launch time.
-    """
-    n = len(weights)
-    stream = torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        for i in range(n):  # warm-up outside capture (first-touch, code object load)
-            runtime.decode_matvec(weights[i], x, y, residual=residual, awq=awq)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for i in range(n):
-            runtime.decode_matvec(weights[i], x, y, residual=residual, awq=awq)
-    reps_w = max(1, warmup // n)
-    reps = max(1, steps // n)
-    with torch.cuda.stream(stream):
-        for _ in range(reps_w):
-            graph.replay()
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    total_ms = ev0.elapsed_time(ev1)
-    launches = reps * n
-    return total_ms / launches, total_ms * 1e3 / launches, launches
-
-
-def cpu_baseline_gf4(rows: int, k: int, seed: int, reps: int = 5):
-    """numpy oracle: GF4 dequant (vectorised) + fp32 W @ x (OpenBLAS), median of reps."""
-    from oracle import gf4 as ogf4
-
-    words = gf4_weight(rows, k, seed).view("<u4")
-    x = np.random.default_rng(seed + 1).standard_normal(k, dtype=np.float32)
+    words = ogf4.gf4_pack(w)
+    x = rng.standard_normal(k, dtype=np.float32)
     ogf4.gf4_dequant(words) @ x  # warm-up
     t_dq, t_mv = [], []
     for _ in range(reps):
         t0 = time.perf_counter()
-        w = ogf4.gf4_dequant(words)
+        wd = ogf4.gf4_dequant(words)
         t1 = time.perf_counter()
-        _ = w @ x
+        _ = wd @ x
         t2 = time.perf_counter()
         t_dq.append(t1 - t0)
         t_mv.append(t2 - t1)
-    return float(np.median(t_dq)), float(np.median(t_mv))
+    blas = max([int(p.get("num_threads", 1)) for p in threadpool_info()] or [1])
+    return float(np.median(t_dq)), float(np.median(t_mv)), blas
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--copies", type=int, default=32, help="distinct weight copies rotated (>= 24)")
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--copies", type=int, default=32, help="distinct GF4 weight copies rotated (>= 24)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--headline-only", action="store_true", help="skip the extra configs")
+    ap.add_argument("--cpu-reps", type=int, default=40)
     args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1"}))
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it (--gpus 1)"}),
+              flush=True)
         return 2
 
     import torch
 
-    from qwowl35_amd import runtime
+    from qwowl35_amd import runtime as rt
 
+    b = Bench(torch, rt)
     rows, k = 12288, 4096
-    dev = torch.device("cuda:0")
-    log(f"config1: GF4 {rows}x{k} b1, {args.copies} copies")
-    raw = torch.from_numpy(gf4_weight(rows, k, seed=1))
-    base = runtime.HipWeight.upload(raw, runtime.TYPE_GF4, rows, k, device=dev)
-    weights = [base]
-    for _ in range(args.copies - 1):
-        st = base.storage.clone()
-        weights.append(runtime.HipWeight.from_device(st, runtime.TYPE_GF4, rows, k))
-    x = torch.from_numpy(np.random.default_rng(2).standard_normal(k, dtype=np.float32)).to(dev)
-    y = torch.zeros(rows, dtype=torch.float32, device=dev)
+    log(f"config 1: GF4 {rows}x{k} b1, {args.copies} copies")
+    weights = [b.weight(rt.TYPE_GF4, rows, k) for _ in range(args.copies)]
+    x = b.normal((1, k))
+    y = torch.zeros((1, rows), dtype=torch.float32, device=b.dev)
+    # plain device copy of a known size: the calibration kernel of the PMC traffic passes
+    calib = weights[0].storage.clone()
     torch.cuda.synchronize()
+    del calib
 
-    ms_per_step, kernel_us, launches = time_gemv(weights, x, y, args.steps, args.warmup, torch, runtime)
-    algo_bytes = rows * k // 2 + 4 * k + 4 * rows
-    value = algo_bytes / (ms_per_step * 1e-3) / 1e9
-    achieved = algo_bytes / (kernel_us * 1e-6) / 1e9
-    log(f"ms/step {ms_per_step:.5f}  kernel {kernel_us:.3f} us  achieved {achieved:.0f} GB/s")
+    ms, _, launches = b.time_calls(gemv_calls(rt, weights, x, y), args.steps, args.warmup)
+    algo = gemv_bytes(rt.TYPE_GF4, rows, k, 1, rt)
+    value = algo / (ms * 1e-3) / 1e9
+    log(f"GF4 b1: {ms * 1e3:.3f} us/launch, {value:.0f} GB/s")
+    traffic, traffic_kernel = read_traffic("gf4_mfma_gemv<1,")
+
+    extra = {}
+    if not args.headline_only:
+        for nb in (2, 4, 8):
+            xb = b.normal((nb, k))
+            yb = torch.zeros((nb, rows), dtype=torch.float32, device=b.dev)
+            m, _, _ = b.time_calls(gemv_calls(rt, weights, xb, yb), args.steps // 2, args.warmup)
+            extra[f"gf4_b{nb}_12288x4096"] = {"us": round(m * 1e3, 3),
+                                              "GB/s": round(gemv_bytes(rt.TYPE_GF4, rows, k, nb, rt) / m / 1e6, 1)}
+        del weights
+        wt = [b.weight(rt.TYPE_GF4, 4096, 12288) for _ in range(args.copies)]
+        xt = b.normal((1, 12288))
+        yt = torch.zeros((1, 4096), dtype=torch.float32, device=b.dev)
+        m, _, _ = b.time_calls(gemv_calls(rt, wt, xt, yt), args.steps // 2, args.warmup)
+        extra["gf4_b1_4096x12288"] = {"us": round(m * 1e3, 3),
+                                      "GB/s": round(gemv_bytes(rt.TYPE_GF4, 4096, 12288, 1, rt) / m / 1e6, 1)}
+        del wt
+
+        # config 2: q8_0 projections of one decoder layer, 3 distinct sets (670 MB)
+        shapes = [(8192, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096),
+                  (4096, 12288)]
+        sets = [[b.weight(rt.TYPE_Q8_0, r, kk) for r, kk in shapes] for _ in range(3)]
+        acts = {kk: b.normal((1, kk)) for kk in (4096, 12288)}
+        outs = {r: torch.zeros((1, r), dtype=torch.float32, device=b.dev) for r, _ in shapes}
+        calls = [lambda s, w=w: rt.decode_matvec(w, acts[w.k], outs[w.rows], stream=s) for st in sets for w in st]
+        m, _, _ = b.time_calls(calls, args.steps // 2, args.warmup)
+        per_set_ms = m * len(shapes)
+        set_bytes = sum(gemv_bytes(rt.TYPE_Q8_0, r, kk, 1, rt) for r, kk in shapes)
+        extra["q8_0_layer_set_b1"] = {"us_per_set": round(per_set_ms * 1e3, 3), "bytes": set_bytes,
+                                      "GB/s": round(set_bytes / per_set_ms / 1e6, 1)}
+        del sets
+
+        # config 3: Q4_K down 4096x12288 (24 copies) and LM head 248320x4096, batch 1 and 8
+        down = [b.weight(rt.TYPE_Q4_K, 4096, 12288) for _ in range(24)]
+        head = b.weight(rt.TYPE_Q4_K, 248320, 4096, tile_rows=16384)
+        for nb in (1, 8):
+            xd = b.normal((nb, 12288))
+            yd = torch.zeros((nb, 4096), dtype=torch.float32, device=b.dev)
+            m, _, _ = b.time_calls(gemv_calls(rt, down, xd, yd), args.steps // 4, args.warmup // 2)
+            extra[f"q4_k_down_b{nb}_4096x12288"] = {
+                "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 4096, 12288, nb, rt) / m / 1e6, 1)}
+            xh = b.normal((nb, 4096))
+            yh = torch.zeros((nb, 248320), dtype=torch.float32, device=b.dev)
+            m, _, _ = b.time_calls(gemv_calls(rt, [head], xh, yh), 200, 20)
+            extra[f"q4_k_head_b{nb}_248320x4096"] = {
+                "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 248320, 4096, nb, rt) / m / 1e6, 1)}
+        del down, head
+        for key, v in extra.items():
+            log(f"{key}: {v}")
 
     cpu = None
     if not args.no_cpu:
-        t_dq, t_mv = cpu_baseline_gf4(rows, k, seed=1)
-        cores = os.cpu_count() or 1
+        t_dq, t_mv, blas = cpu_baseline_gf4(rows, k, seed=1, reps=args.cpu_reps)
         cpu = {
-            "value": round(algo_bytes / (t_dq + t_mv) / 1e9, 3),
+            "value": round(algo / (t_dq + t_mv) / 1e9, 3),
             "unit": "GB/s",
-            "cores": cores,
+            "cores": blas,
             "kind": "port",
-            "sample": f"numpy oracle GF4 dequant ({t_dq * 1e3:.1f} ms) + fp32 W@x ({t_mv * 1e3:.1f} ms), "
-                      f"12288x4096 b1, median of 5",
+            "sample": f"numpy oracle on the host: GF4 dequant of the 12288x4096 b1 weight (1 thread, "
+                      f"{t_dq * 1e3:.1f} ms) + fp32 W@x ({blas} BLAS threads, {t_mv * 1e3:.2f} ms), "
+                      f"median of {args.cpu_reps}",
         }
     out = {
         "metric": "GF4 b1 matvec HBM GB/s (12288x4096)",
@@ -152,17 +253,18 @@ def main() -> int:
         "n_gpus": 1,
         "steps": launches,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 6),
+        "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "gf4-w/fp32-acc",
+        "dtype": "gf4-weights/fp32-acc",
         "data": "synthetic",
         "config": {"workload": "gf4_matvec_b1_12288x4096", "rows": rows, "k": k, "batch": 1,
                    "weight_copies": args.copies},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
+        "extra": extra,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -99,6 +99,17 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weig
 int qw35_hip_dequantize(const qw35_hip_weight *w, const uint32_t *row_ids, uint32_t n_rows, float *dst,
                         void *stream, char *err, uintptr_t err_len);
 
+/* Weight producer: fp32 src [rows][k] (device, 16-byte aligned) -> raw tensor
+ * bytes of type_id in dst (device, 16-byte aligned, rows * row_bytes(type, k)
+ * bytes).  col_scale (device fp32 [k], 16-byte aligned, nullable) multiplies
+ * column c before encoding: the AWQ column scale of pack_ffn_gf4
+ * (tools/qw35_cook_common.py:182-199).  GF4 is bit-identical to the reference
+ * packer pack_gf4_prepared(rows, scale_search=False) (:83-119).  q8_0 (k % 32)
+ * and Q4_K (k % 256) are this library's min/max encoders; the reference has
+ * none (it reads those types through gguf-py).  src must be finite. */
+int qw35_hip_quantize(uint32_t type_id, const float *src, uint64_t rows, uint64_t k, const float *col_scale,
+                      void *dst, void *stream, char *err, uintptr_t err_len);
+
 /* Wait for the stream and report any asynchronous device error.  Replaces
  * qw35_metal_runtime_sync (Qw35FFI.h:71-72). */
 int qw35_hip_sync(void *stream, char *err, uintptr_t err_len);

@@ -64,6 +64,11 @@ PROTOTYPES: dict[str, tuple] = {
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
     ),
+    "qw35_hip_quantize": (
+        C.c_int,
+        [C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_char_p,
+         C.c_size_t],
+    ),
     "qw35_hip_sync": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
 }
 

@@ -233,6 +233,37 @@ int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint3
                : 0;
 }
 
+int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_t k, const float* col_scale,
+                      void* dst, void* stream, char* err, uintptr_t err_len) {
+    if (!type_supported(type_id)) {
+        set_err(err, err_len, "quantize: unsupported tensor type %u", type_id);
+        return 0;
+    }
+    const uint64_t block = type_id == qw35::kTypeGF4 ? 8 : type_id == qw35::kTypeQ8_0 ? 32 : 256;
+    if (k == 0 || k % block != 0 || k > 0x7fffffffull) {
+        set_err(err, err_len, "quantize: k=%llu must be a positive multiple of %llu for %s",
+                (unsigned long long)k, (unsigned long long)block, type_name(type_id));
+        return 0;
+    }
+    if (rows == 0 || rows > 0x7fffffffull) {
+        set_err(err, err_len, "quantize: rows=%llu out of range", (unsigned long long)rows);
+        return 0;
+    }
+    if (!src || !dst) {
+        set_err(err, err_len, "quantize: null input or output");
+        return 0;
+    }
+    if (((uintptr_t)src & 15u) || ((uintptr_t)dst & 15u) || (col_scale && ((uintptr_t)col_scale & 15u))) {
+        set_err(err, err_len, "quantize: src, dst and col_scale must be 16-byte aligned");
+        return 0;
+    }
+    return check_hip(qw35::launch_quantize(type_id, src, (int)rows, (int)k, col_scale, dst,
+                                           static_cast<hipStream_t>(stream)),
+                     "quantize", err, err_len)
+               ? 1
+               : 0;
+}
+
 int qw35_hip_sync(void* stream, char* err, uintptr_t err_len) {
     hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     if (e == hipSuccess) e = hipGetLastError();

@@ -1,0 +1,240 @@
+// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K tensor bytes, on the GPU.
+//
+// GF4 is the reference packer pack_gf4_prepared(rows, scale_search=False)
+// (tools/qw35_cook_common.py:83-119), including the optional AWQ column
+// multiply that pack_ffn_gf4 applies before packing (:182-199, the multiply
+// at :198).  Every step is an IEEE fp32 / binary16 operation with the same
+// rounding as the numpy statement, so the words are bit-identical:
+//   gmax  = first element of the 8-group with the largest |x|, with its sign
+//   b     = (bits(fp16_rne(gmax)) + 0x80) >> 8          (e5m2 byte, :48-51)
+//   s     = fp16(b << 8)                                (:54-56)
+//   q_raw = clip(rint(fl(x / s) * -4 + 4), 0, 7), 0 where s == 0   (:67-80)
+//   word  = b | sum_i (q_raw_i ^ 4) << (8 + 3 i)        (:113-118)
+// q8_0 and Q4_K have no encoder in the reference (it reads them through the
+// external gguf-py); these are this library's own min/max encoders, the GPU
+// statement of the ones the tests use, producing valid GGUF blocks.
+//
+// Inputs must be finite: NaN ordering in numpy's argmax and its float->int
+// casts are platform behaviour, not part of the format.
+#include "qw35_device.h"
+#include "qw35_kernels.h"
+
+namespace qw35 {
+namespace {
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// Grid-stride loops keep the grid at a fixed size for any tensor.
+constexpr int kEncodeThreads = 256;
+constexpr int kEncodeBlocks = 2048;
+
+// One thread per GF4 word (8 consecutive columns of a row).
+__global__ __launch_bounds__(kEncodeThreads) void gf4_pack_kernel(const float* __restrict__ src,
+                                                                  const float* __restrict__ col_scale,
+                                                                  uint32_t* __restrict__ dst, uint64_t n_words,
+                                                                  uint32_t words_per_row) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_words;
+         i += (uint64_t)gridDim.x * kEncodeThreads) {
+        const float4_t lo = *reinterpret_cast<const float4_t*>(src + 8 * i);
+        const float4_t hi = *reinterpret_cast<const float4_t*>(src + 8 * i + 4);
+        float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        if (col_scale) {
+            const uint32_t c0 = 8u * (uint32_t)(i % words_per_row);
+            const float4_t s0 = *reinterpret_cast<const float4_t*>(col_scale + c0);
+            const float4_t s1 = *reinterpret_cast<const float4_t*>(col_scale + c0 + 4);
+            const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(v[j], s[j]);
+        }
+        int best = 0;
+        float best_abs = fabsf(v[0]);
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            if (fabsf(v[j]) > best_abs) {  // strict: the first maximum wins
+                best_abs = fabsf(v[j]);
+                best = j;
+            }
+        }
+        float gmax = v[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j)
+            if (j == best) gmax = v[j];
+        const uint32_t b = ((f32_to_f16_bits(gmax) + 0x80u) >> 8) & 0xFFu;
+        const float s = f16_bits_to_f32(b << 8);
+        uint32_t word = b;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float ratio = (s != 0.0f) ? __fdiv_rn(v[j], s) : 0.0f;
+            const float t = __fadd_rn(__fmul_rn(ratio, -4.0f), 4.0f);
+            const float q = fminf(fmaxf(rintf(t), 0.0f), 7.0f);
+            word |= (((uint32_t)q) ^ 4u) << (8 + 3 * j);
+        }
+        dst[i] = word;
+    }
+}
+
+// One thread per q8_0 block: d = max|x| / 127, q = round_half_away(x * (1/d)).
+__global__ __launch_bounds__(kEncodeThreads) void q8_0_quantize_kernel(const float* __restrict__ src,
+                                                                       const float* __restrict__ col_scale,
+                                                                       uint8_t* __restrict__ dst, uint64_t n_blocks,
+                                                                       uint32_t blocks_per_row) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_blocks;
+         i += (uint64_t)gridDim.x * kEncodeThreads) {
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4_t t = *reinterpret_cast<const float4_t*>(src + 32 * i + 4 * j);
+            v[4 * j] = t.x;
+            v[4 * j + 1] = t.y;
+            v[4 * j + 2] = t.z;
+            v[4 * j + 3] = t.w;
+        }
+        if (col_scale) {
+            const float* cs = col_scale + 32u * (uint32_t)(i % blocks_per_row);
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v[j] = __fmul_rn(v[j], cs[j]);
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float inv = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
+        uint8_t* blk = dst + 34 * i;  // 34-byte blocks: 2-byte aligned
+        uint16_t* h = reinterpret_cast<uint16_t*>(blk);
+        h[0] = (uint16_t)f32_to_f16_bits(d);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int q2[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float sc = __fmul_rn(v[2 * j + u], inv);
+                float q = truncf(__fadd_rn(sc, copysignf(0.5f, sc)));
+                q = fminf(fmaxf(q, -127.0f), 127.0f);
+                q2[u] = (int)q;
+            }
+            h[1 + j] = (uint16_t)((uint32_t)(q2[0] & 0xFF) | ((uint32_t)(q2[1] & 0xFF) << 8));
+        }
+    }
+}
+
+// One thread per Q4_K super-block (256 columns, 8 sub-blocks of 32):
+//   lo_j = min(min(x), 0), hi_j = max(x), scale_j = (hi_j - lo_j) / 15, min_j = -lo_j
+//   d = fp16(max_j scale_j / 63), dmin = fp16(max_j min_j / 63)
+//   sc_j = clip(rint(scale_j / d), 0, 63), m_j = clip(rint(min_j / dmin), 0, 63)
+//   q = clip(rint((x + dmin*m_j) / (d*sc_j)), 0, 15)
+// with the 12-byte 6-bit scale packing of get_scale_min_k4
+// (qw35-server/src/metal/qw35_matvec.metal:2-12) and the nibble layout
+// qs[32c + l] = q[64c + l] | q[64c + 32 + l] << 4.
+__global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const float* __restrict__ src,
+                                                                       const float* __restrict__ col_scale,
+                                                                       uint8_t* __restrict__ dst, uint64_t n_blocks,
+                                                                       uint32_t blocks_per_row) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_blocks;
+         i += (uint64_t)gridDim.x * kEncodeThreads) {
+        const float* x = src + 256 * i;
+        const float* cs = col_scale ? col_scale + 256u * (uint32_t)(i % blocks_per_row) : nullptr;
+        float scale[8], mins[8];
+        for (int j = 0; j < 8; ++j) {
+            float lo = INFINITY, hi = -INFINITY;
+            for (int l = 0; l < 32; ++l) {
+                const float v = cs ? __fmul_rn(x[32 * j + l], cs[32 * j + l]) : x[32 * j + l];
+                lo = fminf(lo, v);
+                hi = fmaxf(hi, v);
+            }
+            lo = fminf(lo, 0.0f);
+            scale[j] = __fdiv_rn(__fsub_rn(hi, lo), 15.0f);
+            mins[j] = -lo;
+        }
+        float smax = scale[0], mmax = mins[0];
+        for (int j = 1; j < 8; ++j) {
+            smax = fmaxf(smax, scale[j]);
+            mmax = fmaxf(mmax, mins[j]);
+        }
+        const uint32_t d_bits = f32_to_f16_bits(__fdiv_rn(smax, 63.0f));
+        const uint32_t dmin_bits = f32_to_f16_bits(__fdiv_rn(mmax, 63.0f));
+        const float df = f16_bits_to_f32(d_bits);
+        const float dminf = f16_bits_to_f32(dmin_bits);
+        uint32_t sc[8], mq[8];
+        float step[8], offs[8];
+        for (int j = 0; j < 8; ++j) {
+            const float a = (df != 0.0f) ? rintf(__fdiv_rn(scale[j], df)) : 0.0f;
+            const float m = (dminf != 0.0f) ? rintf(__fdiv_rn(mins[j], dminf)) : 0.0f;
+            sc[j] = (uint32_t)fminf(fmaxf(a, 0.0f), 63.0f);
+            mq[j] = (uint32_t)fminf(fmaxf(m, 0.0f), 63.0f);
+            step[j] = __fmul_rn(df, (float)sc[j]);
+            offs[j] = __fmul_rn(dminf, (float)mq[j]);
+        }
+        uint8_t* blk = dst + 144 * i;  // 144-byte blocks: 16-byte aligned
+        uint32_t head[4];
+        head[0] = d_bits | (dmin_bits << 16);
+        uint8_t scales[12];
+        for (int j = 0; j < 4; ++j) {
+            scales[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            scales[j + 4] = (uint8_t)((mq[j] & 63) | ((mq[j + 4] >> 4) << 6));
+            scales[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mq[j + 4] & 0xF) << 4));
+        }
+        for (int w = 0; w < 3; ++w)
+            head[1 + w] = (uint32_t)scales[4 * w] | ((uint32_t)scales[4 * w + 1] << 8) |
+                          ((uint32_t)scales[4 * w + 2] << 16) | ((uint32_t)scales[4 * w + 3] << 24);
+        *reinterpret_cast<uint4_t*>(blk) = uint4_t{head[0], head[1], head[2], head[3]};
+        for (int c = 0; c < 4; ++c) {
+            for (int l4 = 0; l4 < 32; l4 += 16) {
+                uint32_t packed[4] = {0, 0, 0, 0};
+                for (int l = 0; l < 16; ++l) {
+                    uint32_t nib[2];
+                    for (int h = 0; h < 2; ++h) {
+                        const int j = 2 * c + h;
+                        const int e = 32 * j + l4 + l;
+                        const float v = cs ? __fmul_rn(x[e], cs[e]) : x[e];
+                        const float qf = (step[j] != 0.0f) ? __fdiv_rn(__fadd_rn(v, offs[j]), step[j]) : 0.0f;
+                        nib[h] = (uint32_t)fminf(fmaxf(rintf(qf), 0.0f), 15.0f);
+                    }
+                    packed[l >> 2] |= (nib[0] | (nib[1] << 4)) << (8 * (l & 3));
+                }
+                *reinterpret_cast<uint4_t*>(blk + 16 + 32 * c + l4) =
+                    uint4_t{packed[0], packed[1], packed[2], packed[3]};
+            }
+        }
+    }
+}
+
+unsigned grid_for(uint64_t n) {
+    const uint64_t g = (n + kEncodeThreads - 1) / kEncodeThreads;
+    return (unsigned)(g < (uint64_t)kEncodeBlocks ? g : (uint64_t)kEncodeBlocks);
+}
+
+}  // namespace
+
+hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, const float* col_scale, void* dst,
+                           hipStream_t stream) {
+    const uint64_t r = (uint64_t)rows;
+    switch (type_id) {
+        case kTypeGF4: {
+            const uint64_t n = r * (uint64_t)(k / 8);
+            hipLaunchKernelGGL(gf4_pack_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src, col_scale,
+                               static_cast<uint32_t*>(dst), n, (uint32_t)(k / 8));
+            break;
+        }
+        case kTypeQ8_0: {
+            const uint64_t n = r * (uint64_t)(k / 32);
+            hipLaunchKernelGGL(q8_0_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
+                               col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 32));
+            break;
+        }
+        default: {
+            const uint64_t n = r * (uint64_t)(k / 256);
+            hipLaunchKernelGGL(q4_k_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
+                               col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
+            break;
+        }
+    }
+    return hipGetLastError();
+}
+
+}  // namespace qw35

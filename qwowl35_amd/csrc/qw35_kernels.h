@@ -36,6 +36,11 @@ hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, const uint32_t* row_ids,
                           int n_out_rows, float* dst, hipStream_t stream);
 
+// fp32 [rows][k] -> tensor bytes of type_id (GF4 packer / q8_0 / Q4_K encoders);
+// col_scale (nullable) multiplies column c first.
+hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, const float* col_scale, void* dst,
+                           hipStream_t stream);
+
 // GF4 prefill dequant-matmul on bf16 MFMA: C[m][n] = sum_k bf16(a_k * A[m][k]) * W[n][k].
 // out_f32 != 0 writes fp32, otherwise bf16 (RNE).
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const uint16_t* a_bf16, const float* awq,

@@ -7,6 +7,7 @@ Names and argument meaning follow the reference runtime's encoders
 * ``ffn_gate_up_swiglu``  <- ``encodeGf4FusedFfn`` / ``qw35_ffn_gate_up_swiglu_gf4_f32`` (:13-35)
 * ``matvec_batch``        <- ``encodeMatvecBatch`` for 1..8 tokens (:260-306)
 * ``dequantize``          <- the per-codec dequant helpers / ``qw35_get_rows_*`` gathers
+* ``quantize``            <- ``pack_ffn_gf4`` / ``pack_gf4_prepared`` (tools/qw35_cook_common.py:83-119,182-199)
 
 Device memory and streams come from torch (plumbing only); every computation
 is a call into ``libqw35_hip.so``.  Errors raise ``Qw35Error`` with the
@@ -143,6 +144,31 @@ def dequantize(w: HipWeight, row_ids: torch.Tensor | None = None, stream=None) -
     dst = torch.empty((n, w.k), dtype=torch.float32, device=w.storage.device)
     _ffi.call("qw35_hip_dequantize", C.byref(w.view), _ptr(row_ids), n, _ptr(dst), _stream(stream))
     return dst
+
+
+def quantize(src: torch.Tensor, type_id: int, col_scale: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Encode an fp32 [rows, k] device matrix; returns the raw tensor bytes (uint8, device).
+
+    GF4 is the reference packer ``pack_gf4_prepared(scale_search=False)`` after
+    the AWQ column multiply of ``pack_ffn_gf4`` (tools/qw35_cook_common.py:83-119,
+    182-199); q8_0 / Q4_K are the library's own encoders.
+    """
+    if src.dtype != torch.float32 or not src.is_cuda or not src.is_contiguous() or src.dim() != 2:
+        raise Qw35Error("quantize: src must be a contiguous 2-D fp32 device tensor")
+    if col_scale is not None and (col_scale.dtype != torch.float32 or not col_scale.is_cuda
+                                  or col_scale.numel() != src.shape[1] or not col_scale.is_contiguous()):
+        raise Qw35Error("quantize: col_scale must be a contiguous fp32 device tensor of length k")
+    rows, k = int(src.shape[0]), int(src.shape[1])
+    out = torch.empty(rows * row_bytes(type_id, k), dtype=torch.uint8, device=src.device)
+    _ffi.call("qw35_hip_quantize", type_id, _ptr(src), rows, k, _ptr(col_scale), _ptr(out), _stream(stream))
+    return out
+
+
+def quantize_weight(src: torch.Tensor, type_id: int, col_scale: torch.Tensor | None = None,
+                    stream=None) -> HipWeight:
+    """``quantize`` into a new HBM tensor, returned as a GEMV-ready ``HipWeight``."""
+    raw = quantize(src, type_id, col_scale, stream)
+    return HipWeight.from_device(raw, type_id, int(src.shape[0]), int(src.shape[1]))
 
 
 def sync(stream=None) -> None:

@@ -135,3 +135,25 @@ def test_error_buffer_truncates_safely(lib):
     err = C.create_string_buffer(8)
     rc = lib.qw35_hip_decode_matvec(C.byref(w), C.c_void_p(4096), None, C.c_void_p(4096), 1, 0, None, err, 8)
     assert rc == 0 and len(err.value) == 7
+
+
+@pytest.mark.parametrize(
+    "type_id,k,rows,needle",
+    [
+        (14, 256, 1, "unsupported tensor type 14"),
+        (100, 12, 1, "multiple of 8 for gf4"),
+        (8, 48, 1, "multiple of 32 for q8_0"),
+        (12, 512 + 32, 1, "multiple of 256 for q4_k"),
+        (100, 256, 0, "rows=0"),
+    ],
+)
+def test_quantize_rejects_bad_shapes(lib, type_id, k, rows, needle):
+    with pytest.raises(_ffi.Qw35Error, match=re.escape(needle)):
+        _ffi.call("qw35_hip_quantize", type_id, C.c_void_p(4096), rows, k, None, C.c_void_p(4096), None)
+
+
+def test_quantize_rejects_bad_pointers(lib):
+    with pytest.raises(_ffi.Qw35Error, match="null input"):
+        _ffi.call("qw35_hip_quantize", 100, None, 1, 256, None, C.c_void_p(4096), None)
+    with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
+        _ffi.call("qw35_hip_quantize", 100, C.c_void_p(4096), 1, 256, C.c_void_p(4100), C.c_void_p(4096), None)
