@@ -99,6 +99,20 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weig
 int qw35_hip_dequantize(const qw35_hip_weight *w, const uint32_t *row_ids, uint32_t n_rows, float *dst,
                         void *stream, char *err, uintptr_t err_len);
 
+/* Multi-token (prefill) matmul of a GF4 weight on bf16 MFMA:
+ *   c[t][r] = sum_k bf16_rne(awq[k] * a[t][k]) * W[r][k]    (awq == NULL: a[t][k] as bf16)
+ * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32
+ * (fp32 input is rounded to bf16 after the AWQ multiply); c: device
+ * [n_tokens][rows], c_dtype QW35_HIP_DTYPE_BF16 (round-to-nearest-even) or
+ * QW35_HIP_DTYPE_F32; fp32 accumulation.  Replaces encodeMatvecBatch /
+ * encodeTiledKMatmul for type 100 (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366,
+ * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255).  GF4 only;
+ * 1 <= n_tokens <= 65536. */
+#define QW35_HIP_DTYPE_F32 0u
+#define QW35_HIP_DTYPE_BF16 1u
+int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
+                            uint32_t c_dtype, uint32_t n_tokens, void *stream, char *err, uintptr_t err_len);
+
 /* Weight producer: fp32 src [rows][k] (device, 16-byte aligned) -> raw tensor
  * bytes of type_id in dst (device, 16-byte aligned, rows * row_bytes(type, k)
  * bytes).  col_scale (device fp32 [k], 16-byte aligned, nullable) multiplies

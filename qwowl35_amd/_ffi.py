@@ -16,6 +16,8 @@ TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
 TYPE_GF4 = 100
 MAX_BATCH = 8
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
 
 
 class TensorDesc(C.Structure):
@@ -63,6 +65,11 @@ PROTOTYPES: dict[str, tuple] = {
     "qw35_hip_dequantize": (
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_matmul_prefill": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
+         C.c_char_p, C.c_size_t],
     ),
     "qw35_hip_quantize": (
         C.c_int,

@@ -233,6 +233,38 @@ int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint3
                : 0;
 }
 
+int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
+                            uint32_t c_dtype, uint32_t n_tokens, void* stream, char* err, uintptr_t err_len) {
+    if (!check_weight(w, "matmul_prefill", err, err_len)) return 0;
+    if (w->type_id != qw35::kTypeGF4) {
+        set_err(err, err_len, "matmul_prefill: only GF4 (type 100) weights are supported, got %s",
+                type_name(w->type_id));
+        return 0;
+    }
+    if (a_dtype > QW35_HIP_DTYPE_BF16 || c_dtype > QW35_HIP_DTYPE_BF16) {
+        set_err(err, err_len, "matmul_prefill: a_dtype/c_dtype must be QW35_HIP_DTYPE_F32 or QW35_HIP_DTYPE_BF16");
+        return 0;
+    }
+    if (n_tokens < 1 || n_tokens > 65536) {
+        set_err(err, err_len, "matmul_prefill: n_tokens=%u must be in 1..65536", n_tokens);
+        return 0;
+    }
+    if (!a || !c) {
+        set_err(err, err_len, "matmul_prefill: null input or output");
+        return 0;
+    }
+    if (((uintptr_t)a & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)c & 3u)) {
+        set_err(err, err_len, "matmul_prefill: a/awq must be 16-byte aligned and c 4-byte aligned");
+        return 0;
+    }
+    return check_hip(qw35::launch_gf4_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
+                                              awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32,
+                                              static_cast<hipStream_t>(stream)),
+                     "matmul_prefill", err, err_len)
+               ? 1
+               : 0;
+}
+
 int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_t k, const float* col_scale,
                       void* dst, void* stream, char* err, uintptr_t err_len) {
     if (!type_supported(type_id)) {

@@ -41,9 +41,10 @@ hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, cons
 hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, const float* col_scale, void* dst,
                            hipStream_t stream);
 
-// GF4 prefill dequant-matmul on bf16 MFMA: C[m][n] = sum_k bf16(a_k * A[m][k]) * W[n][k].
-// out_f32 != 0 writes fp32, otherwise bf16 (RNE).
-hipError_t launch_gf4_prefill(const void* w, int rows, int k, const uint16_t* a_bf16, const float* awq,
-                              void* c, int m, int out_f32, hipStream_t stream);
+// GF4 prefill dequant-matmul on bf16 MFMA:
+//   C[m][n] = sum_k bf16_rne(awq[k] * A[m][k]) * W[n][k],  fp32 accumulation.
+// a: [m][k] bf16 (a_f32 == 0) or fp32; c: [m][rows] bf16 RNE (out_f32 == 0) or fp32.
+hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
+                              int m, int out_f32, hipStream_t stream);
 
 }  // namespace qw35

@@ -5,7 +5,8 @@ Names and argument meaning follow the reference runtime's encoders
 
 * ``decode_matvec``       <- ``encodeDecodeMatvecTensor:weight:input:inputOffset:dst:residual:`` (:184-256)
 * ``ffn_gate_up_swiglu``  <- ``encodeGf4FusedFfn`` / ``qw35_ffn_gate_up_swiglu_gf4_f32`` (:13-35)
-* ``matvec_batch``        <- ``encodeMatvecBatch`` for 1..8 tokens (:260-306)
+* ``matvec_batch``        <- ``encodeMatvecBatch`` (:260-306)
+* ``matmul_prefill``      <- ``encodeTiledKMatmul`` / ``qw35_mul_mm_gf4_f32`` (:309-366)
 * ``dequantize``          <- the per-codec dequant helpers / ``qw35_get_rows_*`` gathers
 * ``quantize``            <- ``pack_ffn_gf4`` / ``pack_gf4_prepared`` (tools/qw35_cook_common.py:83-119,182-199)
 
@@ -126,11 +127,46 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
     return dst
 
 
+def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = None,
+                   out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
+                   stream=None) -> torch.Tensor:
+    """``C[t] = bf16(awq * a[t]) @ W^T`` on bf16 MFMA for a GF4 weight (``encodeTiledKMatmul``).
+
+    ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
+    ``out_dtype`` (bfloat16, rounded to nearest even, or float32).
+    """
+    if a.dim() != 2 or not a.is_cuda or not a.is_contiguous() or a.dtype not in (torch.bfloat16, torch.float32):
+        raise Qw35Error("matmul_prefill: a must be a contiguous 2-D bf16/fp32 device tensor")
+    if a.shape[1] != w.k:
+        raise Qw35Error(f"matmul_prefill: a has {a.shape[1]} columns, weight k={w.k}")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise Qw35Error("matmul_prefill: out_dtype must be bfloat16 or float32")
+    n = int(a.shape[0])
+    if dst is None:
+        dst = torch.empty((n, w.rows), dtype=out_dtype, device=a.device)
+    elif dst.dtype != out_dtype or tuple(dst.shape) != (n, w.rows) or not dst.is_contiguous():
+        raise Qw35Error("matmul_prefill: dst must be a contiguous [n_tokens, rows] tensor of out_dtype")
+    a_dt = _ffi.DTYPE_BF16 if a.dtype == torch.bfloat16 else _ffi.DTYPE_F32
+    c_dt = _ffi.DTYPE_BF16 if out_dtype == torch.bfloat16 else _ffi.DTYPE_F32
+    _ffi.call("qw35_hip_matmul_prefill", C.byref(w.view), _ptr(a), a_dt, _ptr(awq), _ptr(dst), c_dt, n,
+              _stream(stream))
+    return dst
+
+
 def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-    """Multi-token matvec (``encodeMatvecBatch``) for 1..8 tokens of fp32 activations."""
-    if x.dim() != 2 or x.shape[0] > _ffi.MAX_BATCH:
-        raise Qw35Error("matvec_batch takes 1..8 tokens; use the prefill matmul for larger chunks")
-    return decode_matvec(w, x, dst, residual=False, stream=stream)
+    """Multi-token matvec of fp32 activations [n_tokens, k] (``encodeMatvecBatch``, +FFN.m:260-306).
+
+    1..8 tokens run the decode GEMV (fp32 activations); longer GF4 chunks run
+    the bf16-MFMA prefill matmul with fp32 output, as the reference switches
+    to its tiled matmul for multi-token chunks.
+    """
+    if x.dim() != 2:
+        raise Qw35Error("matvec_batch takes [n_tokens, k] activations")
+    if x.shape[0] <= _ffi.MAX_BATCH:
+        return decode_matvec(w, x, dst, residual=False, stream=stream)
+    if w.type_id != TYPE_GF4:
+        raise Qw35Error("matvec_batch: chunks of more than 8 tokens need a GF4 weight (prefill matmul)")
+    return matmul_prefill(w, x, out_dtype=torch.float32, dst=dst, stream=stream)
 
 
 def dequantize(w: HipWeight, row_ids: torch.Tensor | None = None, stream=None) -> torch.Tensor:
