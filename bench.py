@@ -12,9 +12,11 @@ Launches are captured into a hipGraph and replayed; HIP events on the replay
 stream bracket the timed replays.  Printed: one JSON line with the driver's
 contract fields plus ``roofline`` (dominant kernel) and ``cpu_baseline`` (the
 numpy oracle GF4 dequant + matvec on this host's cores), and under ``extra``
-the other decode configs: GF4 batches 2..8 and the transposed shape, the q8_0
-layer set (config 2) and the Q4_K down / LM-head GEMVs at batch 1 and 8
-(config 3).  ``--gpus`` above 1 is refused: this build measures one GPU.
+the other configs: GF4 batches 2..8 and the transposed shape, the q8_0 layer
+set (config 2), the Q4_K down / LM-head GEMVs at batch 1 and 8 (config 3), the
+GF4 prefill matmul with its MFMA utilisation (config 4) and the 32-layer 9B
+decode-step projection stack replayed as one recorded plan (config 5).
+``--gpus`` above 1 is refused: this build measures one GPU.
 """
 from __future__ import annotations
 
@@ -124,6 +126,98 @@ def read_traffic(kernel_hint: str):
     return int(m.group(1)), k.group(1)
 
 
+BF16_DENSE_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(b: Bench, rt, torch) -> dict:
+    """Config 4: GF4 prefill dequant-matmul, W 12288x4096 and 4096x12288 (12
+    rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out."""
+    out = {}
+    for rows, k in ((12288, 4096), (4096, 12288)):
+        ws = [b.weight(rt.TYPE_GF4, rows, k) for _ in range(12)]
+        awq = torch.rand((k,), generator=b.gen, device=b.dev) * 1.5 + 0.5
+        for m in (128, 512, 2048):
+            a = b.normal((m, k)).to(torch.bfloat16)
+            c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
+            calls = [lambda s, w=w: rt.matmul_prefill(w, a, awq=awq, dst=c, stream=s) for w in ws]
+            ms, _, _ = b.time_calls(calls, max(24, 4800 // m), 12)
+            tflops = 2.0 * m * rows * k / (ms * 1e-3) / 1e12
+            out[f"prefill_gf4_m{m}_{rows}x{k}"] = {
+                "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4)}
+        del ws
+    return out
+
+
+def bench_decode_stack(b: Bench, rt, torch) -> dict:
+    """Config 5: the 32-layer Qwen3.5-9B decode-step projection stack as one
+    recorded plan (hipGraph): per layer the q8_0 mixer projections (full
+    attention every 4th layer: q 8192, k 1024, v 1024, o 4096 rows; Gated
+    DeltaNet otherwise: qkv 8192, z 4096, beta 32, alpha 32, out 4096 rows; all
+    k = 4096), GF4 fused gate/up/SwiGLU (12288 x 4096) and GF4 down
+    (4096 x 12288, residual), then the Q4_K LM head (248320 x 4096).  Every
+    layer has its own weight buffers (5.2 GB per token)."""
+    hidden, ffn, vocab, layers = 4096, 12288, 248320, 32
+    src = {}
+
+    def layer_weight(t, rows, k):
+        key = (t, rows, k)
+        if key not in src:
+            src[key] = b.normal((rows, k), 0.02, bf16=(t == rt.TYPE_GF4))
+        return rt.quantize_weight(src[key], t)
+
+    stack = []
+    for il in range(layers):
+        if (il + 1) % 4 == 0:
+            mixer = [layer_weight(rt.TYPE_Q8_0, r, hidden) for r in (8192, 1024, 1024)]
+        else:
+            mixer = [layer_weight(rt.TYPE_Q8_0, r, hidden) for r in (8192, 4096, 32, 32)]
+        out_proj = layer_weight(rt.TYPE_Q8_0, hidden, hidden)
+        ffn_w = [layer_weight(rt.TYPE_GF4, ffn, hidden), layer_weight(rt.TYPE_GF4, ffn, hidden),
+                 layer_weight(rt.TYPE_GF4, hidden, ffn)]
+        stack.append((mixer, out_proj, ffn_w))
+    src.clear()
+    head = b.weight(rt.TYPE_Q4_K, vocab, hidden, tile_rows=16384)
+    total = sum(w.storage.numel() for mixer, o, f in stack for w in (*mixer, o, *f)) + head.storage.numel()
+    out = {}
+    for nb in (1, 8):
+        x = b.normal((nb, hidden))
+        att = b.normal((nb, hidden))
+        awq = torch.rand((hidden,), generator=b.gen, device=b.dev) * 1.5 + 0.5
+        h = torch.zeros((nb, hidden), dtype=torch.float32, device=b.dev)
+        g = torch.zeros((nb, ffn), dtype=torch.float32, device=b.dev)
+        proj = {r: torch.zeros((nb, r), dtype=torch.float32, device=b.dev) for r in (8192, 4096, 1024, 32)}
+        logits = torch.zeros((nb, vocab), dtype=torch.float32, device=b.dev)
+        plan = rt.DecodePlan()
+        for mixer, out_proj, (gate, up, down) in stack:
+            for w in mixer:
+                plan.matvec(w, x, proj[w.rows])
+            plan.matvec(out_proj, att, h, residual=True)
+            plan.swiglu(gate, up, x, g, awq=awq)
+            plan.matvec(down, g, h, residual=True)
+        plan.matvec(head, x, logits)
+        plan.record()
+        with torch.cuda.stream(b.stream):
+            for _ in range(3):
+                plan.launch(stream=b.stream)
+        torch.cuda.synchronize()
+        reps = 20
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(b.stream):
+            ev0.record(b.stream)
+            for _ in range(reps):
+                plan.launch(stream=b.stream)
+            ev1.record(b.stream)
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / reps
+        out[f"decode_stack_9b_b{nb}"] = {
+            "gemvs": len(plan), "weight_bytes": int(total), "us_per_step": round(us, 1),
+            "us_per_token": round(us / nb, 1), "GB/s": round(total / us / 1e3, 1)}
+        plan.close()
+    return out
+
+
 def cpu_baseline_gf4(rows: int, k: int, seed: int, reps: int):
     """numpy oracle on the host: GF4 dequant (vectorised numpy) + fp32 W @ x (BLAS)."""
     from threadpoolctl import threadpool_info
@@ -231,6 +325,9 @@ def main() -> int:
             extra[f"q4_k_head_b{nb}_248320x4096"] = {
                 "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 248320, 4096, nb, rt) / m / 1e6, 1)}
         del down, head
+
+        extra.update(bench_prefill(b, rt, torch))
+        extra.update(bench_decode_stack(b, rt, torch))
         for key, v in extra.items():
             log(f"{key}: {v}")
 

@@ -99,6 +99,37 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weig
 int qw35_hip_dequantize(const qw35_hip_weight *w, const uint32_t *row_ids, uint32_t n_rows, float *dst,
                         void *stream, char *err, uintptr_t err_len);
 
+/* Decode-step plan: a fixed sequence of projection GEMVs recorded once into a
+ * hipGraph and replayed per token.  Replaces the per-token recording of the
+ * projection dispatches in evalToken / encodeDecodeLayers
+ * (qw35-server/src/metal/bridge/Qw35MetalRuntime.m:807-880,1170-1221) and
+ * encodeGf4FusedFfn (Qw35MetalRuntime+FFN.m:13-35).  Every op reads and writes
+ * the device buffers named at create time, so callers refresh the inputs in
+ * place between launches.  The weights pointed to by an op are copied into the
+ * plan; the device memory they describe must outlive it. */
+#define QW35_HIP_OP_MATVEC 0u /* dst (+)= W (awq * x), see qw35_hip_decode_matvec */
+#define QW35_HIP_OP_SWIGLU 1u /* dst = silu(gate (awq*x)) * (up (awq*x)) */
+typedef struct {
+    uint32_t kind;               /* QW35_HIP_OP_* */
+    uint32_t n_batch;            /* 1..8 */
+    int32_t residual;            /* MATVEC only: nonzero adds into dst */
+    uint32_t reserved;
+    const qw35_hip_weight *w;    /* MATVEC weight or SWIGLU gate */
+    const qw35_hip_weight *w_up; /* SWIGLU up, else NULL */
+    const float *x;              /* device [n_batch][k] */
+    const float *awq;            /* device [k] or NULL */
+    float *dst;                  /* device [n_batch][rows] */
+} qw35_hip_plan_op;
+
+/* Validate the ops (same rules as the single calls) and record them; NULL on
+ * error.  Recording launches nothing. */
+void *qw35_hip_plan_create(const qw35_hip_plan_op *ops, uint32_t n_ops, char *err, uintptr_t err_len);
+/* Replay the recorded sequence on `stream` (asynchronous). */
+int qw35_hip_plan_launch(void *plan, void *stream, char *err, uintptr_t err_len);
+/* Number of ops recorded in the plan (0 for NULL). */
+uint32_t qw35_hip_plan_size(const void *plan);
+void qw35_hip_plan_destroy(void *plan);
+
 /* Multi-token (prefill) matmul of a GF4 weight on bf16 MFMA:
  *   c[t][r] = sum_k bf16_rne(awq[k] * a[t][k]) * W[r][k]    (awq == NULL: a[t][k] as bf16)
  * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32

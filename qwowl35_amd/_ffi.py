@@ -48,6 +48,26 @@ class Weight(C.Structure):
     ]
 
 
+OP_MATVEC = 0
+OP_SWIGLU = 1
+
+
+class PlanOp(C.Structure):
+    """``qw35_hip_plan_op``."""
+
+    _fields_ = [
+        ("kind", C.c_uint32),
+        ("n_batch", C.c_uint32),
+        ("residual", C.c_int32),
+        ("reserved", C.c_uint32),
+        ("w", C.POINTER(Weight)),
+        ("w_up", C.POINTER(Weight)),
+        ("x", C.c_void_p),
+        ("awq", C.c_void_p),
+        ("dst", C.c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/qw35_hip.h.
 PROTOTYPES: dict[str, tuple] = {
     "qw35_hip_has_device": (C.c_int, []),
@@ -66,6 +86,10 @@ PROTOTYPES: dict[str, tuple] = {
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
     ),
+    "qw35_hip_plan_create": (C.c_void_p, [C.POINTER(PlanOp), C.c_uint32, C.c_char_p, C.c_size_t]),
+    "qw35_hip_plan_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
+    "qw35_hip_plan_size": (C.c_uint32, [C.c_void_p]),
+    "qw35_hip_plan_destroy": (None, [C.c_void_p]),
     "qw35_hip_matmul_prefill": (
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
@@ -108,10 +132,10 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
 
 
 def call(name: str, *args) -> int:
-    """Call ``name(*args, err, err_len)`` and raise ``Qw35Error`` on a 0 return."""
+    """Call ``name(*args, err, err_len)`` and raise ``Qw35Error`` on a 0 / NULL return."""
     lib = load()
     err = C.create_string_buffer(512)
     rc = getattr(lib, name)(*args, err, C.sizeof(err))
-    if rc == 0:
+    if not rc:
         raise Qw35Error(f"{name}: {err.value.decode(errors='replace')}")
     return rc

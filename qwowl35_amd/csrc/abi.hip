@@ -93,6 +93,65 @@ hipError_t dispatch_gemv(uint32_t type_id, const qw35::GemvArgs& a, hipStream_t 
     }
 }
 
+bool check_matvec(const qw35_hip_weight* w, const float* x, const float* awq, const float* dst, uint32_t n_batch,
+                  const char* what, char* err, uintptr_t err_len) {
+    if (!check_weight(w, what, err, err_len)) return false;
+    if (!x || !dst) {
+        set_err(err, err_len, "%s: null input or output", what);
+        return false;
+    }
+    if (((uintptr_t)x & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)dst & 3u)) {
+        set_err(err, err_len, "%s: x/awq must be 16-byte aligned and dst 4-byte aligned", what);
+        return false;
+    }
+    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
+        set_err(err, err_len, "%s: n_batch=%u must be in 1..%u", what, n_batch, QW35_HIP_MAX_BATCH);
+        return false;
+    }
+    return true;
+}
+
+bool check_swiglu(const qw35_hip_weight* gate, const qw35_hip_weight* up, const float* x, const float* awq,
+                  const float* dst, uint32_t n_batch, const char* what, char* err, uintptr_t err_len) {
+    if (!check_matvec(gate, x, awq, dst, n_batch, what, err, err_len)) return false;
+    if (!check_weight(up, what, err, err_len)) return false;
+    if (gate->type_id != up->type_id || gate->k != up->k || gate->rows != up->rows) {
+        set_err(err, err_len, "%s: gate and up must share type and shape", what);
+        return false;
+    }
+    return true;
+}
+
+qw35::GemvArgs gemv_args(const qw35_hip_weight* w, const qw35_hip_weight* up, const float* x, const float* awq,
+                         float* dst, uint32_t n_batch, int residual) {
+    qw35::GemvArgs a{};
+    a.w = w->data;
+    a.w_up = up ? up->data : nullptr;
+    a.x = x;
+    a.awq = awq;
+    a.y = dst;
+    a.rows = (int)w->rows;
+    a.k = (int)w->k;
+    a.n_batch = (int)n_batch;
+    a.residual = residual ? 1 : 0;
+    return a;
+}
+
+// A recorded decode-step plan: the launches (their weight pointers, shapes and
+// buffers baked into the kernel arguments) held as an instantiated hipGraph.
+struct Plan {
+    uint32_t n_ops = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+void plan_free(Plan* p) {
+    if (!p) return;
+    if (p->exec) (void)hipGraphExecDestroy(p->exec);
+    if (p->graph) (void)hipGraphDestroy(p->graph);
+    delete p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -145,29 +204,8 @@ int qw35_hip_weight_view(const qw35_hip_tensor_desc* desc, const void* device_ba
 
 int qw35_hip_decode_matvec(const qw35_hip_weight* w, const float* x, const float* awq, float* dst,
                            uint32_t n_batch, int residual, void* stream, char* err, uintptr_t err_len) {
-    if (!check_weight(w, "decode_matvec", err, err_len)) return 0;
-    if (!x || !dst) {
-        set_err(err, err_len, "decode_matvec: null input or output");
-        return 0;
-    }
-    if (((uintptr_t)x & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)dst & 3u)) {
-        set_err(err, err_len, "decode_matvec: x/awq must be 16-byte aligned and dst 4-byte aligned");
-        return 0;
-    }
-    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
-        set_err(err, err_len, "decode_matvec: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);
-        return 0;
-    }
-    qw35::GemvArgs a{};
-    a.w = w->data;
-    a.x = x;
-    a.awq = awq;
-    a.y = dst;
-    a.w_up = nullptr;
-    a.rows = (int)w->rows;
-    a.k = (int)w->k;
-    a.n_batch = (int)n_batch;
-    a.residual = residual ? 1 : 0;
+    if (!check_matvec(w, x, awq, dst, n_batch, "decode_matvec", err, err_len)) return 0;
+    const qw35::GemvArgs a = gemv_args(w, nullptr, x, awq, dst, n_batch, residual);
     return check_hip(dispatch_gemv(w->type_id, a, static_cast<hipStream_t>(stream)), "decode_matvec", err, err_len)
                ? 1
                : 0;
@@ -176,39 +214,83 @@ int qw35_hip_decode_matvec(const qw35_hip_weight* w, const float* x, const float
 int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight* gate, const qw35_hip_weight* up, const float* x,
                                 const float* awq, float* dst, uint32_t n_batch, void* stream, char* err,
                                 uintptr_t err_len) {
-    if (!check_weight(gate, "ffn_gate_up_swiglu(gate)", err, err_len)) return 0;
-    if (!check_weight(up, "ffn_gate_up_swiglu(up)", err, err_len)) return 0;
-    if (gate->type_id != up->type_id || gate->k != up->k || gate->rows != up->rows) {
-        set_err(err, err_len, "ffn_gate_up_swiglu: gate and up must share type and shape");
-        return 0;
-    }
-    if (!x || !dst) {
-        set_err(err, err_len, "ffn_gate_up_swiglu: null input or output");
-        return 0;
-    }
-    if (((uintptr_t)x & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)dst & 3u)) {
-        set_err(err, err_len, "ffn_gate_up_swiglu: x/awq must be 16-byte aligned and dst 4-byte aligned");
-        return 0;
-    }
-    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
-        set_err(err, err_len, "ffn_gate_up_swiglu: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);
-        return 0;
-    }
-    qw35::GemvArgs a{};
-    a.w = gate->data;
-    a.w_up = up->data;
-    a.x = x;
-    a.awq = awq;
-    a.y = dst;
-    a.rows = (int)gate->rows;
-    a.k = (int)gate->k;
-    a.n_batch = (int)n_batch;
-    a.residual = 0;
+    if (!check_swiglu(gate, up, x, awq, dst, n_batch, "ffn_gate_up_swiglu", err, err_len)) return 0;
+    const qw35::GemvArgs a = gemv_args(gate, up, x, awq, dst, n_batch, 0);
     return check_hip(dispatch_gemv(gate->type_id, a, static_cast<hipStream_t>(stream)), "ffn_gate_up_swiglu", err,
                      err_len)
                ? 1
                : 0;
 }
+
+void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* err, uintptr_t err_len) {
+    if (!ops || n_ops == 0) {
+        set_err(err, err_len, "plan_create: no ops");
+        return nullptr;
+    }
+    char what[64];
+    for (uint32_t i = 0; i < n_ops; ++i) {
+        const qw35_hip_plan_op& o = ops[i];
+        snprintf(what, sizeof what, "plan_create: op %u", i);
+        if (o.kind == QW35_HIP_OP_MATVEC) {
+            if (o.w_up) {
+                set_err(err, err_len, "%s: a MATVEC op takes no w_up", what);
+                return nullptr;
+            }
+            if (!check_matvec(o.w, o.x, o.awq, o.dst, o.n_batch, what, err, err_len)) return nullptr;
+        } else if (o.kind == QW35_HIP_OP_SWIGLU) {
+            if (o.residual) {
+                set_err(err, err_len, "%s: a SWIGLU op has no residual form", what);
+                return nullptr;
+            }
+            if (!check_swiglu(o.w, o.w_up, o.x, o.awq, o.dst, o.n_batch, what, err, err_len)) return nullptr;
+        } else {
+            set_err(err, err_len, "%s: unknown kind %u", what, o.kind);
+            return nullptr;
+        }
+    }
+    Plan* plan = new Plan();
+    plan->n_ops = n_ops;
+    hipStream_t s = nullptr;
+    if (!check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "plan_create: stream", err, err_len)) {
+        plan_free(plan);
+        return nullptr;
+    }
+    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    hipError_t launch = hipSuccess;
+    if (e == hipSuccess) {
+        for (uint32_t i = 0; i < n_ops && launch == hipSuccess; ++i) {
+            const qw35_hip_plan_op& o = ops[i];
+            const bool sw = o.kind == QW35_HIP_OP_SWIGLU;
+            const qw35::GemvArgs a = gemv_args(o.w, sw ? o.w_up : nullptr, o.x, o.awq, o.dst, o.n_batch,
+                                               sw ? 0 : o.residual);
+            launch = dispatch_gemv(o.w->type_id, a, s);
+        }
+        e = hipStreamEndCapture(s, &plan->graph);
+    }
+    if (e == hipSuccess) e = launch;
+    if (e == hipSuccess) e = hipGraphInstantiate(&plan->exec, plan->graph, nullptr, nullptr, 0);
+    (void)hipStreamDestroy(s);
+    if (!check_hip(e, "plan_create: record", err, err_len)) {
+        plan_free(plan);
+        return nullptr;
+    }
+    return plan;
+}
+
+int qw35_hip_plan_launch(void* plan, void* stream, char* err, uintptr_t err_len) {
+    if (!plan) {
+        set_err(err, err_len, "plan_launch: null plan");
+        return 0;
+    }
+    return check_hip(hipGraphLaunch(static_cast<Plan*>(plan)->exec, static_cast<hipStream_t>(stream)),
+                     "plan_launch", err, err_len)
+               ? 1
+               : 0;
+}
+
+uint32_t qw35_hip_plan_size(const void* plan) { return plan ? static_cast<const Plan*>(plan)->n_ops : 0u; }
+
+void qw35_hip_plan_destroy(void* plan) { plan_free(static_cast<Plan*>(plan)); }
 
 int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint32_t n_rows, float* dst, void* stream,
                         char* err, uintptr_t err_len) {

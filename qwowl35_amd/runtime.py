@@ -8,6 +8,7 @@ Names and argument meaning follow the reference runtime's encoders
 * ``matvec_batch``        <- ``encodeMatvecBatch`` (:260-306)
 * ``matmul_prefill``      <- ``encodeTiledKMatmul`` / ``qw35_mul_mm_gf4_f32`` (:309-366)
 * ``dequantize``          <- the per-codec dequant helpers / ``qw35_get_rows_*`` gathers
+* ``DecodePlan``          <- the per-token recording of ``evalToken`` (Qw35MetalRuntime.m:807-880)
 * ``quantize``            <- ``pack_ffn_gf4`` / ``pack_gf4_prepared`` (tools/qw35_cook_common.py:83-119,182-199)
 
 Device memory and streams come from torch (plumbing only); every computation
@@ -205,6 +206,73 @@ def quantize_weight(src: torch.Tensor, type_id: int, col_scale: torch.Tensor | N
     """``quantize`` into a new HBM tensor, returned as a GEMV-ready ``HipWeight``."""
     raw = quantize(src, type_id, col_scale, stream)
     return HipWeight.from_device(raw, type_id, int(src.shape[0]), int(src.shape[1]))
+
+
+class DecodePlan:
+    """A per-token sequence of projection GEMVs recorded once into a hipGraph
+    (``qw35_hip_plan_*``), the counterpart of the per-token recording in
+    ``evalToken`` / ``encodeDecodeLayers`` (Qw35MetalRuntime.m:807-880,1170-1221).
+
+    Build with ``matvec`` / ``swiglu`` calls naming device buffers, then
+    ``record()``; ``launch()`` replays the whole sequence.  The tensors named in
+    the ops are referenced by the plan and must stay alive (and in place).
+    """
+
+    def __init__(self):
+        self._ops: list[_ffi.PlanOp] = []
+        self._keep: list = []
+        self._handle = None
+
+    def matvec(self, w: HipWeight, x: torch.Tensor, dst: torch.Tensor, residual: bool = False,
+               awq: torch.Tensor | None = None) -> "DecodePlan":
+        nb = _check_act(x, w.k, "x")
+        self._add(_ffi.OP_MATVEC, nb, residual, w, None, x, awq, dst)
+        return self
+
+    def swiglu(self, gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: torch.Tensor,
+               awq: torch.Tensor | None = None) -> "DecodePlan":
+        nb = _check_act(x, gate.k, "x")
+        self._add(_ffi.OP_SWIGLU, nb, False, gate, up, x, awq, dst)
+        return self
+
+    def _add(self, kind, nb, residual, w, up, x, awq, dst):
+        if self._handle is not None:
+            raise Qw35Error("plan already recorded")
+        op = _ffi.PlanOp()
+        op.kind = kind
+        op.n_batch = nb
+        op.residual = int(bool(residual))
+        op.w = C.pointer(w.view)
+        op.w_up = C.pointer(up.view) if up is not None else None
+        op.x = x.data_ptr()
+        op.awq = awq.data_ptr() if awq is not None else None
+        op.dst = dst.data_ptr()
+        self._ops.append(op)
+        self._keep.extend([w, up, x, awq, dst])
+
+    def record(self) -> "DecodePlan":
+        arr = (_ffi.PlanOp * len(self._ops))(*self._ops)
+        self._handle = C.c_void_p(_ffi.call("qw35_hip_plan_create", arr, len(self._ops)))
+        return self
+
+    def __len__(self) -> int:
+        return int(_ffi.load().qw35_hip_plan_size(self._handle)) if self._handle else len(self._ops)
+
+    def launch(self, stream=None) -> None:
+        if self._handle is None:
+            raise Qw35Error("plan_launch: plan not recorded")
+        _ffi.call("qw35_hip_plan_launch", self._handle, _stream(stream))
+
+    def close(self) -> None:
+        if self._handle is not None:
+            _ffi.load().qw35_hip_plan_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def sync(stream=None) -> None:

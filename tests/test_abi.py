@@ -157,3 +157,49 @@ def test_quantize_rejects_bad_pointers(lib):
         _ffi.call("qw35_hip_quantize", 100, None, 1, 256, None, C.c_void_p(4096), None)
     with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
         _ffi.call("qw35_hip_quantize", 100, C.c_void_p(4096), 1, 256, C.c_void_p(4100), C.c_void_p(4096), None)
+
+
+def _plan_op(kind=0, w=None, up=None, x=4096, dst=4096, nb=1, residual=0):
+    op = _ffi.PlanOp()
+    op.kind = kind
+    op.n_batch = nb
+    op.residual = residual
+    op.w = C.pointer(w) if w is not None else None
+    op.w_up = C.pointer(up) if up is not None else None
+    op.x = x
+    op.awq = None
+    op.dst = dst
+    return op
+
+
+@pytest.mark.parametrize(
+    "ops,needle",
+    [
+        ([], "no ops"),
+        ([dict(kind=7)], "op 0: unknown kind 7"),
+        ([dict(), dict(nb=9)], "op 1: n_batch=9"),
+        ([dict(), dict(wkw=dict(type_id=14))], "op 1: unsupported tensor type 14"),
+        ([dict(kind=0, up=True)], "op 0: a MATVEC op takes no w_up"),
+        ([dict(kind=1, up=True, residual=1)], "op 0: a SWIGLU op has no residual form"),
+        ([dict(kind=1, up=True, upkw=dict(k=8192))], "op 0: gate and up must share type and shape"),
+        ([dict(x=0)], "op 0: null input"),
+    ],
+)
+def test_plan_create_validates_every_op(lib, ops, needle):
+    built, keep = [], []
+    for o in ops:
+        w = _weight(**o.get("wkw", {}))
+        up = _weight(**o.get("upkw", {})) if o.get("up") else None
+        keep += [w, up]
+        built.append(_plan_op(kind=o.get("kind", 0), w=w, up=up, x=o.get("x", 4096), nb=o.get("nb", 1),
+                              residual=o.get("residual", 0)))
+    arr = (_ffi.PlanOp * max(1, len(built)))(*built)
+    with pytest.raises(_ffi.Qw35Error, match=re.escape(needle)):
+        _ffi.call("qw35_hip_plan_create", arr if built else None, len(built))
+
+
+def test_plan_null_handles(lib):
+    assert lib.qw35_hip_plan_size(None) == 0
+    lib.qw35_hip_plan_destroy(None)
+    with pytest.raises(_ffi.Qw35Error, match="null plan"):
+        _ffi.call("qw35_hip_plan_launch", None, None)
