@@ -1,0 +1,436 @@
+// q8_0 and Q4_K decode GEMV / fused gate-up-SwiGLU for gfx950, batch 1..8, on MFMA.
+//
+//   y[b][r] (+)= sum_k W[r][k] * a[k] * x[b][k]
+//
+// Reference kernels replaced:
+//   qw35_decode_matmul_q8_0{,_residual}_f32      (qw35-server/src/metal/qw35_matvec.metal:630-683)
+//   qw35_decode_matmul_q4_k_2row{,_residual}_f32 (qw35-server/src/metal/qw35_matvec.metal:171-353)
+//
+// Same structure as the GF4 kernel: a workgroup covers 16*RT rows with KS
+// waves splitting K into 256-column chunks; raw tensor bytes arrive as
+// coalesced 16-byte segments, pass through a per-wave LDS transpose, and each
+// lane then reads the bytes of its MFMA operand.  v_mfma_f32_16x16x32_f16:
+//   * B (weights): lane l holds 8 consecutive k of weight row n = l % 16 of one
+//     32-element block, as exact fp16 integers (q8_0: int8; Q4_K: 4-bit q);
+//   * A (activations): row 2b = fp16 hi, row 2b+1 = fp16 lo of awq*x of batch
+//     row b, scaled per chunk by a power of two (max |v| in [2^13, 2^14));
+//   * one MFMA per 32-element block with a zero accumulator gives the 16x16
+//     block partial; the block's scales are applied to it in fp32:
+//       q8_0 (qw35_types.metal:24-36):  y += d * sum q x
+//       Q4_K (qw35_matvec.metal:2-38):   y += d*sc_j * sum q x - dmin*m_j * sum x
+//     with the chunk's inverse activation scale folded into the same multiply.
+//
+// Byte -> fp16 integer decode (exact, integers below 2048):
+//   int8 q:   perm into 0x64XX halves after flipping the sign bit -> 1152 + q,
+//             then one v_pk_add_f16 of -1152;
+//   nibble q: mask (and shift) -> 0x64XX halves -> 1024 + q, v_pk_add_f16 of -1024.
+#include "qw35_device.h"
+#include "qw35_kernels.h"
+
+#include <type_traits>
+
+namespace qw35 {
+namespace {
+
+constexpr int kFmtQ8 = 0;
+constexpr int kFmtQ4K = 1;
+
+template <int FMT>
+struct Fmt;
+template <>
+struct Fmt<kFmtQ8> {
+    static constexpr int kChunkBytes = 272;  // 8 blocks of 34 bytes = 256 columns
+    static constexpr int kSegs = 17;         // 16-byte segments per row chunk
+    static constexpr int kStride = 288;      // LDS bytes per transposed row (16-byte pad)
+    static constexpr int kTypeId = 8;
+};
+template <>
+struct Fmt<kFmtQ4K> {
+    static constexpr int kChunkBytes = 144;  // one super-block = 256 columns
+    static constexpr int kSegs = 9;
+    static constexpr int kStride = 160;
+    static constexpr int kTypeId = 12;
+};
+
+__device__ __forceinline__ half2_t h2(float lo, float hi) {
+    half2_t r;
+    r.x = (_Float16)lo;
+    r.y = (_Float16)hi;
+    return r;
+}
+
+template <int N>
+__device__ __forceinline__ void kq_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int N, typename F>
+__device__ __forceinline__ void kq_static_for(F&& f) {
+    if constexpr (N > 0) {
+        kq_static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 4 signed bytes -> 2 fp16 pairs (q0,q1), (q2,q3), exact.
+__device__ __forceinline__ void s8x4_to_h(uint32_t w, const half2_t bias, uint32_t& p0, uint32_t& p1) {
+    const uint32_t t = w ^ 0x80808080u;
+    p0 = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, t, 0x04010400u)) + bias);
+    p1 = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, t, 0x04030402u)) + bias);
+}
+
+// 4 nibbles (one per byte, already masked) -> 2 fp16 pairs, exact.
+__device__ __forceinline__ void u4x4_to_h(uint32_t t, const half2_t bias, uint32_t& p0, uint32_t& p1) {
+    p0 = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, t, 0x04010400u)) + bias);
+    p1 = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, t, 0x04030402u)) + bias);
+}
+
+typedef uint32_t uint2_t_ __attribute__((ext_vector_type(2)));
+
+// Per-wave LDS block: one transpose buffer (16 rows of a chunk), one activation
+// buffer (2*NB rows x 264 halves: one chunk, fp16 hi/lo), a zero row, and
+// (Q4_K) the per-sub-block sums of the scaled activations [NB][8].  A wave's
+// LDS operations complete in order, so one buffer of each suffices.
+template <int FMT, int NB>
+struct KqLds {
+    static constexpr int kXpose = 16 * Fmt<FMT>::kStride;
+    static constexpr int kActStride = 264;  // halves per activation row
+    static constexpr int kAct = 2 * NB * kActStride * 2;
+    static constexpr int kSx = FMT == kFmtQ4K ? NB * 8 * 4 : 0;
+    static constexpr int kXposeOff = 0;
+    static constexpr int kActOff = kXpose;
+    static constexpr int kZeroOff = kActOff + kAct;
+    static constexpr int kSxOff = kZeroOff + 128;
+    static constexpr int kBytes = kSxOff + kSx;
+};
+
+// Wave w owns chunks [w*CPW, (w+1)*CPW) of all RT row tiles.  Loads run P
+// chunks ahead: chunk c's activations and weight segments are issued (in that
+// order) when chunk c-P has been consumed, into register slot c % P.
+template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU, bool HAS_AWQ>
+__global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    using F = Fmt<FMT>;
+    using L = KqLds<FMT, NB>;
+    constexpr int NM = SWIGLU ? 2 : 1;
+    constexpr int LPT = (16 * F::kSegs + 63) / 64;  // 16-byte weight loads per lane per tile
+    constexpr int WPC = RT * NM * LPT;                // weight loads per chunk
+    constexpr int LPC = NB + (HAS_AWQ ? 1 : 0) + WPC; // loads per chunk
+    static_assert(P >= 1 && P <= CPW && P * LPC <= 60, "vmcnt budget");
+    const int k = args.k;
+    const int rows = args.rows;
+    const int n_batch = args.n_batch;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 15;
+    const int kq = lane >> 4;
+    const int row0 = blockIdx.x * 16 * RT;
+    const int chunks = k >> 8;
+    const size_t row_bytes = (size_t)chunks * F::kChunkBytes;
+
+    uint8_t* wblk = smem + (size_t)wave * L::kBytes;
+    float* part = reinterpret_cast<float*>(smem + (size_t)KS * L::kBytes);  // [KS][RT][NM][NB][16]
+    if (lane < 32) reinterpret_cast<uint32_t*>(wblk + L::kZeroOff)[lane] = 0u;
+    _Float16* xs = reinterpret_cast<_Float16*>(wblk + L::kActOff);
+    float* sx = reinterpret_cast<float*>(wblk + L::kSxOff);
+    uint8_t* xb = wblk + L::kXposeOff;
+
+    // Register slots of the P chunks in flight.
+    float4_t xv[P][NB];
+    float4_t av[P];
+    uint4_t wv[P][RT * NM][LPT];
+
+    auto issue = [&](auto CI) {
+        constexpr int c = decltype(CI)::value;
+        constexpr int sl = c % P;
+        int chunk = wave * CPW + c;
+        chunk = chunk < chunks ? chunk : 0;
+        const int col = chunk * 256 + 4 * lane;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int bb = b < n_batch ? b : 0;
+            xv[sl][b] = *reinterpret_cast<const float4_t*>(args.x + (size_t)bb * k + col);
+        }
+        if (HAS_AWQ) av[sl] = *reinterpret_cast<const float4_t*>(args.awq + col);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? args.w : args.w_up);
+#pragma unroll
+                for (int i = 0; i < LPT; ++i) {
+                    int s = lane + 64 * i;
+                    s = s < 16 * F::kSegs ? s : 0;
+                    int r = row0 + 16 * t + s / F::kSegs;
+                    r = r < rows ? r : rows - 1;
+                    wv[sl][t * NM + m][i] = load_stream16(
+                        wbase + (size_t)r * row_bytes + (size_t)chunk * F::kChunkBytes + 16 * (s % F::kSegs));
+                }
+            }
+        }
+    };
+
+    kq_static_for<P>([&](auto CI) { issue(CI); });
+
+    const half2_t bias = FMT == kFmtQ8 ? h2(-1152.0f, -1152.0f) : h2(-1024.0f, -1024.0f);
+    float acc[RT][NM][2];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[t][m][0] = acc[t][m][1] = 0.0f;
+
+    kq_static_for<CPW>([&](auto CI) {
+        constexpr int c = decltype(CI)::value;
+        constexpr int sl = c % P;
+        constexpr int later = (CPW - 1 - c) < (P - 1) ? (CPW - 1 - c) : (P - 1);  // chunks issued after c
+        kq_wait_vmcnt<later * LPC>();
+        const bool live = wave * CPW + c < chunks;
+        if (live) {
+            // Stage chunk c's activations: fp16 hi/lo with a per-chunk power-of-two scale.
+            float isc[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                float4_t v = xv[sl][b];
+                if (HAS_AWQ) v *= av[sl];
+                const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+                const float sc = fp16_range_scale(wave_max_abs(mx));
+                isc[b] = 1.0f / sc;
+                v *= sc;
+                const half2_t hi0 = h2(v[0], v[1]);
+                const half2_t hi1 = h2(v[2], v[3]);
+                const half2_t lo0 = h2(v[0] - (float)hi0.x, v[1] - (float)hi0.y);
+                const half2_t lo1 = h2(v[2] - (float)hi1.x, v[3] - (float)hi1.y);
+                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + 4 * lane) =
+                    uint2_t_{as_u32(hi0), as_u32(hi1)};
+                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + 4 * lane) =
+                    uint2_t_{as_u32(lo0), as_u32(lo1)};
+                if constexpr (FMT == kFmtQ4K) {
+                    // sum of the scaled activations of each 32-column sub-block (8 lanes)
+                    float s4 = (v[0] + v[1]) + (v[2] + v[3]);
+                    s4 += dpp_f32<kDppQuadXor1>(s4);
+                    s4 += dpp_f32<kDppQuadXor2>(s4);
+                    s4 += dpp_f32<kDppRowHalfMirror>(s4);
+                    if ((lane & 7) == 7) sx[b * 8 + (lane >> 3)] = s4;
+                }
+            }
+            float inv_sc[2];  // batches 2kq and 2kq+1
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                float v = 1.0f;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    if (b == 2 * kq + jj) v = isc[b];
+                inv_sc[jj] = v;
+            }
+            const bool a_live = n < 2 * n_batch;
+            const _Float16* arow =
+                a_live ? xs + (size_t)n * L::kActStride : reinterpret_cast<const _Float16*>(wblk + L::kZeroOff);
+            const int a_step = a_live ? 32 : 0;
+
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    // Transpose tile t of matrix m through LDS.
+#pragma unroll
+                    for (int q = 0; q < LPT; ++q) {
+                        const int s = lane + 64 * q;
+                        if (s < 16 * F::kSegs)
+                            *reinterpret_cast<uint4_t*>(xb + (s / F::kSegs) * F::kStride + 16 * (s % F::kSegs)) =
+                                wv[sl][t * NM + m][q];
+                    }
+                    wave_sync_lds();
+                    const uint8_t* wrow = xb + n * F::kStride;
+                    if constexpr (FMT == kFmtQ8) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            // qs bytes [2 + 8 kq, +8) of block j: 4-byte aligned for odd j, 2 mod 4 for even j
+                            const int off = 34 * j + 2 + 8 * kq;
+                            uint32_t d0, d1;
+                            if ((j & 1) == 1) {
+                                d0 = *reinterpret_cast<const uint32_t*>(wrow + off);
+                                d1 = *reinterpret_cast<const uint32_t*>(wrow + off + 4);
+                            } else {
+                                const uint32_t* base = reinterpret_cast<const uint32_t*>(wrow + off - 2);
+                                const uint32_t e0 = base[0], e1 = base[1], e2 = base[2];
+                                d0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
+                                d1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
+                            }
+                            const float dsc = (float)*reinterpret_cast<const _Float16*>(wrow + 34 * j);
+                            uint32_t b4[4];
+                            s8x4_to_h(d0, bias, b4[0], b4[1]);
+                            s8x4_to_h(d1, bias, b4[2], b4[3]);
+                            const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
+                            const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
+                            const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
+                            acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
+                        }
+                    } else {
+                        const uint4_t hd = *reinterpret_cast<const uint4_t*>(wrow);
+                        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)hd.x);
+                        const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x >> 16));
+                        // 6-bit scales and mins of the 8 sub-blocks, one per byte (get_scale_min_k4).
+                        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu;
+                        const uint32_t mn_lo = hd.z & 0x3F3F3F3Fu;
+                        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+                        const uint32_t mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                        // batches past NB read row NB-1 (their results are never stored)
+                        const int b0 = min(2 * kq, NB - 1), b1 = min(2 * kq + 1, NB - 1);
+                        const float4_t sxa = *reinterpret_cast<const float4_t*>(sx + b0 * 8);
+                        const float4_t sxb = *reinterpret_cast<const float4_t*>(sx + b0 * 8 + 4);
+                        const float4_t sxc = *reinterpret_cast<const float4_t*>(sx + b1 * 8);
+                        const float4_t sxd = *reinterpret_cast<const float4_t*>(sx + b1 * 8 + 4);
+                        const float sx0[8] = {sxa[0], sxa[1], sxa[2], sxa[3], sxb[0], sxb[1], sxb[2], sxb[3]};
+                        const float sx1[8] = {sxc[0], sxc[1], sxc[2], sxc[3], sxd[0], sxd[1], sxd[2], sxd[3]};
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc) {
+                            const uint2_t_ qd = *reinterpret_cast<const uint2_t_*>(wrow + 16 + 32 * cc + 8 * kq);
+#pragma unroll
+                            for (int hi = 0; hi < 2; ++hi) {
+                                const int j = 2 * cc + hi;
+                                const uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
+                                const uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
+                                uint32_t b4[4];
+                                u4x4_to_h(t0, bias, b4[0], b4[1]);
+                                u4x4_to_h(t1, bias, b4[2], b4[3]);
+                                const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
+                                const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
+                                const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                                const uint32_t scw = j < 4 ? sc_lo : sc_hi;
+                                const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
+                                const float scj = (float)((scw >> (8 * (j & 3))) & 0xFFu);
+                                const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
+                                const float ds = d * scj;
+                                const float dm = dmin * mnj;
+                                const float v0 = __builtin_fmaf(-dm, sx0[j], ds * (dd[0] + dd[1]));
+                                const float v1 = __builtin_fmaf(-dm, sx1[j], ds * (dd[2] + dd[3]));
+                                acc[t][m][0] = __builtin_fmaf(inv_sc[0], v0, acc[t][m][0]);
+                                acc[t][m][1] = __builtin_fmaf(inv_sc[1], v1, acc[t][m][1]);
+                            }
+                        }
+                    }
+                    // The next tile (or chunk) rewrites the transpose and activation buffers.
+                    wave_sync_lds();
+                }
+            }
+        }
+        if constexpr (c + P < CPW) issue(std::integral_constant<int, c + P>{});
+    });
+
+    // Partials of the KS waves meet in LDS; lane group kq holds batches 2kq, 2kq+1.
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int b = 2 * kq + jj;
+                if (b < NB) part[(((wave * RT + t) * NM + m) * NB + b) * 16 + n] = acc[t][m][jj];
+            }
+    __syncthreads();
+    for (int o = threadIdx.x; o < RT * NB * 16; o += 64 * KS) {
+        const int t = o / (NB * 16);
+        const int b = (o / 16) % NB;
+        const int nn = o & 15;
+        const int r = row0 + 16 * t + nn;
+        float tot[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < KS; ++w) sum += part[(((w * RT + t) * NM + m) * NB + b) * 16 + nn];
+            tot[m] = sum;
+        }
+        if (r < rows && b < n_batch) {
+            float* yp = args.y + (size_t)b * rows + r;
+            float v = SWIGLU ? silu(tot[0]) * tot[NM - 1] : tot[0];
+            if (args.residual) v += *yp;
+            *yp = v;
+        }
+    }
+}
+
+struct KqPlan {
+    int rt, ks, cpw, p;
+};
+
+// KS waves x CPW chunks cover k, P chunks in flight per wave; RT row tiles
+// per workgroup for tall matrices (the LM head).
+KqPlan plan_kq(int rows, int k) {
+    const int chunks = k >> 8;
+    const int tiles = (rows + 15) / 16;
+    if (chunks <= 4) return {1, 4, 1, 1};
+    if (chunks <= 8) return {1, 8, 1, 1};
+    if (chunks <= 16) return {tiles >= 1024 ? 2 : 1, 8, 2, 2};
+    if (chunks <= 32) return {1, 8, 4, 3};
+    return {1, 8, 6, 3};
+}
+
+template <int FMT, int NB, int RT, int KS, int CPW, bool SWIGLU>
+size_t kq_lds_bytes() {
+    constexpr int NM = SWIGLU ? 2 : 1;
+    return (size_t)KS * KqLds<FMT, NB>::kBytes + (size_t)KS * RT * NM * NB * 16 * 4;
+}
+
+template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU>
+hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
+    const size_t lds = kq_lds_bytes<FMT, NB, RT, KS, CPW, SWIGLU>();
+    if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+    const int grid = (a.rows + 16 * RT - 1) / (16 * RT);
+    if (a.awq)
+        hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds,
+                           stream, a);
+    else
+        hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, false>), dim3(grid), dim3(64 * KS), lds,
+                           stream, a);
+    return hipGetLastError();
+}
+
+template <int FMT, int NB, bool SWIGLU>
+hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
+    KqPlan p = plan_kq(a.rows, a.k);
+    if (SWIGLU && p.p > 2) p.p = 2;  // two matrices per chunk: two chunks in flight
+#define QW35_KQ_PLAN(RT, KS, CPW, P)                        \
+    if (p.rt == RT && p.ks == KS && p.cpw == CPW && p.p == P) \
+        return kq_launch_cfg<FMT, NB, RT, KS, CPW, P, SWIGLU>(a, stream);
+    QW35_KQ_PLAN(1, 4, 1, 1)
+    QW35_KQ_PLAN(1, 8, 1, 1)
+    QW35_KQ_PLAN(1, 8, 2, 2)
+    QW35_KQ_PLAN(2, 8, 2, 2)
+    QW35_KQ_PLAN(1, 8, 4, 3)
+    QW35_KQ_PLAN(1, 8, 6, 3)
+    QW35_KQ_PLAN(1, 8, 4, 2)
+    QW35_KQ_PLAN(1, 8, 6, 2)
+#undef QW35_KQ_PLAN
+    return hipErrorInvalidValue;
+}
+
+template <int FMT, bool SWIGLU>
+hipError_t kq_launch_any(const GemvArgs& a, hipStream_t stream) {
+    if (a.n_batch == 1) return kq_launch_nb<FMT, 1, SWIGLU>(a, stream);
+    if (a.n_batch == 2) return kq_launch_nb<FMT, 2, SWIGLU>(a, stream);
+    if (a.n_batch <= 4) return kq_launch_nb<FMT, 4, SWIGLU>(a, stream);
+    return kq_launch_nb<FMT, 8, SWIGLU>(a, stream);
+}
+
+}  // namespace
+
+hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? kq_launch_any<kFmtQ8, true>(a, stream) : kq_launch_any<kFmtQ8, false>(a, stream);
+}
+
+hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? kq_launch_any<kFmtQ4K, true>(a, stream) : kq_launch_any<kFmtQ4K, false>(a, stream);
+}
+
+}  // namespace qw35
