@@ -186,12 +186,14 @@ def bench_decode_stack(b: Bench, rt, torch) -> dict:
         awq = torch.rand((hidden,), generator=b.gen, device=b.dev) * 1.5 + 0.5
         h = torch.zeros((nb, hidden), dtype=torch.float32, device=b.dev)
         g = torch.zeros((nb, ffn), dtype=torch.float32, device=b.dev)
-        proj = {r: torch.zeros((nb, r), dtype=torch.float32, device=b.dev) for r in (8192, 4096, 1024, 32)}
+        att_out = [torch.zeros((nb, r), dtype=torch.float32, device=b.dev) for r in (8192, 1024, 1024)]
+        delta_out = [torch.zeros((nb, r), dtype=torch.float32, device=b.dev) for r in (8192, 4096, 32, 32)]
         logits = torch.zeros((nb, vocab), dtype=torch.float32, device=b.dev)
         plan = rt.DecodePlan()
         for mixer, out_proj, (gate, up, down) in stack:
-            for w in mixer:
-                plan.matvec(w, x, proj[w.rows])
+            outs = att_out if len(mixer) == 3 else delta_out  # q/k/v or qkv/z/beta/alpha
+            for w, o in zip(mixer, outs):
+                plan.matvec(w, x, o)
             plan.matvec(out_proj, att, h, residual=True)
             plan.swiglu(gate, up, x, g, awq=awq)
             plan.matvec(down, g, h, residual=True)

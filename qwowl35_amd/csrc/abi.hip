@@ -137,6 +137,24 @@ qw35::GemvArgs gemv_args(const qw35_hip_weight* w, const qw35_hip_weight* up, co
     return a;
 }
 
+// Two plan ops can share one launch: both matvecs of the same k-quant type and
+// k over the same activations, batch and AWQ, with the same residual flag,
+// writing disjoint outputs that neither reads.
+bool overlaps(const void* p, uint64_t pn, const void* q, uint64_t qn) {
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return a < b + qn && b < a + pn;
+}
+
+bool mergeable(const qw35_hip_plan_op& a, const qw35_hip_plan_op& b) {
+    if (a.kind != QW35_HIP_OP_MATVEC || b.kind != QW35_HIP_OP_MATVEC) return false;
+    if (b.w->type_id != a.w->type_id || b.w->k != a.w->k || b.x != a.x || b.awq != a.awq ||
+        b.n_batch != a.n_batch || (b.residual != 0) != (a.residual != 0))
+        return false;
+    const uint64_t xa = (uint64_t)a.n_batch * a.w->k * 4;
+    const uint64_t da = (uint64_t)a.n_batch * a.w->rows * 4, db = (uint64_t)b.n_batch * b.w->rows * 4;
+    return !overlaps(a.dst, da, b.dst, db) && !overlaps(a.x, xa, a.dst, da) && !overlaps(a.x, xa, b.dst, db);
+}
+
 // A recorded decode-step plan: the launches (their weight pointers, shapes and
 // buffers baked into the kernel arguments) held as an instantiated hipGraph.
 struct Plan {
@@ -258,12 +276,31 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
     hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
     hipError_t launch = hipSuccess;
     if (e == hipSuccess) {
-        for (uint32_t i = 0; i < n_ops && launch == hipSuccess; ++i) {
+        for (uint32_t i = 0; i < n_ops && launch == hipSuccess;) {
             const qw35_hip_plan_op& o = ops[i];
             const bool sw = o.kind == QW35_HIP_OP_SWIGLU;
-            const qw35::GemvArgs a = gemv_args(o.w, sw ? o.w_up : nullptr, o.x, o.awq, o.dst, o.n_batch,
-                                               sw ? 0 : o.residual);
+            qw35::GemvArgs a = gemv_args(o.w, sw ? o.w_up : nullptr, o.x, o.awq, o.dst, o.n_batch,
+                                         sw ? 0 : o.residual);
+            // Consecutive q8_0 / Q4_K matvecs over the same activations share one launch.
+            uint32_t j = i + 1;
+            if (!sw && o.w->type_id != qw35::kTypeGF4) {
+                while (j < n_ops && j - i < (uint32_t)qw35::kMaxSegments) {
+                    bool ok = true;
+                    for (uint32_t q = i; q < j && ok; ++q) ok = mergeable(ops[q], ops[j]);
+                    if (!ok) break;
+                    ++j;
+                }
+            }
+            if (j - i > 1) {
+                a.n_seg = (int)(j - i);
+                for (uint32_t q = i; q < j; ++q) {
+                    a.seg_w[q - i] = ops[q].w->data;
+                    a.seg_y[q - i] = ops[q].dst;
+                    a.seg_rows[q - i] = (int)ops[q].w->rows;
+                }
+            }
             launch = dispatch_gemv(o.w->type_id, a, s);
+            i = j;
         }
         e = hipStreamEndCapture(s, &plan->graph);
     }

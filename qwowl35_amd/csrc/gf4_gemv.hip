@@ -37,6 +37,7 @@
 // Every x load is issued before the weight loads, so waiting for x never waits
 // on the weight stream (vector loads complete in order); the weights are then
 // consumed in issue order as they arrive.
+#include "gf4_decode.h"
 #include "qw35_device.h"
 #include "qw35_kernels.h"
 
@@ -44,73 +45,6 @@
 
 namespace qw35 {
 namespace {
-
-constexpr uint32_t kFlip = 0x92492400u;
-constexpr uint32_t kMaskA = 0x00070070u;
-constexpr uint32_t kMaskB = 0x00380380u;
-constexpr uint32_t kMagicA = 0x64005400u;
-constexpr uint32_t kMagicB = 0x58004800u;
-
-__device__ __forceinline__ half2_t h2(float lo, float hi) {
-    half2_t r;
-    r.x = (_Float16)lo;
-    r.y = (_Float16)hi;
-    return r;
-}
-
-// Loop-invariant operands of the decode, held in VGPRs so that the VOP3 forms
-// (v_bitop3_b32, v_pk_fma_f16) take them without literals.
-struct Gf4Consts {
-    uint32_t mask_a, mask_b, magic_a, magic_b;
-    half2_t quarter_neg, off_a, off_b;
-};
-
-// (t & mask) ^ magic' = ((t ^ flip) & mask) | magic: the code flip q = c ^ 4
-// (bit 2 of every field) is folded into the magic constants.
-constexpr uint32_t kMagicFlipA = kMagicA ^ ((kFlip >> 4) & kMaskA);  // == ((kFlip >> 10) & kMaskA) ^ kMagicA
-constexpr uint32_t kMagicFlipB = kMagicB ^ ((kFlip >> 4) & kMaskB);
-static_assert(((kFlip >> 4) & kMaskA) == ((kFlip >> 10) & kMaskA), "flip bits agree for both shifts");
-static_assert(((kFlip >> 4) & kMaskB) == ((kFlip >> 10) & kMaskB), "flip bits agree for both shifts");
-
-__device__ __forceinline__ Gf4Consts gf4_consts() {
-    Gf4Consts c;
-    c.mask_a = kMaskA;
-    c.mask_b = kMaskB;
-    c.magic_a = kMagicFlipA;
-    c.magic_b = kMagicFlipB;
-    c.quarter_neg = h2(-0.25f, -0.25f);
-    c.off_a = h2(68.0f / 4.0f, 1028.0f / 4.0f);
-    c.off_b = h2(12.0f / 4.0f, 132.0f / 4.0f);
-    return c;
-}
-
-// v_bitop3_b32 with truth table 0x6a: (a & b) ^ c.
-__device__ __forceinline__ uint32_t and_xor(uint32_t a, uint32_t mask, uint32_t bits) {
-    uint32_t r;
-    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
-    return r;
-}
-
-// One GF4 word -> MFMA B operand: 8 exact fp16 weights in column order
-// 0,4,1,5,2,6,3,7 (15 VALU ops).
-//   E_j = P_j * (-1/4) + (base + 4)/4 = (4 - q)/4   (exact)
-//   B_j = E_j * s                                   (exact, |B| <= |s|)
-__device__ __forceinline__ half8_t gf4_word_to_b(uint32_t w, const Gf4Consts& c) {
-    const uint32_t t1 = w >> 4;
-    const uint32_t t2 = w >> 10;
-    const half2_t p0 = as_half2(and_xor(t1, c.mask_a, c.magic_a));
-    const half2_t p1 = as_half2(and_xor(t1, c.mask_b, c.magic_b));
-    const half2_t p2 = as_half2(and_xor(t2, c.mask_a, c.magic_a));
-    const half2_t p3 = as_half2(and_xor(t2, c.mask_b, c.magic_b));
-    const half2_t e0 = __builtin_elementwise_fma(p0, c.quarter_neg, c.off_a);
-    const half2_t e1 = __builtin_elementwise_fma(p1, c.quarter_neg, c.off_b);
-    const half2_t e2 = __builtin_elementwise_fma(p2, c.quarter_neg, c.off_a);
-    const half2_t e3 = __builtin_elementwise_fma(p3, c.quarter_neg, c.off_b);
-    // (b << 24) | (b << 8): the e5m2 byte as the high byte of both halves = (s, s).
-    const half2_t s2 = as_half2(__builtin_amdgcn_perm(w, w, 0x000C000Cu));
-    const uint4_t u = {as_u32(e0 * s2), as_u32(e1 * s2), as_u32(e2 * s2), as_u32(e3 * s2)};
-    return __builtin_bit_cast(half8_t, u);
-}
 
 // s_waitcnt encoding (gfx9): wait until at most `n` vector-memory operations
 // of this wave are outstanding; expcnt and lgkmcnt are left unconstrained.

@@ -1,10 +1,12 @@
-// q8_0 and Q4_K decode GEMV / fused gate-up-SwiGLU for gfx950, batch 1..8, on MFMA.
+// q8_0, Q4_K and GF4 decode GEMV / fused gate-up-SwiGLU for gfx950, batch 1..8, on MFMA.
 //
 //   y[b][r] (+)= sum_k W[r][k] * a[k] * x[b][k]
 //
 // Reference kernels replaced:
 //   qw35_decode_matmul_q8_0{,_residual}_f32      (qw35-server/src/metal/qw35_matvec.metal:630-683)
 //   qw35_decode_matmul_q4_k_2row{,_residual}_f32 (qw35-server/src/metal/qw35_matvec.metal:171-353)
+//   qw35_decode_matmul_gf4_2row{,_residual}_f32, qw35_ffn_gate_up_swiglu_gf4_f32
+//                                                (qw35-server/src/metal/qw35_gf4.metal:62-136,209-246)
 //
 // Same structure as the GF4 kernel: a workgroup covers 16*RT rows with KS
 // waves splitting K into 256-column chunks; raw tensor bytes arrive as
@@ -24,6 +26,11 @@
 //   int8 q:   perm into 0x64XX halves after flipping the sign bit -> 1152 + q,
 //             then one v_pk_add_f16 of -1152;
 //   nibble q: mask (and shift) -> 0x64XX halves -> 1024 + q, v_pk_add_f16 of -1024.
+// GF4 words carry their scale inside the exact fp16 operand (gf4_decode.h), so a
+// chunk's eight MFMAs accumulate in one register set; lane group kq takes words
+// 8kq..8kq+7 of a row (two 16-byte LDS reads) and the activation operand
+// follows that k order and the (0,4)(1,5)(2,6)(3,7) pairing within each word.
+#include "gf4_decode.h"
 #include "qw35_device.h"
 #include "qw35_kernels.h"
 
@@ -34,6 +41,7 @@ namespace {
 
 constexpr int kFmtQ8 = 0;
 constexpr int kFmtQ4K = 1;
+constexpr int kFmtGF4 = 2;
 
 template <int FMT>
 struct Fmt;
@@ -52,12 +60,13 @@ struct Fmt<kFmtQ4K> {
     static constexpr int kTypeId = 12;
 };
 
-__device__ __forceinline__ half2_t h2(float lo, float hi) {
-    half2_t r;
-    r.x = (_Float16)lo;
-    r.y = (_Float16)hi;
-    return r;
-}
+template <>
+struct Fmt<kFmtGF4> {
+    static constexpr int kChunkBytes = 128;  // 32 words = 256 columns
+    static constexpr int kSegs = 8;
+    static constexpr int kStride = 144;
+    static constexpr int kTypeId = 100;
+};
 
 template <int N>
 __device__ __forceinline__ void kq_wait_vmcnt() {
@@ -125,13 +134,31 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     constexpr int LPC = NB + (HAS_AWQ ? 1 : 0) + WPC; // loads per chunk
     static_assert(P >= 1 && P <= CPW && P * LPC <= 60, "vmcnt budget");
     const int k = args.k;
-    const int rows = args.rows;
     const int n_batch = args.n_batch;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n = lane & 15;
     const int kq = lane >> 4;
-    const int row0 = blockIdx.x * 16 * RT;
+    // Segment of this workgroup (uniform): its matrix, output and row count.
+    const void* wmat = args.w;
+    float* yout = args.y;
+    int rows = args.rows;
+    int blk = blockIdx.x;
+    if (args.n_seg > 1) {
+        int seg = 0;
+#pragma unroll
+        for (int s = 0; s < kMaxSegments - 1; ++s) {
+            const int tiles = (args.seg_rows[seg] + 16 * RT - 1) / (16 * RT);
+            if (seg + 1 < args.n_seg && blk >= tiles) {
+                blk -= tiles;
+                ++seg;
+            }
+        }
+        wmat = args.seg_w[seg];
+        yout = args.seg_y[seg];
+        rows = args.seg_rows[seg];
+    }
+    const int row0 = blk * 16 * RT;
     const int chunks = k >> 8;
     const size_t row_bytes = (size_t)chunks * F::kChunkBytes;
 
@@ -163,7 +190,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
         for (int t = 0; t < RT; ++t) {
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
-                const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? args.w : args.w_up);
+                const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? wmat : args.w_up);
 #pragma unroll
                 for (int i = 0; i < LPT; ++i) {
                     int s = lane + 64 * i;
@@ -180,6 +207,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     kq_static_for<P>([&](auto CI) { issue(CI); });
 
     const half2_t bias = FMT == kFmtQ8 ? h2(-1152.0f, -1152.0f) : h2(-1024.0f, -1024.0f);
+    const Gf4Consts gc = gf4_consts();
     float acc[RT][NM][2];
 #pragma unroll
     for (int t = 0; t < RT; ++t)
@@ -203,10 +231,23 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                 const float sc = fp16_range_scale(wave_max_abs(mx));
                 isc[b] = 1.0f / sc;
                 v *= sc;
-                const half2_t hi0 = h2(v[0], v[1]);
-                const half2_t hi1 = h2(v[2], v[3]);
-                const half2_t lo0 = h2(v[0] - (float)hi0.x, v[1] - (float)hi0.y);
-                const half2_t lo1 = h2(v[2] - (float)hi1.x, v[3] - (float)hi1.y);
+                float e[4] = {v[0], v[1], v[2], v[3]};
+                if constexpr (FMT == kFmtGF4) {
+                    // Columns 8g..8g+7 stored as x0 x4 x1 x5 x2 x6 x3 x7: even lanes (columns
+                    // 0..3 of the group) write pairs (x0,x4) (x1,x5), odd lanes (x2,x6) (x3,x7).
+                    float u[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor1>(v[q]);
+                    if (lane & 1) {
+                        e[0] = u[2]; e[1] = v[2]; e[2] = u[3]; e[3] = v[3];
+                    } else {
+                        e[0] = v[0]; e[1] = u[0]; e[2] = v[1]; e[3] = u[1];
+                    }
+                }
+                const half2_t hi0 = h2(e[0], e[1]);
+                const half2_t hi1 = h2(e[2], e[3]);
+                const half2_t lo0 = h2(e[0] - (float)hi0.x, e[1] - (float)hi0.y);
+                const half2_t lo1 = h2(e[2] - (float)hi1.x, e[3] - (float)hi1.y);
                 *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + 4 * lane) =
                     uint2_t_{as_u32(hi0), as_u32(hi1)};
                 *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + 4 * lane) =
@@ -233,6 +274,13 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
             const _Float16* arow =
                 a_live ? xs + (size_t)n * L::kActStride : reinterpret_cast<const _Float16*>(wblk + L::kZeroOff);
             const int a_step = a_live ? 32 : 0;
+            // GF4: the chunk's activation operands, shared by every tile (words 8kq + j).
+            half8_t ga[FMT == kFmtGF4 ? 8 : 1];
+            if constexpr (FMT == kFmtGF4) {
+                const _Float16* ap = a_live ? arow + 64 * kq : arow;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ga[j] = *reinterpret_cast<const half8_t*>(ap + (a_live ? 8 * j : 0));
+            }
 
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
@@ -248,7 +296,17 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                     }
                     wave_sync_lds();
                     const uint8_t* wrow = xb + n * F::kStride;
-                    if constexpr (FMT == kFmtQ8) {
+                    if constexpr (FMT == kFmtGF4) {
+                        const uint4_t w0 = *reinterpret_cast<const uint4_t*>(wrow + 32 * kq);
+                        const uint4_t w1 = *reinterpret_cast<const uint4_t*>(wrow + 32 * kq + 16);
+                        const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                        float4_t dd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(ga[j], gf4_word_to_b(ww[j], gc), dd, 0, 0, 0);
+                        acc[t][m][0] = __builtin_fmaf(inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
+                        acc[t][m][1] = __builtin_fmaf(inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
+                    } else if constexpr (FMT == kFmtQ8) {
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
                             // qs bytes [2 + 8 kq, +8) of block j: 4-byte aligned for odd j, 2 mod 4 for even j
@@ -352,7 +410,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
             tot[m] = sum;
         }
         if (r < rows && b < n_batch) {
-            float* yp = args.y + (size_t)b * rows + r;
+            float* yp = yout + (size_t)b * rows + r;
             float v = SWIGLU ? silu(tot[0]) * tot[NM - 1] : tot[0];
             if (args.residual) v += *yp;
             *yp = v;
@@ -386,7 +444,11 @@ template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU>
 hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
     const size_t lds = kq_lds_bytes<FMT, NB, RT, KS, CPW, SWIGLU>();
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
-    const int grid = (a.rows + 16 * RT - 1) / (16 * RT);
+    int grid = (a.rows + 16 * RT - 1) / (16 * RT);
+    if (a.n_seg > 1) {
+        grid = 0;
+        for (int s = 0; s < a.n_seg; ++s) grid += (a.seg_rows[s] + 16 * RT - 1) / (16 * RT);
+    }
     if (a.awq)
         hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds,
                            stream, a);
@@ -398,7 +460,12 @@ hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
 
 template <int FMT, int NB, bool SWIGLU>
 hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
-    KqPlan p = plan_kq(a.rows, a.k);
+    int total_rows = a.rows;
+    if (a.n_seg > 1) {
+        total_rows = 0;
+        for (int s = 0; s < a.n_seg; ++s) total_rows += a.seg_rows[s];
+    }
+    KqPlan p = plan_kq(total_rows, a.k);
     if (SWIGLU && p.p > 2) p.p = 2;  // two matrices per chunk: two chunks in flight
 #define QW35_KQ_PLAN(RT, KS, CPW, P)                        \
     if (p.rt == RT && p.ks == KS && p.cpw == CPW && p.p == P) \
@@ -431,6 +498,10 @@ hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream) {
 
 hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream) {
     return a.w_up ? kq_launch_any<kFmtQ4K, true>(a, stream) : kq_launch_any<kFmtQ4K, false>(a, stream);
+}
+
+hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? kq_launch_any<kFmtGF4, true>(a, stream) : kq_launch_any<kFmtGF4, false>(a, stream);
 }
 
 }  // namespace qw35

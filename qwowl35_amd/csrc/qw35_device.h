@@ -64,7 +64,7 @@ __device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_c
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
 // fp32 -> fp16 round-to-nearest-even, packed.
-__device__ __forceinline__ half2_t pack_half2(float lo, float hi) {
+__device__ __forceinline__ half2_t h2(float lo, float hi) {
     half2_t r;
     r.x = (_Float16)lo;
     r.y = (_Float16)hi;

@@ -15,6 +15,10 @@ constexpr uint32_t kTypeGF4 = 100;
 // Largest decode batch of the GEMV kernels.
 constexpr int kMaxDecodeBatch = 8;
 
+// Matrices sharing k, type, activations and batch can share one launch
+// (q8_0 / Q4_K kernels): segment s covers the rows of seg_w[s], written to seg_y[s].
+constexpr int kMaxSegments = 4;
+
 struct GemvArgs {
     const void* w;        // raw tensor bytes, row-major, rows x row_bytes
     const float* x;       // [n_batch][k]
@@ -25,12 +29,19 @@ struct GemvArgs {
     int k;
     int n_batch;
     int residual;         // y += result instead of y = result
+    int n_seg;            // 0: the single matrix (w, y, rows); 2..kMaxSegments: the segments
+    const void* seg_w[kMaxSegments];
+    float* seg_y[kMaxSegments];
+    int seg_rows[kMaxSegments];
 };
 
 // Each launcher validates nothing (the C ABI does) and returns the launch status.
 hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream);
+// GF4 on the chunked k-quant kernel structure (rolling prefetch, per-chunk
+// activation staging); launch_gf4_gemv picks between the two.
+hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream);
 
 // Full or row-gathered fp32 dequantisation (row_ids == nullptr: all rows).
 hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, const uint32_t* row_ids,

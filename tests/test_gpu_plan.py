@@ -120,3 +120,36 @@ def test_plan_reads_inputs_updated_in_place(cuda):
         logits = om.matvec_f64(deq["head"], b["res"].cpu().numpy())
         assert om.rel_l2(b["logits"].cpu().numpy(), logits) <= GEMV_REL_L2
     plan.close()
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_k"])
+@pytest.mark.parametrize("nb", [1, 5])
+def test_plan_merges_projections_sharing_inputs(cuda, name, nb):
+    """Consecutive k-quant matvecs over one input (a mixer's q/k/v or
+    qkv/z/beta/alpha) are recorded as one multi-segment launch; every segment
+    must equal its own single call, bit for bit, including ragged row counts."""
+    import torch
+
+    rt = _rt()
+    t = TYPES[name]
+    k = 512
+    rng = np.random.default_rng(40 + nb)
+    rows = [160, 32, 48, 7, 96]
+    ws = [rt.HipWeight.upload(make_weight(t, r, k, seed=100 + i)[0], t, r, k, device=cuda)
+          for i, r in enumerate(rows)]
+    x = _t(rng.standard_normal((nb, k), dtype=np.float32), cuda)
+    awq = _t(rng.uniform(0.5, 2, k).astype(np.float32), cuda)
+    outs = [torch.full((nb, r), float("nan"), dtype=torch.float32, device=cuda) for r in rows]
+    want = [rt.decode_matvec(w, x, awq=awq) for w in ws]
+    plan = rt.DecodePlan()
+    for w, o in zip(ws, outs):
+        plan.matvec(w, x, o, awq=awq)
+    plan.record()
+    for _ in range(2):
+        for o in outs:
+            o.fill_(float("nan"))
+        plan.launch()
+        torch.cuda.synchronize()
+        for o, wv in zip(outs, want):
+            assert torch.equal(o, wv)
+    plan.close()
