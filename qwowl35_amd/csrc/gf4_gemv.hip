@@ -361,11 +361,16 @@ hipError_t launch_nb(const GemvArgs& a, hipStream_t stream) {
     return hipErrorInvalidValue;
 }
 
+// Largest batch slice (8, 4, 2, 1 rows) whose plan fits the 160 KiB LDS.
+int gf4_batch_slice(const GemvArgs& a, bool swiglu) {
+    int slice = 8;
+    while (slice > 1 && plan_lds(plan_gf4(slice, a.rows, a.k, swiglu), slice, swiglu) > 160 * 1024) slice >>= 1;
+    return slice;
+}
+
 template <bool SWIGLU>
 hipError_t launch_gf4_any(const GemvArgs& a, hipStream_t stream) {
-    // Largest batch slice (8, 4, 2, 1 rows) whose plan fits the 160 KiB LDS.
-    int slice = 8;
-    while (slice > 1 && plan_lds(plan_gf4(slice, a.rows, a.k, SWIGLU), slice, SWIGLU) > 160 * 1024) slice >>= 1;
+    const int slice = gf4_batch_slice(a, SWIGLU);
     if (plan_lds(plan_gf4(1, a.rows, a.k, SWIGLU), 1, SWIGLU) > 160 * 1024) return hipErrorInvalidValue;
     for (int b0 = 0; b0 < a.n_batch; b0 += slice) {
         GemvArgs s = a;
@@ -385,6 +390,10 @@ hipError_t launch_gf4_any(const GemvArgs& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream) {
+    // When the activations of the whole batch do not fit this kernel's LDS it
+    // would stream the weights once per batch slice; the chunked kernel (per-chunk
+    // activation staging) takes the batch in one launch.
+    if (a.n_batch > gf4_batch_slice(a, a.w_up != nullptr)) return launch_gf4_gemv_chunked(a, stream);
     return a.w_up ? launch_gf4_any<true>(a, stream) : launch_gf4_any<false>(a, stream);
 }
 

@@ -422,16 +422,22 @@ struct KqPlan {
     int rt, ks, cpw, p;
 };
 
-// KS waves x CPW chunks cover k, P chunks in flight per wave; RT row tiles
-// per workgroup for tall matrices (the LM head).
-KqPlan plan_kq(int rows, int k) {
+// KS waves x CPW chunks cover k with P chunks in flight per wave; RT row tiles
+// per workgroup amortise the per-chunk activation staging over more rows, which
+// pays from batch 4 up on matrices with enough tiles (measured on MI355X:
+// 12288 x 4096 at batch 8, q8_0 32 -> 21 us, GF4 26 -> 14 us; Q4_K prefers four
+// tiles with one chunk in flight).
+KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
     if (chunks <= 4) return {1, 4, 1, 1};
     if (chunks <= 8) return {1, 8, 1, 1};
-    if (chunks <= 16) return {tiles >= 1024 ? 2 : 1, 8, 2, 2};
-    if (chunks <= 32) return {1, 8, 4, 3};
-    return {1, 8, 6, 3};
+    if (chunks <= 16) {
+        if (nb >= 4 && tiles >= 512) return fmt == kFmtQ4K ? KqPlan{4, 8, 2, 1} : KqPlan{3, 8, 2, 2};
+        return {1, 8, 2, 2};
+    }
+    if (chunks <= 32) return {1, 8, 4, 2};
+    return {1, 8, 6, 2};
 }
 
 template <int FMT, int NB, int RT, int KS, int CPW, bool SWIGLU>
@@ -458,6 +464,13 @@ hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Loads in flight per wave for a configuration (must fit the vmcnt counter).
+template <int FMT, int NB, int RT, int P, bool SWIGLU>
+constexpr bool kq_fits() {
+    constexpr int lpt = (16 * Fmt<FMT>::kSegs + 63) / 64;
+    return P * (NB + 1 + RT * (SWIGLU ? 2 : 1) * lpt) <= 60;
+}
+
 template <int FMT, int NB, bool SWIGLU>
 hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
     int total_rows = a.rows;
@@ -465,19 +478,21 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
         total_rows = 0;
         for (int s = 0; s < a.n_seg; ++s) total_rows += a.seg_rows[s];
     }
-    KqPlan p = plan_kq(total_rows, a.k);
-    if (SWIGLU && p.p > 2) p.p = 2;  // two matrices per chunk: two chunks in flight
-#define QW35_KQ_PLAN(RT, KS, CPW, P)                        \
-    if (p.rt == RT && p.ks == KS && p.cpw == CPW && p.p == P) \
-        return kq_launch_cfg<FMT, NB, RT, KS, CPW, P, SWIGLU>(a, stream);
+    KqPlan p = plan_kq(FMT, total_rows, a.k, NB);
+#define QW35_KQ_PLAN(RT, KS, CPW, P)                                                             \
+    if constexpr (kq_fits<FMT, NB, RT, P, SWIGLU>()) {                                             \
+        if (p.rt == RT && p.ks == KS && p.cpw == CPW && p.p == P)                                  \
+            return kq_launch_cfg<FMT, NB, RT, KS, CPW, P, SWIGLU>(a, stream);                      \
+    }
     QW35_KQ_PLAN(1, 4, 1, 1)
     QW35_KQ_PLAN(1, 8, 1, 1)
     QW35_KQ_PLAN(1, 8, 2, 2)
-    QW35_KQ_PLAN(2, 8, 2, 2)
-    QW35_KQ_PLAN(1, 8, 4, 3)
-    QW35_KQ_PLAN(1, 8, 6, 3)
+    QW35_KQ_PLAN(3, 8, 2, 2)
+    QW35_KQ_PLAN(4, 8, 2, 1)
     QW35_KQ_PLAN(1, 8, 4, 2)
     QW35_KQ_PLAN(1, 8, 6, 2)
+    // over the load budget (fused gate/up at batch 8): one tile per workgroup
+    if (p.rt > 1) return kq_launch_cfg<FMT, NB, 1, 8, 2, (kq_fits<FMT, NB, 1, 2, SWIGLU>() ? 2 : 1), SWIGLU>(a, stream);
 #undef QW35_KQ_PLAN
     return hipErrorInvalidValue;
 }
