@@ -126,6 +126,21 @@ def read_traffic(kernel_hint: str):
     return int(m.group(1)), k.group(1)
 
 
+def stream_ceiling(b: Bench, rt, torch, bufs) -> dict:
+    """Streaming-read ceiling on the same box: the library's read probe over the
+    same rotated 25 MB buffers (launch and ramp included, like the GEMV) and
+    over one 1 GiB buffer."""
+    sinks = [torch.empty(rt.stream_read(bufs[0]).numel(), dtype=torch.int32, device=b.dev) for _ in bufs]
+    calls = [lambda s, t=t, k=k: rt.stream_read(t, k, stream=s) for t, k in zip(bufs, sinks)]
+    ms, _, _ = b.time_calls(calls, 2000, 200)
+    big = torch.zeros(1 << 30, dtype=torch.uint8, device=b.dev)
+    sink_big = rt.stream_read(big)
+    ms_big, _, _ = b.time_calls([lambda s: rt.stream_read(big, sink_big, stream=s)], 40, 5)
+    n = bufs[0].numel()
+    return {"GB/s_25MB": round(n / (ms * 1e-3) / 1e9, 1), "us_25MB": round(ms * 1e3, 3),
+            "GB/s_1GiB": round((1 << 30) / (ms_big * 1e-3) / 1e9, 1)}
+
+
 BF16_DENSE_PEAK_TFLOPS = 2500.0
 
 
@@ -282,6 +297,9 @@ def main() -> int:
     traffic, traffic_kernel = read_traffic("gf4_mfma_gemv<1,")
 
     extra = {}
+    ceil = stream_ceiling(b, rt, torch, [w.storage for w in weights])
+    extra["stream_read_ceiling"] = ceil
+    extra["gf4_b1_frac_of_stream_ceiling"] = round(value / ceil["GB/s_25MB"], 4)
     if not args.headline_only:
         for nb in (2, 4, 8):
             xb = b.normal((nb, k))

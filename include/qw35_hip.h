@@ -155,6 +155,15 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_
 int qw35_hip_quantize(uint32_t type_id, const float *src, uint64_t rows, uint64_t k, const float *col_scale,
                       void *dst, void *stream, char *err, uintptr_t err_len);
 
+/* Streaming-read probe: reads every byte of the device buffer `buf` once
+ * (`bytes` a multiple of 16, 16-byte aligned) and writes one XOR digest per
+ * workgroup into `sink` (device, qw35_hip_stream_read_sink_len(bytes) uint32
+ * values).  No counterpart in the reference: it measures the HBM read ceiling
+ * that the GEMV bandwidths are reported against. */
+uint32_t qw35_hip_stream_read_sink_len(uint64_t bytes);
+int qw35_hip_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, void *stream, char *err,
+                         uintptr_t err_len);
+
 /* Wait for the stream and report any asynchronous device error.  Replaces
  * qw35_metal_runtime_sync (Qw35FFI.h:71-72). */
 int qw35_hip_sync(void *stream, char *err, uintptr_t err_len);

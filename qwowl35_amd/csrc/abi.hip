@@ -415,6 +415,24 @@ int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_
                : 0;
 }
 
+uint32_t qw35_hip_stream_read_sink_len(uint64_t bytes) { return qw35::stream_read_blocks(bytes); }
+
+int qw35_hip_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, void* stream, char* err,
+                         uintptr_t err_len) {
+    if (!buf || !sink || bytes == 0) {
+        set_err(err, err_len, "stream_read: null buffer or sink, or zero bytes");
+        return 0;
+    }
+    if ((bytes & 15u) || ((uintptr_t)buf & 15u) || ((uintptr_t)sink & 3u)) {
+        set_err(err, err_len, "stream_read: buf and bytes must be 16-byte aligned, sink 4-byte aligned");
+        return 0;
+    }
+    return check_hip(qw35::launch_stream_read(buf, bytes, sink, static_cast<hipStream_t>(stream)), "stream_read", err,
+                     err_len)
+               ? 1
+               : 0;
+}
+
 int qw35_hip_sync(void* stream, char* err, uintptr_t err_len) {
     hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     if (e == hipSuccess) e = hipGetLastError();

@@ -238,3 +238,56 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
 }
 
 }  // namespace qw35
+
+// Streaming-read probe: the measured HBM read ceiling the GEMVs are compared
+// with.  Every 16-byte word of `buf` is loaded once (non-temporal, four loads in
+// flight per thread) and folded into one XOR per workgroup, written to
+// sink[blockIdx.x] so that no load can be elided.
+namespace qw35 {
+namespace {
+
+constexpr int kReadThreads = 256;
+
+__global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4_t* __restrict__ buf, uint64_t words,
+                                                                   uint32_t* __restrict__ sink) {
+    uint32_t acc = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * kReadThreads;
+    uint64_t i = (uint64_t)blockIdx.x * kReadThreads + threadIdx.x;
+    for (; i + 3 * stride < words; i += 4 * stride) {
+        const uint4_t a = load_stream16(buf + i);
+        const uint4_t b = load_stream16(buf + i + stride);
+        const uint4_t c = load_stream16(buf + i + 2 * stride);
+        const uint4_t d = load_stream16(buf + i + 3 * stride);
+        acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+    }
+    for (; i < words; i += stride) {
+        const uint4_t a = load_stream16(buf + i);
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    __shared__ uint32_t red[kReadThreads / 64];
+    for (int o = 1; o < 64; o <<= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t v = 0;
+        for (int w = 0; w < kReadThreads / 64; ++w) v ^= red[w];
+        sink[blockIdx.x] = v;
+    }
+}
+
+}  // namespace
+
+unsigned stream_read_blocks(uint64_t bytes) {
+    const uint64_t words = bytes / 16;
+    uint64_t blocks = (words + 4 * kReadThreads - 1) / (4 * kReadThreads);
+    if (blocks > 8192) blocks = 8192;
+    return blocks ? (unsigned)blocks : 1u;
+}
+
+hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t stream) {
+    hipLaunchKernelGGL(stream_read_kernel, dim3(stream_read_blocks(bytes)), dim3(kReadThreads), 0, stream,
+                       static_cast<const uint4_t*>(buf), bytes / 16, sink);
+    return hipGetLastError();
+}
+
+}  // namespace qw35

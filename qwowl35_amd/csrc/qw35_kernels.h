@@ -52,6 +52,11 @@ hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, cons
 hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, const float* col_scale, void* dst,
                            hipStream_t stream);
 
+// Streaming-read probe over `bytes` (a multiple of 16) of `buf`; sink holds
+// stream_read_blocks(bytes) uint32 values.
+unsigned stream_read_blocks(uint64_t bytes);
+hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t stream);
+
 // GF4 prefill dequant-matmul on bf16 MFMA:
 //   C[m][n] = sum_k bf16_rne(awq[k] * A[m][k]) * W[n][k],  fp32 accumulation.
 // a: [m][k] bf16 (a_f32 == 0) or fp32; c: [m][rows] bf16 RNE (out_f32 == 0) or fp32.

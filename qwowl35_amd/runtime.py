@@ -275,5 +275,16 @@ class DecodePlan:
             pass
 
 
+def stream_read(buf: torch.Tensor, sink: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Streaming-read probe over a device buffer (measures the HBM read ceiling);
+    returns the per-workgroup XOR digests (int32 view of uint32)."""
+    nbytes = buf.numel() * buf.element_size()
+    n = int(_ffi.load().qw35_hip_stream_read_sink_len(nbytes))
+    if sink is None:
+        sink = torch.empty(n, dtype=torch.int32, device=buf.device)
+    _ffi.call("qw35_hip_stream_read", _ptr(buf), nbytes, _ptr(sink), _stream(stream))
+    return sink
+
+
 def sync(stream=None) -> None:
     _ffi.call("qw35_hip_sync", _stream(stream))

@@ -203,3 +203,11 @@ def test_plan_null_handles(lib):
     lib.qw35_hip_plan_destroy(None)
     with pytest.raises(_ffi.Qw35Error, match="null plan"):
         _ffi.call("qw35_hip_plan_launch", None, None)
+
+
+def test_stream_read_validates(lib):
+    assert lib.qw35_hip_stream_read_sink_len(16) >= 1
+    with pytest.raises(_ffi.Qw35Error, match="zero bytes"):
+        _ffi.call("qw35_hip_stream_read", C.c_void_p(4096), 0, C.c_void_p(4096), None)
+    with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
+        _ffi.call("qw35_hip_stream_read", C.c_void_p(4096), 24, C.c_void_p(4096), None)

@@ -116,3 +116,15 @@ def test_quantize_then_gemv_roundtrip(cuda):
         assert np.array_equal(deq.view(np.uint32), om.dequant(type_id, raw, rows, k).view(np.uint32)), name
         y = _rt().decode_matvec(hw, _t(x, cuda)).cpu().numpy()
         assert om.rel_l2(y, om.matvec_f64(deq, x)) <= 1e-3, name
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 48, 25_165_824])
+def test_stream_read_probe_reads_every_word(cuda, nbytes):
+    """The read probe's per-workgroup XOR digests fold to the XOR of all words."""
+    import torch
+
+    rng = np.random.default_rng(nbytes)
+    host = rng.integers(0, 2**32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = torch.from_numpy(host.view(np.int32)).to(cuda)
+    sink = _rt().stream_read(buf).cpu().numpy().view(np.uint32)
+    assert int(np.bitwise_xor.reduce(sink)) == int(np.bitwise_xor.reduce(host))
