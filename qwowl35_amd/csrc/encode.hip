@@ -246,7 +246,7 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
 namespace qw35 {
 namespace {
 
-constexpr int kReadThreads = 256;
+constexpr int kReadThreads = 512;
 
 __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4_t* __restrict__ buf, uint64_t words,
                                                                    uint32_t* __restrict__ sink) {
@@ -277,10 +277,11 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4_t
 
 }  // namespace
 
+// About 768 words (12 KiB) per workgroup, at most 16384 workgroups: the fastest
+// of the launch shapes measured on MI355X for 25 MB (5.1 us) and 1 GiB (6.9 TB/s).
 unsigned stream_read_blocks(uint64_t bytes) {
-    const uint64_t words = bytes / 16;
-    uint64_t blocks = (words + 4 * kReadThreads - 1) / (4 * kReadThreads);
-    if (blocks > 8192) blocks = 8192;
+    uint64_t blocks = bytes / 16 / 768;
+    if (blocks > 16384) blocks = 16384;
     return blocks ? (unsigned)blocks : 1u;
 }
 
