@@ -267,7 +267,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--copies", type=int, default=32, help="distinct GF4 weight copies rotated (>= 24)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--headline-only", action="store_true", help="skip the extra configs")
+    ap.add_argument("--headline-only", action="store_true", help="skip the extra configs (= --extras none)")
+    ap.add_argument("--extras", default="all",
+                    help="comma list of extra configs: gf4,q8,q4k,prefill,stack (or all / none)")
     ap.add_argument("--cpu-reps", type=int, default=40)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -300,14 +302,17 @@ def main() -> int:
     ceil = stream_ceiling(b, rt, torch, [w.storage for w in weights])
     extra["stream_read_ceiling"] = ceil
     extra["gf4_b1_frac_of_stream_ceiling"] = round(value / ceil["GB/s_25MB"], 4)
-    if not args.headline_only:
+    want = set() if args.headline_only or args.extras == "none" else (
+        {"gf4", "q8", "q4k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
+    if "gf4" in want:
         for nb in (2, 4, 8):
             xb = b.normal((nb, k))
             yb = torch.zeros((nb, rows), dtype=torch.float32, device=b.dev)
             m, _, _ = b.time_calls(gemv_calls(rt, weights, xb, yb), args.steps // 2, args.warmup)
             extra[f"gf4_b{nb}_12288x4096"] = {"us": round(m * 1e3, 3),
                                               "GB/s": round(gemv_bytes(rt.TYPE_GF4, rows, k, nb, rt) / m / 1e6, 1)}
-        del weights
+    del weights
+    if "gf4" in want:
         wt = [b.weight(rt.TYPE_GF4, 4096, 12288) for _ in range(args.copies)]
         xt = b.normal((1, 12288))
         yt = torch.zeros((1, 4096), dtype=torch.float32, device=b.dev)
@@ -315,7 +320,7 @@ def main() -> int:
         extra["gf4_b1_4096x12288"] = {"us": round(m * 1e3, 3),
                                       "GB/s": round(gemv_bytes(rt.TYPE_GF4, 4096, 12288, 1, rt) / m / 1e6, 1)}
         del wt
-
+    if "q8" in want:
         # config 2: q8_0 projections of one decoder layer, 3 distinct sets (670 MB)
         shapes = [(8192, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096),
                   (4096, 12288)]
@@ -329,7 +334,7 @@ def main() -> int:
         extra["q8_0_layer_set_b1"] = {"us_per_set": round(per_set_ms * 1e3, 3), "bytes": set_bytes,
                                       "GB/s": round(set_bytes / per_set_ms / 1e6, 1)}
         del sets
-
+    if "q4k" in want:
         # config 3: Q4_K down 4096x12288 (24 copies) and LM head 248320x4096, batch 1 and 8
         down = [b.weight(rt.TYPE_Q4_K, 4096, 12288) for _ in range(24)]
         head = b.weight(rt.TYPE_Q4_K, 248320, 4096, tile_rows=16384)
@@ -345,11 +350,12 @@ def main() -> int:
             extra[f"q4_k_head_b{nb}_248320x4096"] = {
                 "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 248320, 4096, nb, rt) / m / 1e6, 1)}
         del down, head
-
+    if "prefill" in want:
         extra.update(bench_prefill(b, rt, torch))
+    if "stack" in want:
         extra.update(bench_decode_stack(b, rt, torch))
-        for key, v in extra.items():
-            log(f"{key}: {v}")
+    for key, v in extra.items():
+        log(f"{key}: {v}")
 
     cpu = None
     if not args.no_cpu:
