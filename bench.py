@@ -146,7 +146,9 @@ BF16_DENSE_PEAK_TFLOPS = 2500.0
 
 def bench_prefill(b: Bench, rt, torch) -> dict:
     """Config 4: GF4 prefill dequant-matmul, W 12288x4096 and 4096x12288 (12
-    rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out."""
+    rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out; the staged
+    path (workspace, fp16 MFMA; the time includes the staging pass) and the
+    direct path (bf16 MFMA)."""
     out = {}
     for rows, k in ((12288, 4096), (4096, 12288)):
         ws = [b.weight(rt.TYPE_GF4, rows, k) for _ in range(12)]
@@ -154,12 +156,15 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
         for m in (128, 512, 2048):
             a = b.normal((m, k)).to(torch.bfloat16)
             c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
-            calls = [lambda s, w=w: rt.matmul_prefill(w, a, awq=awq, dst=c, stream=s) for w in ws]
-            ms, _, _ = b.time_calls(calls, max(24, 4800 // m), 12)
-            tflops = 2.0 * m * rows * k / (ms * 1e-3) / 1e12
-            out[f"prefill_gf4_m{m}_{rows}x{k}"] = {
-                "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
-                "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4)}
+            wsp = rt.prefill_workspace(m, k, device=b.dev)
+            for path, work in (("", wsp), ("_direct", None)):
+                calls = [lambda s, w=w, work=work: rt.matmul_prefill(w, a, awq=awq, dst=c, workspace=work, stream=s)
+                         for w in ws]
+                ms, _, _ = b.time_calls(calls, max(24, 4800 // m), 12)
+                tflops = 2.0 * m * rows * k / (ms * 1e-3) / 1e12
+                out[f"prefill_gf4_m{m}_{rows}x{k}{path}"] = {
+                    "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                    "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4)}
         del ws
     return out
 

@@ -130,7 +130,7 @@ int qw35_hip_plan_launch(void *plan, void *stream, char *err, uintptr_t err_len)
 uint32_t qw35_hip_plan_size(const void *plan);
 void qw35_hip_plan_destroy(void *plan);
 
-/* Multi-token (prefill) matmul of a GF4 weight on bf16 MFMA:
+/* Multi-token (prefill) matmul of a GF4 weight on MFMA:
  *   c[t][r] = sum_k bf16_rne(awq[k] * a[t][k]) * W[r][k]    (awq == NULL: a[t][k] as bf16)
  * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32
  * (fp32 input is rounded to bf16 after the AWQ multiply); c: device
@@ -141,8 +141,16 @@ void qw35_hip_plan_destroy(void *plan);
  * 1 <= n_tokens <= 65536. */
 #define QW35_HIP_DTYPE_F32 0u
 #define QW35_HIP_DTYPE_BF16 1u
+/* workspace: NULL, or device memory of qw35_hip_matmul_prefill_workspace_size
+ * bytes (256-byte aligned, owned by the caller, not shared by concurrent
+ * calls).  With a workspace the activations are first staged as fp16 with a
+ * per-token power-of-two scale (exact for every value above 2^-28 of the
+ * token's largest) and contracted on fp16 MFMA; without, the loader converts
+ * them and contracts on bf16 MFMA.  Both compute the same products. */
+uint64_t qw35_hip_matmul_prefill_workspace_size(uint32_t n_tokens, uint64_t k);
 int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
-                            uint32_t c_dtype, uint32_t n_tokens, void *stream, char *err, uintptr_t err_len);
+                            uint32_t c_dtype, uint32_t n_tokens, void *workspace, uint64_t workspace_bytes,
+                            void *stream, char *err, uintptr_t err_len);
 
 /* Weight producer: fp32 src [rows][k] (device, 16-byte aligned) -> raw tensor
  * bytes of type_id in dst (device, 16-byte aligned, rows * row_bytes(type, k)

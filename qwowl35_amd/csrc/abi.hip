@@ -352,8 +352,14 @@ int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint3
                : 0;
 }
 
+uint64_t qw35_hip_matmul_prefill_workspace_size(uint32_t n_tokens, uint64_t k) {
+    if (n_tokens < 1 || n_tokens > 65536 || k == 0 || k > kMaxK) return 0;
+    return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)k);
+}
+
 int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
-                            uint32_t c_dtype, uint32_t n_tokens, void* stream, char* err, uintptr_t err_len) {
+                            uint32_t c_dtype, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes,
+                            void* stream, char* err, uintptr_t err_len) {
     if (!check_weight(w, "matmul_prefill", err, err_len)) return 0;
     if (w->type_id != qw35::kTypeGF4) {
         set_err(err, err_len, "matmul_prefill: only GF4 (type 100) weights are supported, got %s",
@@ -376,8 +382,16 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         set_err(err, err_len, "matmul_prefill: a/awq must be 16-byte aligned and c 4-byte aligned");
         return 0;
     }
+    if (workspace) {
+        const uint64_t need = qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->k);
+        if (workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
+            set_err(err, err_len, "matmul_prefill: workspace must be 256-byte aligned and >= %llu bytes, got %llu",
+                    (unsigned long long)need, (unsigned long long)workspace_bytes);
+            return 0;
+        }
+    }
     return check_hip(qw35::launch_gf4_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
-                                              awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32,
+                                              awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace,
                                               static_cast<hipStream_t>(stream)),
                      "matmul_prefill", err, err_len)
                ? 1

@@ -22,6 +22,7 @@
 //   (the format of tools/qw35_cook_common.py:79 with c = q_raw ^ 4).
 // * Blocks are assigned XCD by XCD (consecutive block ids land on different
 //   XCDs), M-tile fastest, so the blocks that share a W tile share an L2.
+#include "gf4_decode.h"
 #include "qw35_device.h"
 #include "qw35_kernels.h"
 
@@ -36,10 +37,11 @@ constexpr int kLdsRow = kBK * 2 + 16;   // bytes per staged row: 64 bf16 + 16 B 
 constexpr int kXcds = 8;
 
 struct PrefillArgs {
-    const uint32_t* w;   // GF4 words [N][K/8]
-    const void* a;       // [M][K] bf16 or fp32
-    const float* awq;    // [K] or nullptr
-    void* c;             // [M][N] bf16 or fp32
+    const uint32_t* w;       // GF4 words [N][K/8]
+    const void* a;           // [M][K] bf16 or fp32 (staged path: fp16, see below)
+    const float* awq;        // [K] or nullptr
+    void* c;                 // [M][N] bf16 or fp32
+    const float* row_scale;  // staged path: per token row, the inverse of its fp16 scale
     int m, n, k;
     int tiles_m, tiles_n;
 };
@@ -60,6 +62,87 @@ __device__ __forceinline__ uint4_t gf4_word_to_bf16x8(uint32_t w) {
     return uint4_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
 }
 
+// Staged activations (the path taken when the caller provides a workspace):
+// one workgroup per token row writes A'' = fp16(2^e * bf16_rne(awq * A)) with
+// 2^e the power of two that puts the row's max |A'| in [2^14, 2^15), and
+// row_scale = 2^-e.  Every bf16 value of at least 2^-28 of the row maximum is
+// exact in fp16 (smaller ones round at 2^-39 of the maximum), so the matmul
+// can contract on fp16 MFMA with the GF4 weights decoded by the 15-op fp16
+// decode of gf4_decode.h.  Each group of 8 columns is stored in the decode's
+// column order 0,4,1,5,2,6,3,7.
+constexpr int kStageThreads = 256;
+
+template <bool A_F32, bool HAS_AWQ>
+__global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void* __restrict__ a,
+                                                                      const float* __restrict__ awq, int k,
+                                                                      uint16_t* __restrict__ a16,
+                                                                      float* __restrict__ row_scale) {
+    constexpr int kMaxGroups = 12288 / 8 / kStageThreads;  // groups of 8 columns per thread
+    const int row = blockIdx.x;
+    const int groups = k >> 3;
+    float v[kMaxGroups][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxGroups; ++j) {
+        const int g = threadIdx.x + j * kStageThreads;
+        if (g >= groups) break;
+        const size_t e0 = (size_t)row * k + 8 * g;
+        if constexpr (A_F32) {
+            const float4_t lo = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a) + e0);
+            const float4_t hi = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a) + e0 + 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[j][q] = lo[q];
+                v[j][4 + q] = hi[q];
+            }
+        } else {
+            const uint4_t u = *reinterpret_cast<const uint4_t*>(static_cast<const uint16_t*>(a) + e0);
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[j][2 * q] = bf16_lo(w4[q]);
+                v[j][2 * q + 1] = bf16_hi(w4[q]);
+            }
+        }
+        if constexpr (HAS_AWQ || A_F32) {
+            float s8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+            if constexpr (HAS_AWQ) {
+                const float4_t s0 = *reinterpret_cast<const float4_t*>(awq + 8 * g);
+                const float4_t s1 = *reinterpret_cast<const float4_t*>(awq + 8 * g + 4);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    s8[q] = s0[q];
+                    s8[4 + q] = s1[q];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q += 2) {  // A' = bf16_rne(awq * A), kept as fp32
+                const uint32_t pk = pack_bf16(v[j][q] * s8[q], v[j][q + 1] * s8[q + 1]);
+                v[j][q] = bf16_lo(pk);
+                v[j][q + 1] = bf16_hi(pk);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
+    }
+    __shared__ float red[kStageThreads / 64];
+    mx = wave_max_abs(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = 2.0f * fp16_range_scale(mx);  // max in [2^14, 2^15)
+    if (threadIdx.x == 0) row_scale[row] = 1.0f / sc;
+#pragma unroll
+    for (int j = 0; j < kMaxGroups; ++j) {
+        const int g = threadIdx.x + j * kStageThreads;
+        if (g >= groups) break;
+        const float* x = v[j];
+        const uint4_t out{as_u32(h2(x[0] * sc, x[4] * sc)), as_u32(h2(x[1] * sc, x[5] * sc)),
+                          as_u32(h2(x[2] * sc, x[6] * sc)), as_u32(h2(x[3] * sc, x[7] * sc))};
+        *reinterpret_cast<uint4_t*>(a16 + (size_t)row * k + 8 * g) = out;
+    }
+}
+
 template <int BM, int BN, int NT, bool A_F32>
 struct StepRegs {
     static constexpr int A_CHUNKS = BM * 8 / NT;  // 8-element A chunks per thread
@@ -68,9 +151,10 @@ struct StepRegs {
     uint32_t b[WPT];
 };
 
-template <int BM, int BN, int WGM, int WGN, bool A_F32, bool HAS_AWQ, bool OUT_F32>
+// Direct path: bf16 MFMA on A' converted in the loader.
 // Two waves per SIMD (<= 256 VGPRs): one wave's loads and conversions overlap
 // the other's MFMAs.
+template <int BM, int BN, int WGM, int WGN, bool A_F32, bool HAS_AWQ, bool OUT_F32>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2))) void gf4_prefill_kernel(
     PrefillArgs p) {
     constexpr int NT = 64 * WGM * WGN;
@@ -101,6 +185,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const int n0 = (t / p.tiles_m) * BN;
     const int K = p.k;
     const int words_per_row = K >> 3;
+    const Gf4Consts gc = gf4_consts();
 
     // Per-thread global sources (rows clamped into range; stores are masked).
     const uint8_t* a_src[A_CHUNKS];
@@ -268,6 +353,203 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
+// Staged path: fp16 A'' (prefill_stage_kernel) against GF4 words decoded
+// straight from global memory into MFMA operand registers.
+//
+// * A block owns a BM x (64 * NW) tile of C.  Its NW waves split the weight
+//   rows (64 per wave) and all read the block's BM token rows from LDS, so every
+//   GF4 word is loaded and decoded (15 VALU ops, fp16, gf4_decode.h) by exactly
+//   one wave and the only LDS traffic is the token tile.
+// * v_mfma_f32_32x32x16_f16 with the weight tile as first operand: lane l
+//   supplies weight row l % 32 and receives D[n][m = l % 32], four consecutive
+//   weight rows per register group, so results leave as 8- or 16-byte stores.
+// * Within a 64-wide k step lane half h of sub-step kk takes the 8 columns of
+//   GF4 word 4h + kk, so each lane's four words of a row are one 16-byte load;
+//   the token operand follows that order (and the decode's 0,4,1,5,2,6,3,7
+//   column order, which the staging pass already wrote).
+// * Global loads run two steps ahead in two register stages; the token tile
+//   is double buffered in LDS, one barrier per step.
+template <int BM, int NW, int WPE, bool OUT_F32>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
+    PrefillArgs p) {
+    constexpr int NT = 64 * NW;
+    constexpr int BN = 64 * NW;
+    constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave
+    constexpr int FN = 2;                   // 32-row weight tiles per wave
+    constexpr int A_CHUNKS = BM * 8 / NT;   // 16-byte token chunks per thread per step
+    constexpr int BUF = BM * kLdsRow;
+    static_assert(BM % 32 == 0 && BM * 8 % NT == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
+    typedef float float16_t __attribute__((ext_vector_type(16)));
+    typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+
+    const int tiles = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if (tiles % kXcds == 0) t = (t % kXcds) * (tiles / kXcds) + t / kXcds;
+    const int m0 = (t % p.tiles_m) * BM;
+    const int n0 = (t / p.tiles_m) * BN + wave * 64;
+    const int K = p.k;
+    const int words_per_row = K >> 3;
+    const Gf4Consts gc = gf4_consts();
+
+    uint32_t a_off[A_CHUNKS];
+    int a_lds[A_CHUNKS];
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+        const int c = tid + i * NT;
+        const int row = c >> 3;
+        const int col = c & 7;
+        const int gm = min(m0 + row, p.m - 1);
+        a_off[i] = ((uint32_t)gm * (uint32_t)K + (uint32_t)col * 8u) * 2u;
+        a_lds[i] = row * kLdsRow + col * 16;
+    }
+    const uint32_t* w_src[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+        w_src[j] = p.w + (size_t)min(n0 + 32 * j + l32, p.n - 1) * words_per_row + 4 * half;
+    const uint8_t* a_base = static_cast<const uint8_t*>(p.a);
+
+    typedef uint4_t Tokens[A_CHUNKS];
+    typedef uint4_t Words[FN];
+    auto load_tokens = [&](int kt, Tokens& a) {
+        const uint32_t k0 = (uint32_t)kt * kBK;
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; ++i) a[i] = *reinterpret_cast<const uint4_t*>(a_base + a_off[i] + k0 * 2);
+    };
+    auto load_words = [&](int kt, Words& w) {
+        const uint32_t k0 = (uint32_t)kt * kBK;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) w[j] = load_stream16(w_src[j] + (k0 >> 3));
+    };
+    auto store_tokens = [&](const Tokens& a, uint8_t* buf) {
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4_t*>(buf + a_lds[i]) = a[i];
+    };
+
+    float16_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const int a_rd = l32 * kLdsRow + half * 64;
+
+    auto compute = [&](const Words& w, const uint8_t* buf) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            half8_t wf[FN], af[FM];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint32_t word = kk == 0 ? w[j].x : kk == 1 ? w[j].y : kk == 2 ? w[j].z : w[j].w;
+                wf[j] = gf4_word_to_b(word, gc);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[i] = *reinterpret_cast<const half8_t*>(buf + a_rd + i * 32 * kLdsRow + kk * 16);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], af[i], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Pipeline, per step kt: the step's tokens were written to LDS at the end
+    // of step kt-1 and its weight words loaded at step kt-2.  A step first
+    // issues the loads of step kt+2 (tokens into the register set the previous
+    // step emptied into LDS, words into the ring slot two ahead), then runs its
+    // MFMAs, then writes the tokens of step kt+1 to the other LDS buffer.  The
+    // words ring has four slots and the loop body covers four steps, so every
+    // register set is loaded and consumed under one static name and nothing
+    // loaded is copied across the loop back-edge (a copy would wait for the
+    // load).  K is a multiple of 4 * kBK (the host checks k % 256 == 0); the
+    // prefetches past the last step re-read it instead of branching.
+    const int KT = K / kBK;
+    uint8_t* buf0 = smem;
+    uint8_t* buf1 = smem + BUF;
+    Tokens t0, t1;
+    Words w0, w1, w2, w3;
+    load_tokens(0, t0);
+    load_words(0, w0);
+    load_tokens(1, t1);
+    load_words(1, w1);
+    store_tokens(t0, buf0);
+    __syncthreads();
+    auto step = [&](int kt, Tokens& t_next, Words& w_next, const Words& w_cur, const uint8_t* cur,
+                    const Tokens& t_fill, uint8_t* fill) {
+        const int ahead = min(kt + 2, KT - 1);
+        load_tokens(ahead, t_next);
+        load_words(ahead, w_next);
+        __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this step's math
+        compute(w_cur, cur);
+        store_tokens(t_fill, fill);
+        __syncthreads();
+    };
+    for (int kt = 0; kt < KT; kt += 4) {
+        step(kt, t0, w2, w0, buf0, t1, buf1);
+        step(kt + 1, t1, w3, w1, buf1, t0, buf0);
+        step(kt + 2, t0, w0, w2, buf0, t1, buf1);
+        step(kt + 3, t1, w1, w3, buf1, t0, buf0);
+    }
+
+    // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
+    const bool vec_ok = (p.n & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int gm = m0 + 32 * i + l32;
+        if (gm >= p.m) continue;
+        const float rs = p.row_scale[gm];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int gn = n0 + 32 * j + 8 * g + 4 * half;
+                const size_t o = (size_t)gm * p.n + gn;
+                const float d[4] = {acc[i][j][4 * g] * rs, acc[i][j][4 * g + 1] * rs, acc[i][j][4 * g + 2] * rs,
+                                    acc[i][j][4 * g + 3] * rs};
+                if (vec_ok && gn + 3 < p.n) {
+                    if constexpr (OUT_F32)
+                        *reinterpret_cast<float4_t*>(static_cast<float*>(p.c) + o) = float4_t{d[0], d[1], d[2], d[3]};
+                    else
+                        *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(p.c) + o) =
+                            uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (gn + r < p.n) {
+                            if constexpr (OUT_F32)
+                                static_cast<float*>(p.c)[o + r] = d[r];
+                            else
+                                static_cast<uint16_t*>(p.c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int NW, int WPE>
+hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
+    const size_t lds = 2 * (size_t)BM * kLdsRow;
+    PrefillArgs p = a;
+    p.tiles_m = (a.m + BM - 1) / BM;
+    p.tiles_n = (a.n + 64 * NW - 1) / (64 * NW);
+    const dim3 grid(p.tiles_m * p.tiles_n);
+    if (out_f32)
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, WPE, true>), grid, dim3(64 * NW), lds, s, p);
+    else
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, WPE, false>), grid, dim3(64 * NW), lds, s, p);
+    return hipGetLastError();
+}
+
 template <int BM, int BN, int WGM, int WGN>
 hipError_t launch_tile(const PrefillArgs& a, bool a_f32, bool has_awq, bool out_f32, hipStream_t s) {
     constexpr int NT = 64 * WGM * WGN;
@@ -276,7 +558,7 @@ hipError_t launch_tile(const PrefillArgs& a, bool a_f32, bool has_awq, bool out_
     p.tiles_m = (a.m + BM - 1) / BM;
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n);
-#define QW35_PF(AF, AW, OF)                                                                              \
+#define QW35_PF(AF, AW, OF) \
     hipLaunchKernelGGL((gf4_prefill_kernel<BM, BN, WGM, WGN, AF, AW, OF>), grid, dim3(NT), lds, s, p)
     if (a_f32) {
         if (has_awq) {
@@ -310,8 +592,12 @@ int num_cus() {
 
 }  // namespace
 
+size_t gf4_prefill_workspace_bytes(int m, int k) {
+    return ((size_t)m * k * 2 + 255) / 256 * 256 + (size_t)m * 4;
+}
+
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                              int m, int out_f32, hipStream_t stream) {
+                              int m, int out_f32, void* workspace, hipStream_t stream) {
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
     p.a = a;
@@ -320,10 +606,36 @@ hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int
     p.m = m;
     p.n = rows;
     p.k = k;
-    const bool af = a_f32 != 0, aw = awq != nullptr, of = out_f32 != 0;
+    bool af = a_f32 != 0, aw = awq != nullptr;
+    const bool of = out_f32 != 0;
+    const bool staged = workspace != nullptr;
+    if (staged) {
+        uint16_t* a16 = static_cast<uint16_t*>(workspace);
+        float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ((size_t)m * k * 2 + 255) / 256 * 256);
+#define QW35_STAGE(AF, AW) \
+    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, a16, rs)
+        if (af) {
+            if (aw) QW35_STAGE(true, true); else QW35_STAGE(true, false);
+        } else {
+            if (aw) QW35_STAGE(false, true); else QW35_STAGE(false, false);
+        }
+#undef QW35_STAGE
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        p.a = a16;
+        p.awq = nullptr;
+        p.row_scale = rs;
+        af = false;
+        aw = false;
+    }
     // Largest tile that still gives every CU a block.
     const long cus = num_cus();
     auto tiles = [&](int bm, int bn) { return (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn); };
+    if (staged) {
+        if (tiles(128, 256) >= cus) return launch_f16_tile<128, 4, 1>(p, of, stream);
+        if (tiles(64, 256) >= cus) return launch_f16_tile<64, 4, 2>(p, of, stream);
+        return launch_f16_tile<32, 4, 2>(p, of, stream);
+    }
     if (!af && tiles(256, 128) >= cus) return launch_tile<256, 128, 4, 2>(p, af, aw, of, stream);
     if (tiles(128, 128) >= cus) return launch_tile<128, 128, 2, 2>(p, af, aw, of, stream);
     return launch_tile<64, 64, 2, 2>(p, af, aw, of, stream);

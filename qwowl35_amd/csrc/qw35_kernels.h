@@ -60,7 +60,10 @@ hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, h
 // GF4 prefill dequant-matmul on bf16 MFMA:
 //   C[m][n] = sum_k bf16_rne(awq[k] * A[m][k]) * W[n][k],  fp32 accumulation.
 // a: [m][k] bf16 (a_f32 == 0) or fp32; c: [m][rows] bf16 RNE (out_f32 == 0) or fp32.
+// workspace (nullable, gf4_prefill_workspace_bytes(m, k) bytes, 256-byte aligned):
+// stage A as fp16 with per-row power-of-two scales and contract on fp16 MFMA.
+size_t gf4_prefill_workspace_bytes(int m, int k);
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                              int m, int out_f32, hipStream_t stream);
+                              int m, int out_f32, void* workspace, hipStream_t stream);
 
 }  // namespace qw35

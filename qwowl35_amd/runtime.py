@@ -128,13 +128,23 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
     return dst
 
 
+def prefill_workspace(n_tokens: int, k: int, device="cuda") -> torch.Tensor:
+    """Device workspace for ``matmul_prefill`` (256-byte aligned uint8)."""
+    n = int(_ffi.load().qw35_hip_matmul_prefill_workspace_size(n_tokens, k))
+    if n == 0:
+        raise Qw35Error(f"prefill workspace: unsupported shape n_tokens={n_tokens}, k={k}")
+    return torch.empty(n, dtype=torch.uint8, device=device)  # the caching allocator aligns to 512 B
+
+
 def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = None,
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
-                   stream=None) -> torch.Tensor:
-    """``C[t] = bf16(awq * a[t]) @ W^T`` on bf16 MFMA for a GF4 weight (``encodeTiledKMatmul``).
+                   workspace: torch.Tensor | None | bool = True, stream=None) -> torch.Tensor:
+    """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4 weight (``encodeTiledKMatmul``).
 
     ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
     ``out_dtype`` (bfloat16, rounded to nearest even, or float32).
+    ``workspace``: True (allocate one), a tensor from ``prefill_workspace``, or
+    None/False for the path without staging (bf16 MFMA).
     """
     if a.dim() != 2 or not a.is_cuda or not a.is_contiguous() or a.dtype not in (torch.bfloat16, torch.float32):
         raise Qw35Error("matmul_prefill: a must be a contiguous 2-D bf16/fp32 device tensor")
@@ -149,8 +159,13 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
         raise Qw35Error("matmul_prefill: dst must be a contiguous [n_tokens, rows] tensor of out_dtype")
     a_dt = _ffi.DTYPE_BF16 if a.dtype == torch.bfloat16 else _ffi.DTYPE_F32
     c_dt = _ffi.DTYPE_BF16 if out_dtype == torch.bfloat16 else _ffi.DTYPE_F32
+    if workspace is True:
+        workspace = prefill_workspace(n, w.k, device=a.device)
+    elif workspace is False:
+        workspace = None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _ffi.call("qw35_hip_matmul_prefill", C.byref(w.view), _ptr(a), a_dt, _ptr(awq), _ptr(dst), c_dt, n,
-              _stream(stream))
+              _ptr(workspace), ws_bytes, _stream(stream))
     return dst
 
 

@@ -5,7 +5,9 @@ operands the kernel contracts, A' = bf16_rne(awq * A) and the GF4 weights
 (exact in bf16).  Bars: fp32 output within 1e-3 relative L2; bf16 output
 within one bf16 ulp of the fp64 value per element, plus the fp32-accumulation
 allowance 2^-16 * sum_k |A'_k W_k| (a few percent of an ulp at these shapes).
-Full config-4 shapes are checked on a seeded sample of output rows.
+Full config-4 shapes are checked on a seeded sample of output rows.  Both
+paths are covered: staged (workspace: fp16 activations with per-token
+power-of-two scales, fp16 MFMA) and direct (bf16 MFMA).
 """
 from __future__ import annotations
 
@@ -50,7 +52,7 @@ def _bf16_out_ok(got_bf16_bits: np.ndarray, want: np.ndarray, a_eff: np.ndarray,
     return bool(np.all(err <= bound)), f"worst err/bound {worst:.3f}"
 
 
-def _case(cuda, m, n, k, seed, awq_on, out_f32, a_f32=False):
+def _case(cuda, m, n, k, seed, awq_on, out_f32, a_f32=False, staged=True):
     import torch
 
     rng = np.random.default_rng(seed)
@@ -69,7 +71,7 @@ def _case(cuda, m, n, k, seed, awq_on, out_f32, a_f32=False):
         a_dev = _bf16_tensor(bits, cuda)
         a_eff = om.prefill_operand(bits, awq)
     out = _rt().matmul_prefill(hw, a_dev, awq=_t(awq, cuda) if awq is not None else None,
-                               out_dtype=torch.float32 if out_f32 else torch.bfloat16)
+                               out_dtype=torch.float32 if out_f32 else torch.bfloat16, workspace=staged)
     want = a_eff.astype(np.float64) @ wdq.astype(np.float64).T
     if out_f32:
         got = out.cpu().numpy()
@@ -84,14 +86,49 @@ def _case(cuda, m, n, k, seed, awq_on, out_f32, a_f32=False):
                                    (64, 4096, 4096), (300, 520, 12288)])
 @pytest.mark.parametrize("awq_on", [False, True])
 @pytest.mark.parametrize("out_f32", [False, True])
-def test_prefill_parity(cuda, m, n, k, awq_on, out_f32):
-    _case(cuda, m, n, k, seed=m * 7 + n + k, awq_on=awq_on, out_f32=out_f32)
+@pytest.mark.parametrize("staged", [True, False])
+def test_prefill_parity(cuda, m, n, k, awq_on, out_f32, staged):
+    _case(cuda, m, n, k, seed=m * 7 + n + k, awq_on=awq_on, out_f32=out_f32, staged=staged)
 
 
 @pytest.mark.parametrize("m,n,k", [(5, 48, 256), (200, 384, 4096)])
 def test_prefill_fp32_activations(cuda, m, n, k):
-    _case(cuda, m, n, k, seed=3 + m, awq_on=True, out_f32=True, a_f32=True)
-    _case(cuda, m, n, k, seed=4 + m, awq_on=False, out_f32=False, a_f32=True)
+    for staged in (True, False):
+        _case(cuda, m, n, k, seed=3 + m, awq_on=True, out_f32=True, a_f32=True, staged=staged)
+        _case(cuda, m, n, k, seed=4 + m, awq_on=False, out_f32=False, a_f32=True, staged=staged)
+
+
+def test_prefill_staged_extreme_token_scales(cuda):
+    """Staging scales each token row by its own power of two: rows of very
+    different magnitude (and an all-zero row) keep their relative accuracy."""
+    import torch
+
+    rng = np.random.default_rng(31)
+    n, k, m = 96, 1024, 6
+    words = ogf4.gf4_pack(bf16_normal(rng, (n, k), 0.02))
+    hw = _rt().HipWeight.upload(words.view(np.uint8), om.TYPE_GF4, n, k)
+    a32 = rng.standard_normal((m, k), dtype=np.float32) * np.array([1e-6, 1.0, 3e4, 0.0, 1e-3, 2.5e8],
+                                                                    np.float32)[:, None]
+    bits = om.f32_to_bf16_bits(a32)
+    out = _rt().matmul_prefill(hw, _bf16_tensor(bits, cuda), out_dtype=torch.float32).cpu().numpy()
+    want = om.prefill_f64(ogf4.gf4_dequant(words), bits)
+    for r in range(m):
+        if r == 3:
+            assert np.all(out[r] == 0.0)
+        else:
+            assert om.rel_l2(out[r], want[r]) <= 1e-6, r
+
+
+def test_prefill_workspace_validation(cuda):
+    import torch
+
+    rng = np.random.default_rng(2)
+    words = ogf4.gf4_pack(bf16_normal(rng, (32, 256), 0.02))
+    hw = _rt().HipWeight.upload(words.view(np.uint8), om.TYPE_GF4, 32, 256)
+    a = torch.zeros((4, 256), dtype=torch.bfloat16, device=cuda)
+    small = torch.empty(64, dtype=torch.uint8, device=cuda)
+    with pytest.raises(_rt().Qw35Error, match="workspace"):
+        _rt().matmul_prefill(hw, a, workspace=small)
 
 
 def test_prefill_prefix_equals_shorter_chunk(cuda):
@@ -124,15 +161,17 @@ def test_prefill_config4_shapes(cuda, m, n, k):
     a = torch.randn((m, k), generator=g, device=cuda).to(torch.bfloat16)
     awq = torch.rand((k,), generator=g, device=cuda) * 1.5 + 0.5
     out = rt.matmul_prefill(hw, a, awq=awq)
+    direct = rt.matmul_prefill(hw, a, awq=awq, workspace=None)
     rows = np.sort(np.random.default_rng(m).choice(m, size=min(48, m), replace=False))
     words = hw.storage.cpu().numpy().view("<u4").reshape(n, k // 8)
     wdq = ogf4.gf4_dequant(words)
     a_bits = a.view(torch.int16).cpu().numpy().view(np.uint16)[rows]
     a_eff = om.prefill_operand(a_bits, awq.cpu().numpy())
     want = a_eff.astype(np.float64) @ wdq.astype(np.float64).T
-    got_bits = out.view(torch.int16).cpu().numpy().view(np.uint16)[rows]
-    ok, msg = _bf16_out_ok(got_bits, want, a_eff, wdq)
-    assert ok, msg
+    for res in (out, direct):
+        got_bits = res.view(torch.int16).cpu().numpy().view(np.uint16)[rows]
+        ok, msg = _bf16_out_ok(got_bits, want, a_eff, wdq)
+        assert ok, msg
 
 
 def test_matvec_batch_long_chunk_uses_prefill(cuda):
