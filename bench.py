@@ -156,7 +156,7 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
         for m in (128, 512, 2048):
             a = b.normal((m, k)).to(torch.bfloat16)
             c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
-            wsp = rt.prefill_workspace(m, k, device=b.dev)
+            wsp = rt.prefill_workspace(ws[0], m, device=b.dev)
             for path, work in (("", wsp), ("_direct", None)):
                 calls = [lambda s, w=w, work=work: rt.matmul_prefill(w, a, awq=awq, dst=c, workspace=work, stream=s)
                          for w in ws]

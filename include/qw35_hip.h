@@ -138,16 +138,23 @@ void qw35_hip_plan_destroy(void *plan);
  * QW35_HIP_DTYPE_F32; fp32 accumulation.  Replaces encodeMatvecBatch /
  * encodeTiledKMatmul for type 100 (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366,
  * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255).  GF4 only;
- * 1 <= n_tokens <= 65536. */
+ * 1 <= n_tokens <= 65536, rows <= 2^24. */
 #define QW35_HIP_DTYPE_F32 0u
 #define QW35_HIP_DTYPE_BF16 1u
-/* workspace: NULL, or device memory of qw35_hip_matmul_prefill_workspace_size
- * bytes (256-byte aligned, owned by the caller, not shared by concurrent
- * calls).  With a workspace the activations are first staged as fp16 with a
- * per-token power-of-two scale (exact for every value above 2^-28 of the
- * token's largest) and contracted on fp16 MFMA; without, the loader converts
- * them and contracts on bf16 MFMA.  Both compute the same products. */
-uint64_t qw35_hip_matmul_prefill_workspace_size(uint32_t n_tokens, uint64_t k);
+/* workspace: NULL, or device memory of
+ * qw35_hip_matmul_prefill_workspace_size(w, n_tokens) bytes (256-byte
+ * aligned, owned by the caller, not shared by concurrent calls).  With a
+ * workspace the activations are first staged as fp16 with a per-token
+ * power-of-two scale (exact for every value above 2^-28 of the token's
+ * largest) and contracted on fp16 MFMA; shapes with too few output tiles for
+ * the device also split K, with fp32 partial sums in the workspace reduced in
+ * a fixed order.  Without a workspace the loader converts the activations and
+ * contracts on bf16 MFMA.  Both compute the same products.  The size depends
+ * on the weight's shape and n_tokens (0: invalid weight or n_tokens); a
+ * smaller workspace that still holds the staged activations (2 bytes per
+ * activation plus 4 per token, each part rounded up to 256 bytes) is
+ * accepted and splits K less. */
+uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight *w, uint32_t n_tokens);
 int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
                             uint32_t c_dtype, uint32_t n_tokens, void *workspace, uint64_t workspace_bytes,
                             void *stream, char *err, uintptr_t err_len);

@@ -90,7 +90,7 @@ PROTOTYPES: dict[str, tuple] = {
     "qw35_hip_plan_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
     "qw35_hip_plan_size": (C.c_uint32, [C.c_void_p]),
     "qw35_hip_plan_destroy": (None, [C.c_void_p]),
-    "qw35_hip_matmul_prefill_workspace_size": (C.c_uint64, [C.c_uint32, C.c_uint64]),
+    "qw35_hip_matmul_prefill_workspace_size": (C.c_uint64, [C.c_void_p, C.c_uint32]),
     "qw35_hip_matmul_prefill": (
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,

@@ -352,9 +352,12 @@ int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint3
                : 0;
 }
 
-uint64_t qw35_hip_matmul_prefill_workspace_size(uint32_t n_tokens, uint64_t k) {
-    if (n_tokens < 1 || n_tokens > 65536 || k == 0 || k > kMaxK) return 0;
-    return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)k);
+uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
+    char msg[8];
+    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || w->type_id != qw35::kTypeGF4 || n_tokens < 1 ||
+        n_tokens > 65536)
+        return 0;
+    return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
 }
 
 int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
@@ -374,6 +377,10 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         set_err(err, err_len, "matmul_prefill: n_tokens=%u must be in 1..65536", n_tokens);
         return 0;
     }
+    if (w->rows > (1ull << 24)) {  // keeps every launch grid within 2^31 blocks
+        set_err(err, err_len, "matmul_prefill: rows=%llu must be <= 16777216", (unsigned long long)w->rows);
+        return 0;
+    }
     if (!a || !c) {
         set_err(err, err_len, "matmul_prefill: null input or output");
         return 0;
@@ -383,7 +390,8 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         return 0;
     }
     if (workspace) {
-        const uint64_t need = qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->k);
+        const uint64_t need =
+            qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, qw35::PrefillCfg{32, 2, 1});
         if (workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
             set_err(err, err_len, "matmul_prefill: workspace must be 256-byte aligned and >= %llu bytes, got %llu",
                     (unsigned long long)need, (unsigned long long)workspace_bytes);
@@ -392,7 +400,7 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
     }
     return check_hip(qw35::launch_gf4_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
                                               awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace,
-                                              static_cast<hipStream_t>(stream)),
+                                              workspace ? workspace_bytes : 0, static_cast<hipStream_t>(stream)),
                      "matmul_prefill", err, err_len)
                ? 1
                : 0;

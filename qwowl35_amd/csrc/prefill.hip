@@ -22,6 +22,8 @@
 //   (the format of tools/qw35_cook_common.py:79 with c = q_raw ^ 4).
 // * Blocks are assigned XCD by XCD (consecutive block ids land on different
 //   XCDs), M-tile fastest, so the blocks that share a W tile share an L2.
+#include <cmath>
+
 #include "gf4_decode.h"
 #include "qw35_device.h"
 #include "qw35_kernels.h"
@@ -44,6 +46,8 @@ struct PrefillArgs {
     const float* row_scale;  // staged path: per token row, the inverse of its fp16 scale
     int m, n, k;
     int tiles_m, tiles_n;
+    int splits;              // staged path: K split this many ways (1: none)
+    int k_len;               // columns per split
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
@@ -356,8 +360,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 // Staged path: fp16 A'' (prefill_stage_kernel) against GF4 words decoded
 // straight from global memory into MFMA operand registers.
 //
-// * A block owns a BM x (64 * NW) tile of C.  Its NW waves split the weight
-//   rows (64 per wave) and all read the block's BM token rows from LDS, so every
+// * A block owns a BM x (32 * FN * NW) tile of C.  Its NW waves split the
+//   weight rows (32 * FN per wave) and all read the block's BM token rows from
+//   LDS, so every
 //   GF4 word is loaded and decoded (15 VALU ops, fp16, gf4_decode.h) by exactly
 //   one wave and the only LDS traffic is the token tile.
 // * v_mfma_f32_32x32x16_f16 with the weight tile as first operand: lane l
@@ -369,13 +374,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   column order, which the staging pass already wrote).
 // * Global loads run two steps ahead in two register stages; the token tile
 //   is double buffered in LDS, one barrier per step.
-template <int BM, int NW, int WPE, bool OUT_F32>
+template <int BM, int NW, int FN, int WPE, bool OUT_F32>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
     constexpr int NT = 64 * NW;
-    constexpr int BN = 64 * NW;
-    constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave
-    constexpr int FN = 2;                   // 32-row weight tiles per wave
+    constexpr int BN = 32 * FN * NW;
+    constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave; FN: 32-row weight tiles per wave
     constexpr int A_CHUNKS = BM * 8 / NT;   // 16-byte token chunks per thread per step
     constexpr int BUF = BM * kLdsRow;
     static_assert(BM % 32 == 0 && BM * 8 % NT == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
@@ -389,12 +393,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const int half = lane >> 5;
     const int l32 = lane & 31;
 
+    // Block -> (split, tile): the blocks of one K range are consecutive, and
+    // the XCD remap hands each XCD a contiguous run of them.
     const int tiles = p.tiles_m * p.tiles_n;
+    const int blocks = tiles * p.splits;
     int t = blockIdx.x;
-    if (tiles % kXcds == 0) t = (t % kXcds) * (tiles / kXcds) + t / kXcds;
+    if (blocks % kXcds == 0) t = (t % kXcds) * (blocks / kXcds) + t / kXcds;
+    const int split = t / tiles;
+    t -= split * tiles;
     const int m0 = (t % p.tiles_m) * BM;
-    const int n0 = (t / p.tiles_m) * BN + wave * 64;
+    const int n0 = (t / p.tiles_m) * BN + wave * 32 * FN;
     const int K = p.k;
+    const int k_begin = split * p.k_len;
     const int words_per_row = K >> 3;
     const Gf4Consts gc = gf4_consts();
 
@@ -406,13 +416,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         const int row = c >> 3;
         const int col = c & 7;
         const int gm = min(m0 + row, p.m - 1);
-        a_off[i] = ((uint32_t)gm * (uint32_t)K + (uint32_t)col * 8u) * 2u;
+        a_off[i] = ((uint32_t)gm * (uint32_t)K + (uint32_t)k_begin + (uint32_t)col * 8u) * 2u;
         a_lds[i] = row * kLdsRow + col * 16;
     }
     const uint32_t* w_src[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-        w_src[j] = p.w + (size_t)min(n0 + 32 * j + l32, p.n - 1) * words_per_row + 4 * half;
+        w_src[j] = p.w + (size_t)min(n0 + 32 * j + l32, p.n - 1) * words_per_row + (k_begin >> 3) + 4 * half;
     const uint8_t* a_base = static_cast<const uint8_t*>(p.a);
 
     typedef uint4_t Tokens[A_CHUNKS];
@@ -469,9 +479,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // words ring has four slots and the loop body covers four steps, so every
     // register set is loaded and consumed under one static name and nothing
     // loaded is copied across the loop back-edge (a copy would wait for the
-    // load).  K is a multiple of 4 * kBK (the host checks k % 256 == 0); the
-    // prefetches past the last step re-read it instead of branching.
-    const int KT = K / kBK;
+    // load).  Each split covers a multiple of 4 * kBK columns (the host checks
+    // k_len % 256 == 0); the prefetches past the last step re-read it instead
+    // of branching.
+    const int KT = p.k_len / kBK;
     uint8_t* buf0 = smem;
     uint8_t* buf1 = smem + BUF;
     Tokens t0, t1;
@@ -500,12 +511,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     }
 
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
-    const bool vec_ok = (p.n & 3) == 0;
+    // Split launches write unscaled fp32 partial sums, split s at
+    // c + s * m * n (OUT_F32 is then true); prefill_split_reduce finishes.
+    void* const c = OUT_F32 ? static_cast<void*>(static_cast<float*>(p.c) + (size_t)split * p.m * p.n) : p.c;
+    const bool vec_ok = (p.n & 3) == 0 && ((uintptr_t)p.c & 15) == 0;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         const int gm = m0 + 32 * i + l32;
         if (gm >= p.m) continue;
-        const float rs = p.row_scale[gm];
+        const float rs = p.splits > 1 ? 1.0f : p.row_scale[gm];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -516,18 +530,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                                     acc[i][j][4 * g + 3] * rs};
                 if (vec_ok && gn + 3 < p.n) {
                     if constexpr (OUT_F32)
-                        *reinterpret_cast<float4_t*>(static_cast<float*>(p.c) + o) = float4_t{d[0], d[1], d[2], d[3]};
+                        *reinterpret_cast<float4_t*>(static_cast<float*>(c) + o) = float4_t{d[0], d[1], d[2], d[3]};
                     else
-                        *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(p.c) + o) =
+                        *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
                             uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         if (gn + r < p.n) {
                             if constexpr (OUT_F32)
-                                static_cast<float*>(p.c)[o + r] = d[r];
+                                static_cast<float*>(c)[o + r] = d[r];
                             else
-                                static_cast<uint16_t*>(p.c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+                                static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
                         }
                     }
                 }
@@ -536,17 +550,70 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     }
 }
 
-template <int BM, int NW, int WPE>
+// C[m][n] = row_scale[m] * sum_s partial[s][m][n], splits summed in order.
+// One thread per 4 consecutive outputs of a row.
+constexpr int kReduceThreads = 256;
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const float* __restrict__ partial,
+                                                                       int splits, int m, int n,
+                                                                       const float* __restrict__ row_scale,
+                                                                       void* __restrict__ c) {
+    const int n4 = (n + 3) >> 2;
+    const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
+    if (idx >= (size_t)m * n4) return;
+    const int row = (int)(idx / n4);
+    const int col = (int)(idx - (size_t)row * n4) * 4;
+    const size_t o = (size_t)row * n + col;
+    const size_t stride = (size_t)m * n;
+    const float rs = row_scale[row];
+    const int cnt = min(4, n - col);
+    float d[4] = {0.f, 0.f, 0.f, 0.f};
+    const bool vec = (n & 3) == 0 && ((uintptr_t)c & 15) == 0;
+    if (vec) {
+        for (int sp = 0; sp < splits; ++sp) {
+            const float4_t v = *reinterpret_cast<const float4_t*>(partial + sp * stride + o);
+            d[0] += v.x;
+            d[1] += v.y;
+            d[2] += v.z;
+            d[3] += v.w;
+        }
+    } else {
+        for (int sp = 0; sp < splits; ++sp)
+            for (int r = 0; r < cnt; ++r) d[r] += partial[sp * stride + o + r];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d[r] *= rs;
+    if (vec) {
+        if constexpr (OUT_F32) {
+            *reinterpret_cast<float4_t*>(static_cast<float*>(c) + o) = float4_t{d[0], d[1], d[2], d[3]};
+        } else {
+            typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
+                uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
+        }
+    } else {
+        for (int r = 0; r < cnt; ++r) {
+            if constexpr (OUT_F32)
+                static_cast<float*>(c)[o + r] = d[r];
+            else
+                static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+        }
+    }
+}
+
+template <int BM, int NW, int FN, int WPE>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
+    constexpr int BN = 32 * FN * NW;
     const size_t lds = 2 * (size_t)BM * kLdsRow;
     PrefillArgs p = a;
     p.tiles_m = (a.m + BM - 1) / BM;
-    p.tiles_n = (a.n + 64 * NW - 1) / (64 * NW);
-    const dim3 grid(p.tiles_m * p.tiles_n);
+    p.tiles_n = (a.n + BN - 1) / BN;
+    const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (out_f32)
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, WPE, true>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true>), grid, dim3(64 * NW), lds, s, p);
     else
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, WPE, false>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false>), grid, dim3(64 * NW), lds, s, p);
     return hipGetLastError();
 }
 
@@ -590,14 +657,58 @@ int num_cus() {
     return cus;
 }
 
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
 }  // namespace
 
-size_t gf4_prefill_workspace_bytes(int m, int k) {
-    return ((size_t)m * k * 2 + 255) / 256 * 256 + (size_t)m * 4;
+// Staged-path launch shape from a cost model fitted to MI355X measurements of
+// the Qwen3.5-9B projection shapes (M = 128..2048): the grid runs in
+// ceil(blocks / CUs) rounds; a block costs 0.108 us per MFLOP of MFMA work
+// plus 29.9 us per MB it streams (its token tile once per k step, its weight
+// slab once); a K split adds 0.5 us per MB of fp32 partial sums (written,
+// read back by the reduction, one more launch).  Over the measured shapes the
+// pick is the fastest or within 5% of it.
+PrefillCfg plan_gf4_prefill(int m, int rows, int k) {
+    constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9, kUsPerPartialMB = 0.5;
+    const int cus = num_cus();
+    const int chunks = k / 256;
+    static constexpr int kShapes[][2] = {{128, 4}, {128, 2}, {64, 4}, {64, 2}, {32, 2}};
+    PrefillCfg best{32, 2, 1};
+    double best_us = 0;
+    for (const auto& sh : kShapes) {
+        const int bm = sh[0], fn = sh[1], bn = 128 * fn;
+        if (bm > 32 && m <= bm / 2) continue;  // half the token tile or more would be padding
+        const long tiles = (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn);
+        for (int sp = 1; sp <= 16 && sp <= chunks; ++sp) {
+            if (chunks % sp != 0 || (sp > 1 && k / sp < 512)) continue;
+            const long blocks = tiles * sp;
+            const double rounds = (double)((blocks + cus - 1) / cus);
+            const double k_len = (double)k / sp;
+            double us = rounds * (kUsPerMflop * 2.0 * bm * bn * k_len * 1e-6 + kUsPerMB * k_len * (2.0 * bm + 0.5 * bn) * 1e-6);
+            if (sp > 1) us += kUsPerPartialMB * 4.0 * sp * m * rows * 1e-6;
+            if (best_us == 0 || us < best_us) {
+                best_us = us;
+                best = {bm, fn, sp};
+            }
+            if (blocks >= cus) break;  // more splits only add partial sums
+        }
+    }
+    return best;
 }
 
-hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                              int m, int out_f32, void* workspace, hipStream_t stream) {
+size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg) {
+    size_t b = round256((size_t)m * k * 2) + round256((size_t)m * 4);
+    if (cfg.splits > 1) b += (size_t)cfg.splits * m * rows * 4;
+    return b;
+}
+
+size_t gf4_prefill_workspace_bytes(int m, int rows, int k) {
+    return gf4_prefill_workspace_bytes(m, rows, k, plan_gf4_prefill(m, rows, k));
+}
+
+hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
+                                  void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
+                                  hipStream_t stream) {
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
     p.a = a;
@@ -606,12 +717,16 @@ hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int
     p.m = m;
     p.n = rows;
     p.k = k;
+    p.splits = 1;
+    p.k_len = k;
     bool af = a_f32 != 0, aw = awq != nullptr;
     const bool of = out_f32 != 0;
-    const bool staged = workspace != nullptr;
-    if (staged) {
-        uint16_t* a16 = static_cast<uint16_t*>(workspace);
-        float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ((size_t)m * k * 2 + 255) / 256 * 256);
+    if (workspace) {
+        if (cfg.splits < 1 || k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0) return hipErrorInvalidValue;
+        uint8_t* ws = static_cast<uint8_t*>(workspace);
+        uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
+        float* rs = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2));
+        float* partial = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2) + round256((size_t)m * 4));
 #define QW35_STAGE(AF, AW) \
     hipLaunchKernelGGL((prefill_stage_kernel<AF, AW>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, a16, rs)
         if (af) {
@@ -620,25 +735,53 @@ hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int
             if (aw) QW35_STAGE(false, true); else QW35_STAGE(false, false);
         }
 #undef QW35_STAGE
-        const hipError_t e = hipGetLastError();
+        hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         p.a = a16;
         p.awq = nullptr;
         p.row_scale = rs;
-        af = false;
-        aw = false;
+        p.splits = cfg.splits;
+        p.k_len = k / cfg.splits;
+        const bool split = cfg.splits > 1;
+        if (split) p.c = partial;
+        const bool kf32 = of || split;
+        switch (cfg.bm * 10 + cfg.fn) {
+            case 1282: e = launch_f16_tile<128, 4, 2, 1>(p, kf32, stream); break;
+            case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
+            case 642: e = launch_f16_tile<64, 4, 2, 2>(p, kf32, stream); break;
+            case 644: e = launch_f16_tile<64, 4, 4, 2>(p, kf32, stream); break;
+            case 322: e = launch_f16_tile<32, 4, 2, 2>(p, kf32, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+        if (e != hipSuccess || !split) return e;
+        const size_t threads = (size_t)m * ((rows + 3) / 4);
+        const dim3 grid((unsigned)((threads + kReduceThreads - 1) / kReduceThreads));
+        if (of)
+            hipLaunchKernelGGL((prefill_split_reduce<true>), grid, dim3(kReduceThreads), 0, stream, partial,
+                               cfg.splits, m, rows, rs, c);
+        else
+            hipLaunchKernelGGL((prefill_split_reduce<false>), grid, dim3(kReduceThreads), 0, stream, partial,
+                               cfg.splits, m, rows, rs, c);
+        return hipGetLastError();
     }
-    // Largest tile that still gives every CU a block.
+    // Direct path: largest tile that still gives every CU a block.
     const long cus = num_cus();
     auto tiles = [&](int bm, int bn) { return (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn); };
-    if (staged) {
-        if (tiles(128, 256) >= cus) return launch_f16_tile<128, 4, 1>(p, of, stream);
-        if (tiles(64, 256) >= cus) return launch_f16_tile<64, 4, 2>(p, of, stream);
-        return launch_f16_tile<32, 4, 2>(p, of, stream);
-    }
     if (!af && tiles(256, 128) >= cus) return launch_tile<256, 128, 4, 2>(p, af, aw, of, stream);
     if (tiles(128, 128) >= cus) return launch_tile<128, 128, 2, 2>(p, af, aw, of, stream);
     return launch_tile<64, 64, 2, 2>(p, af, aw, of, stream);
+}
+
+hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
+                              int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    PrefillCfg cfg = plan_gf4_prefill(m, rows, k);
+    // A workspace sized for another token count may not hold this call's
+    // partial sums: split less (ultimately not at all) rather than fail.
+    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
+        do --cfg.splits;
+        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
+    }
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream);
 }
 
 }  // namespace qw35

@@ -57,13 +57,25 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
 unsigned stream_read_blocks(uint64_t bytes);
 hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 
-// GF4 prefill dequant-matmul on bf16 MFMA:
+// GF4 prefill dequant-matmul:
 //   C[m][n] = sum_k bf16_rne(awq[k] * A[m][k]) * W[n][k],  fp32 accumulation.
 // a: [m][k] bf16 (a_f32 == 0) or fp32; c: [m][rows] bf16 RNE (out_f32 == 0) or fp32.
-// workspace (nullable, gf4_prefill_workspace_bytes(m, k) bytes, 256-byte aligned):
-// stage A as fp16 with per-row power-of-two scales and contract on fp16 MFMA.
-size_t gf4_prefill_workspace_bytes(int m, int k);
+// workspace (nullable, 256-byte aligned, at least the unsplit size
+// gf4_prefill_workspace_bytes(m, rows, k, {.., 1})): stage A as fp16 with
+// per-row power-of-two scales and contract on fp16 MFMA, split over K (fp32
+// partials in the workspace) when the tiles alone would leave CUs idle and
+// workspace_bytes holds the partials.  Without a workspace: bf16 MFMA, no split.
+struct PrefillCfg {
+    int bm;      // tokens per block: 128, 64 or 32
+    int fn;      // 32-row weight tiles per wave (4 waves per block): 2 or 4 (4 needs bm >= 64)
+    int splits;  // K splits; k / splits must be a multiple of 256
+};
+PrefillCfg plan_gf4_prefill(int m, int rows, int k);
+size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg);
+size_t gf4_prefill_workspace_bytes(int m, int rows, int k);
+hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
+                                  void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream);
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                              int m, int out_f32, void* workspace, hipStream_t stream);
+                              int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace qw35

@@ -128,11 +128,11 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
     return dst
 
 
-def prefill_workspace(n_tokens: int, k: int, device="cuda") -> torch.Tensor:
-    """Device workspace for ``matmul_prefill`` (256-byte aligned uint8)."""
-    n = int(_ffi.load().qw35_hip_matmul_prefill_workspace_size(n_tokens, k))
+def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tensor:
+    """Device workspace for ``matmul_prefill`` of ``n_tokens`` tokens on ``w`` (256-byte aligned uint8)."""
+    n = int(_ffi.load().qw35_hip_matmul_prefill_workspace_size(C.byref(w.view), n_tokens))
     if n == 0:
-        raise Qw35Error(f"prefill workspace: unsupported shape n_tokens={n_tokens}, k={k}")
+        raise Qw35Error(f"prefill workspace: unsupported weight or n_tokens={n_tokens}")
     return torch.empty(n, dtype=torch.uint8, device=device)  # the caching allocator aligns to 512 B
 
 
@@ -160,7 +160,7 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
     a_dt = _ffi.DTYPE_BF16 if a.dtype == torch.bfloat16 else _ffi.DTYPE_F32
     c_dt = _ffi.DTYPE_BF16 if out_dtype == torch.bfloat16 else _ffi.DTYPE_F32
     if workspace is True:
-        workspace = prefill_workspace(n, w.k, device=a.device)
+        workspace = prefill_workspace(w, n, device=a.device)
     elif workspace is False:
         workspace = None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0

@@ -7,7 +7,9 @@ within one bf16 ulp of the fp64 value per element, plus the fp32-accumulation
 allowance 2^-16 * sum_k |A'_k W_k| (a few percent of an ulp at these shapes).
 Full config-4 shapes are checked on a seeded sample of output rows.  Both
 paths are covered: staged (workspace: fp16 activations with per-token
-power-of-two scales, fp16 MFMA) and direct (bf16 MFMA).
+power-of-two scales, fp16 MFMA) and direct (bf16 MFMA).  The small shapes
+take the staged path's K split (fp32 partial sums in the workspace, then an
+ordered reduction), including a row count that is not a multiple of 4.
 """
 from __future__ import annotations
 
@@ -83,7 +85,7 @@ def _case(cuda, m, n, k, seed, awq_on, out_f32, a_f32=False, staged=True):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 256), (9, 64, 256), (37, 100, 512), (130, 272, 1024),
-                                   (64, 4096, 4096), (300, 520, 12288)])
+                                   (50, 302, 2048), (64, 4096, 4096), (300, 520, 12288)])
 @pytest.mark.parametrize("awq_on", [False, True])
 @pytest.mark.parametrize("out_f32", [False, True])
 @pytest.mark.parametrize("staged", [True, False])
@@ -132,7 +134,10 @@ def test_prefill_workspace_validation(cuda):
 
 
 def test_prefill_prefix_equals_shorter_chunk(cuda):
-    """Rows of C depend only on their own token: a chunk's first rows equal a shorter chunk's."""
+    """Rows of C depend only on their own token: a chunk's first rows equal a
+    shorter chunk's.  Bit for bit on the direct path (every tile shape sums k
+    in the same order); the staged path may split K differently for the two
+    token counts, which only changes fp32 rounding of the partial sums."""
     import torch
 
     rng = np.random.default_rng(12)
@@ -140,9 +145,12 @@ def test_prefill_prefix_equals_shorter_chunk(cuda):
     words = ogf4.gf4_pack(bf16_normal(rng, (n, k), 0.02))
     hw = _rt().HipWeight.upload(words.view(np.uint8), om.TYPE_GF4, n, k)
     a = _bf16_tensor(om.f32_to_bf16_bits(rng.standard_normal((700, k), dtype=np.float32)), cuda)
-    long = _rt().matmul_prefill(hw, a, out_dtype=torch.float32)
-    short = _rt().matmul_prefill(hw, a[:33].contiguous(), out_dtype=torch.float32)
+    long = _rt().matmul_prefill(hw, a, out_dtype=torch.float32, workspace=None)
+    short = _rt().matmul_prefill(hw, a[:33].contiguous(), out_dtype=torch.float32, workspace=None)
     assert torch.equal(long[:33], short)
+    long = _rt().matmul_prefill(hw, a, out_dtype=torch.float32).cpu().numpy()
+    short = _rt().matmul_prefill(hw, a[:33].contiguous(), out_dtype=torch.float32).cpu().numpy()
+    assert om.rel_l2(long[:33], short) <= 1e-6
 
 
 @pytest.mark.parametrize("m", [128, 512, 2048])
