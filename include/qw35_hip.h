@@ -179,6 +179,15 @@ uint32_t qw35_hip_stream_read_sink_len(uint64_t bytes);
 int qw35_hip_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, void *stream, char *err,
                          uintptr_t err_len);
 
+/* MFMA throughput probe: n_workgroups x 4 waves each run `iters` rounds of 8
+ * independent v_mfma_f32_32x32x16_f16 (the prefill kernel's instruction;
+ * 32768 flops each) with no memory traffic, so a timed call measures the
+ * sustained fp16 MFMA rate (flops = n_workgroups * iters * 1048576).  sink:
+ * device fp32 [n_workgroups * 256].  No counterpart in the reference: it
+ * measures the ceiling the prefill utilisation is reported against. */
+int qw35_hip_mfma_probe(uint32_t n_workgroups, uint32_t iters, float *sink, void *stream, char *err,
+                        uintptr_t err_len);
+
 /* Wait for the stream and report any asynchronous device error.  Replaces
  * qw35_metal_runtime_sync (Qw35FFI.h:71-72). */
 int qw35_hip_sync(void *stream, char *err, uintptr_t err_len);

@@ -103,6 +103,7 @@ PROTOTYPES: dict[str, tuple] = {
     ),
     "qw35_hip_stream_read_sink_len": (C.c_uint32, [C.c_uint64]),
     "qw35_hip_stream_read": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
+    "qw35_hip_mfma_probe": (C.c_int, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
     "qw35_hip_sync": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
 }
 

@@ -455,6 +455,22 @@ int qw35_hip_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, void* 
                : 0;
 }
 
+int qw35_hip_mfma_probe(uint32_t n_workgroups, uint32_t iters, float* sink, void* stream, char* err,
+                        uintptr_t err_len) {
+    if (!sink || n_workgroups < 1 || n_workgroups > 65536 || iters < 1 || iters > 1000000) {
+        set_err(err, err_len, "mfma_probe: null sink, or n_workgroups outside 1..65536 or iters outside 1..1000000");
+        return 0;
+    }
+    if ((uintptr_t)sink & 3u) {
+        set_err(err, err_len, "mfma_probe: sink must be 4-byte aligned");
+        return 0;
+    }
+    return check_hip(qw35::launch_mfma_probe(n_workgroups, iters, sink, static_cast<hipStream_t>(stream)),
+                     "mfma_probe", err, err_len)
+               ? 1
+               : 0;
+}
+
 int qw35_hip_sync(void* stream, char* err, uintptr_t err_len) {
     hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     if (e == hipSuccess) e = hipGetLastError();

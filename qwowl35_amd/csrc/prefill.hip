@@ -644,6 +644,36 @@ hipError_t launch_tile(const PrefillArgs& a, bool a_f32, bool has_awq, bool out_
     return hipGetLastError();
 }
 
+// MFMA throughput probe: each wave runs `iters` rounds of 8 independent
+// v_mfma_f32_32x32x16_f16 (the prefill kernel's instruction) with no memory
+// traffic; one float per thread goes to sink so the work stays live.
+constexpr int kProbeThreads = 256;
+
+__global__ __launch_bounds__(kProbeThreads) void mfma_probe_kernel(int iters, float* __restrict__ sink) {
+    typedef float float16_t __attribute__((ext_vector_type(16)));
+    half8_t a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (_Float16)((float)((threadIdx.x + i) & 15) * 0x1p-12f);
+        b[i] = (_Float16)((float)(i + 1) * 0x1p-10f);
+    }
+    float16_t acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[j][r];
+    sink[(size_t)blockIdx.x * kProbeThreads + threadIdx.x] = s;
+}
+
 int num_cus() {
     static int cus = [] {
         int dev = 0, n = 0;
@@ -746,7 +776,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         if (split) p.c = partial;
         const bool kf32 = of || split;
         switch (cfg.bm * 10 + cfg.fn) {
-            case 1282: e = launch_f16_tile<128, 4, 2, 1>(p, kf32, stream); break;
+            case 1282: e = launch_f16_tile<128, 4, 2, 2>(p, kf32, stream); break;
             case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
             case 642: e = launch_f16_tile<64, 4, 2, 2>(p, kf32, stream); break;
             case 644: e = launch_f16_tile<64, 4, 4, 2>(p, kf32, stream); break;
@@ -770,6 +800,11 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     if (!af && tiles(256, 128) >= cus) return launch_tile<256, 128, 4, 2>(p, af, aw, of, stream);
     if (tiles(128, 128) >= cus) return launch_tile<128, 128, 2, 2>(p, af, aw, of, stream);
     return launch_tile<64, 64, 2, 2>(p, af, aw, of, stream);
+}
+
+hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(workgroups), dim3(kProbeThreads), 0, stream, (int)iters, sink);
+    return hipGetLastError();
 }
 
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,

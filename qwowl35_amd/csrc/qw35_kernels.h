@@ -65,6 +65,10 @@ hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, h
 // per-row power-of-two scales and contract on fp16 MFMA, split over K (fp32
 // partials in the workspace) when the tiles alone would leave CUs idle and
 // workspace_bytes holds the partials.  Without a workspace: bf16 MFMA, no split.
+// MFMA throughput probe: workgroups x 4 waves x iters x 8 v_mfma_f32_32x32x16_f16
+// (32768 flops each); sink holds workgroups * 256 floats.
+hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream);
+
 struct PrefillCfg {
     int bm;      // tokens per block: 128, 64 or 32
     int fn;      // 32-row weight tiles per wave (4 waves per block): 2 or 4 (4 needs bm >= 64)

@@ -301,5 +301,18 @@ def stream_read(buf: torch.Tensor, sink: torch.Tensor | None = None, stream=None
     return sink
 
 
+MFMA_PROBE_FLOPS_PER_WG_ITER = 4 * 8 * 32768  # waves x MFMAs per round x flops per 32x32x16 MFMA
+
+
+def mfma_probe(n_workgroups: int, iters: int, sink: torch.Tensor | None = None, stream=None,
+               device="cuda") -> torch.Tensor:
+    """MFMA throughput probe (fp16 32x32x16, no memory traffic): the work is
+    ``n_workgroups * iters * MFMA_PROBE_FLOPS_PER_WG_ITER`` flops; returns the sink."""
+    if sink is None:
+        sink = torch.empty(n_workgroups * 256, dtype=torch.float32, device=device)
+    _ffi.call("qw35_hip_mfma_probe", n_workgroups, iters, _ptr(sink), _stream(stream))
+    return sink
+
+
 def sync(stream=None) -> None:
     _ffi.call("qw35_hip_sync", _stream(stream))

@@ -205,6 +205,15 @@ def test_plan_null_handles(lib):
         _ffi.call("qw35_hip_plan_launch", None, None)
 
 
+def test_mfma_probe_validates(lib):
+    with pytest.raises(_ffi.Qw35Error, match="n_workgroups"):
+        _ffi.call("qw35_hip_mfma_probe", 0, 10, C.c_void_p(4096), None)
+    with pytest.raises(_ffi.Qw35Error, match="iters"):
+        _ffi.call("qw35_hip_mfma_probe", 4, 0, C.c_void_p(4096), None)
+    with pytest.raises(_ffi.Qw35Error, match="null sink"):
+        _ffi.call("qw35_hip_mfma_probe", 4, 10, None, None)
+
+
 def test_stream_read_validates(lib):
     assert lib.qw35_hip_stream_read_sink_len(16) >= 1
     with pytest.raises(_ffi.Qw35Error, match="zero bytes"):

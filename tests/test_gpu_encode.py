@@ -118,6 +118,30 @@ def test_quantize_then_gemv_roundtrip(cuda):
         assert om.rel_l2(y, om.matvec_f64(deq, x)) <= 1e-3, name
 
 
+def test_mfma_probe_sums(cuda):
+    """Every lane's 8 accumulators hold iters * sum_k a_k b_k of exact small
+    fp16 products, so the sink is a closed form of the lane index."""
+    rt = _rt()
+    iters = 64
+    sink = rt.mfma_probe(3, iters).cpu().numpy().reshape(3, 256)
+    # lane l of a wave supplies A row l % 32 = ((l + i) & 15) * 2^-12 for its 8 k values
+    # (i = 0..7, k block 8 * (l // 32)); B column j = (i + 1) * 2^-10 for every column.
+    # D[row][col] = sum over 16 k of A[row][k] B[k][col]; each lane sums its 16 D values.
+    a = np.array([[((t + i) & 15) * 2.0 ** -12 for i in range(8)] for t in range(64)])
+    b = np.array([(i + 1) * 2.0 ** -10 for i in range(8)])
+    d = np.zeros((32, 32))
+    for l in range(64):
+        for i in range(8):
+            d[l % 32, :] += a[l, i] * b[i]  # k = 8 * (l // 32) + i contributes A[l%32][k] * B[k][*]
+    want = np.zeros(64)
+    for l in range(64):
+        rows = [8 * (r // 4) + 4 * (l // 32) + r % 4 for r in range(16)]
+        want[l] = 8 * iters * sum(d[rr, l % 32] for rr in rows)
+    for w in range(3):
+        for wave in range(4):
+            np.testing.assert_allclose(sink[w, 64 * wave:64 * wave + 64], want, rtol=1e-5)
+
+
 @pytest.mark.parametrize("nbytes", [16, 4096 + 48, 25_165_824])
 def test_stream_read_probe_reads_every_word(cuda, nbytes):
     """The read probe's per-workgroup XOR digests fold to the XOR of all words."""
