@@ -55,9 +55,7 @@ __device__ __forceinline__ Gf4Consts gf4_consts() {
 
 // v_bitop3_b32 with truth table 0x6a: (a & b) ^ c.
 __device__ __forceinline__ uint32_t and_xor(uint32_t a, uint32_t mask, uint32_t bits) {
-    uint32_t r;
-    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
-    return r;
+    return __builtin_amdgcn_bitop3_b32(a, mask, bits, 0x6a);
 }
 
 // One GF4 word -> MFMA B operand: 8 exact fp16 weights in column order
@@ -79,6 +77,30 @@ __device__ __forceinline__ half8_t gf4_word_to_b(uint32_t w, const Gf4Consts& c)
     const half2_t s2 = as_half2(__builtin_amdgcn_perm(w, w, 0x000C000Cu));
     const uint4_t u = {as_u32(e0 * s2), as_u32(e1 * s2), as_u32(e2 * s2), as_u32(e3 * s2)};
     return __builtin_bit_cast(half8_t, u);
+}
+
+// One GF4 word -> 8 biased exact fp16 values P_i = base_i + q_i in column
+// order 0,4,1,5,2,6,3,7 (6 VALU ops, no scale):
+//   (64 + q0, 1024 + q4) (8 + q1, 128 + q5) (64 + q2, 1024 + q6) (8 + q3, 128 + q7).
+// The level of column i is 4 - q_i = kGf4Bias[slot] - P_slot, where
+// kGf4Bias = 4 + base per slot; the word's weight is (4 - q_i) * s / 4.
+__device__ __forceinline__ half8_t gf4_word_to_biased(uint32_t w, const Gf4Consts& c) {
+    const uint32_t t1 = w >> 4;
+    const uint32_t t2 = w >> 10;
+    const uint4_t u = {and_xor(t1, c.mask_a, c.magic_a), and_xor(t1, c.mask_b, c.magic_b),
+                       and_xor(t2, c.mask_a, c.magic_a), and_xor(t2, c.mask_b, c.magic_b)};
+    return __builtin_bit_cast(half8_t, u);
+}
+
+// 4 + base of each slot of gf4_word_to_biased.
+__device__ __forceinline__ float gf4_bias(int slot) {
+    return (slot & 1) ? ((slot & 2) ? 132.0f : 1028.0f) : ((slot & 2) ? 12.0f : 68.0f);
+}
+
+// The word's e5m2 scale as fp32 (v_cvt_f32_bf8 of byte 0: OCP E5M2 is the
+// high byte of an IEEE binary16, so this is exactly fp16(b << 8)).
+__device__ __forceinline__ float gf4_scale_f32(uint32_t w) {
+    return __builtin_amdgcn_cvt_f32_bf8((int)w, 0);
 }
 
 }  // namespace qw35

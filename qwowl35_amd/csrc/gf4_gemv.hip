@@ -65,12 +65,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 //            group of 8 columns stored as x0 x4 x1 x5 x2 x6 x3 x7.
 //   zeros    64 halves (the A operand of rows past the batch).
 // After the KS blocks: the per-wave partial outputs.
-template <int NB, int CPW>
+template <int NB, int CPW, bool BD = false>
 struct WaveLds {
     static constexpr int kXposeBytes = 2 * 2048;
     static constexpr int kStride = CPW * 256 + 8;  // halves per activation row
     static constexpr int kActBytes = 2 * NB * kStride * 2;
-    static constexpr int kBytes = kXposeBytes + kActBytes + 128;
+    static constexpr int kXwOff = kXposeBytes + kActBytes + 128;
+    static constexpr int kXwBytes = BD ? NB * CPW * 32 * 4 : 0;  // per-word bias sums (block-diagonal form)
+    static constexpr int kBytes = kXwOff + kXwBytes;
 };
 
 template <int N, typename F>
@@ -84,15 +86,26 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Workgroup = KS waves covering 16*RT rows x all k.  Wave w owns the K-slice
 // [w*CPW*256, (w+1)*CPW*256) of all RT row tiles; its weight loads are issued
 // up front in the order (chunk, tile, matrix, half) and consumed in that order.
-template <int NB, int RT, int KS, int CPW, bool SWIGLU, bool HAS_AWQ>
+//
+// BD (block-diagonal form, batch 1..2): A row 4j+i holds the activations of
+// word j of the MFMA's four words only (i = 0,1: hi, lo of batch row 0;
+// i = 2,3: of batch row 1), so D[4j+i][n] is the partial of one word of row n,
+// and it lands in the lane that decoded that word.  B is then the biased
+// decode P = base + q (6 VALU ops, gf4_word_to_biased) and the word's scale is
+// applied once in fp32:
+//   sum_i (4 - q_i) x_i * s/4 = (s/4) * (X''_w - D_hi - D_lo),
+//   X''_w = sum_i (4 + base_i) * x_i    (row-independent, staged with the activations).
+template <int NB, int RT, int KS, int CPW, bool SWIGLU, bool HAS_AWQ, bool BD>
 __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int NM = SWIGLU ? 2 : 1;
-    using L = WaveLds<NB, CPW>;
+    static_assert(!BD || NB <= 2, "block-diagonal form holds two batch rows");
+    using L = WaveLds<NB, CPW, BD>;
     constexpr int STRIDE = L::kStride;
     constexpr int GPL = (CPW * 32 + 63) / 64;  // activation groups per lane per batch row
     constexpr int NTC = CPW * RT * NM;         // tile-chunks per wave
     constexpr int NLOADS = 2 * NTC;
+    constexpr int NKQ = BD ? 4 : 1;            // lane groups holding distinct partials
     static_assert(NLOADS <= 48, "vmcnt budget");
     const int k = args.k;
     const int rows = args.rows;
@@ -109,7 +122,8 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
     uint8_t* wblk = smem + (size_t)wave * L::kBytes;
     _Float16* xs = reinterpret_cast<_Float16*>(wblk + L::kXposeBytes);
     _Float16* zrow = xs + 2 * NB * STRIDE;
-    float* part = reinterpret_cast<float*>(smem + (size_t)KS * L::kBytes);  // [KS][RT][NM][NB][16]
+    float* xw = reinterpret_cast<float*>(wblk + L::kXwOff);                  // [NB][CPW*32] (BD)
+    float* part = reinterpret_cast<float*>(smem + (size_t)KS * L::kBytes);  // [KS][RT][NM][NB][NKQ][16]
     if (lane < 32) reinterpret_cast<uint32_t*>(zrow)[lane] = 0u;
 
     // 1. Activation slice (and AWQ) into registers, clamped, unused until step 3.
@@ -165,7 +179,8 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
 
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. Wave-private fp16 hi/lo activations with a per-wave power-of-two scale.
+    // 3. Wave-private fp16 hi/lo activations with a per-wave power-of-two scale
+    //    (and, BD, the per-word bias sums X'' of the same hi + lo values).
     wait_vmcnt<NLOADS>();
     float inv_scale[NB];
 #pragma unroll
@@ -192,15 +207,22 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
                 const float4_t v1 = xv[b][j][1] * sc;
                 const float e[8] = {v0[0], v1[0], v0[1], v1[1], v0[2], v1[2], v0[3], v1[3]};
                 uint32_t hi[4], lo[4];
+                float xsum = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const half2_t hh = h2(e[2 * q], e[2 * q + 1]);
+                    const half2_t ll = h2(e[2 * q] - (float)hh.x, e[2 * q + 1] - (float)hh.y);
                     hi[q] = as_u32(hh);
-                    lo[q] = as_u32(h2(e[2 * q] - (float)hh.x, e[2 * q + 1] - (float)hh.y));
+                    lo[q] = as_u32(ll);
+                    if constexpr (BD) {
+                        xsum = __builtin_fmaf(gf4_bias(2 * q), (float)hh.x + (float)ll.x, xsum);
+                        xsum = __builtin_fmaf(gf4_bias(2 * q + 1), (float)hh.y + (float)ll.y, xsum);
+                    }
                 }
                 *reinterpret_cast<uint4_t*>(xs + (size_t)(2 * b) * STRIDE + 8 * g) = uint4_t{hi[0], hi[1], hi[2], hi[3]};
                 *reinterpret_cast<uint4_t*>(xs + (size_t)(2 * b + 1) * STRIDE + 8 * g) =
                     uint4_t{lo[0], lo[1], lo[2], lo[3]};
+                if constexpr (BD) xw[b * CPW * 32 + g] = xsum;
             }
         }
     }
@@ -209,20 +231,27 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
     //    here is private to the wave and LDS operations of one wave execute in
     //    order, so no workgroup barrier is needed before the compute.
     const int mrow = lane & 15;
-    const bool a_live = mrow < 2 * n_batch;
-    const _Float16* arow = xs + (size_t)mrow * STRIDE + 64 * kq;
+    // A operand row of this lane: plain form, rows 2b / 2b+1 of the batch;
+    // BD form, row 4j+i carries word j == kq only.
+    const bool a_live = BD ? ((mrow >> 2) == kq && ((mrow & 3) >> 1) < n_batch) : (mrow < 2 * n_batch);
+    const _Float16* arow = xs + (size_t)(BD ? (mrow & 3) : mrow) * STRIDE + 64 * kq;
     const int swz_r = (n >> 1) & 7;
     const int rd0 = n * 128 + 16 * ((2 * kq) ^ swz_r);
     const int rd1 = n * 128 + 16 * ((2 * kq + 1) ^ swz_r);
     const int wr0 = lrow * 128 + 16 * (lseg ^ ((lrow >> 1) & 7));              // h = 0: rows 0..7
     const int wr1 = (8 + lrow) * 128 + 16 * (lseg ^ (((8 + lrow) >> 1) & 7));  // h = 1: rows 8..15
     const Gf4Consts cst = gf4_consts();
-    float4_t acc[RT][NM];
+    float4_t acc[RT][NM];   // plain form: the D accumulator
+    float accb[RT][NM][2];  // BD form: batch rows 0, 1 of word partials of this lane group
 #pragma unroll
     for (int t = 0; t < RT; ++t)
 #pragma unroll
-        for (int m = 0; m < NM; ++m) acc[t][m] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < NM; ++m) {
+            acc[t][m] = float4_t{0.f, 0.f, 0.f, 0.f};
+            accb[t][m][0] = accb[t][m][1] = 0.0f;
+        }
     half8_t a[8];
+    float xwv[NB][8];
 
     static_for<NTC>([&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -236,7 +265,19 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 const _Float16* ap = a_live ? arow + c * 256 : zrow;
 #pragma unroll
-                for (int q = 0; q < 8; ++q) a[q] = *reinterpret_cast<const half8_t*>(ap + 8 * q);
+                for (int q = 0; q < 8; ++q) a[q] = *reinterpret_cast<const half8_t*>(ap + (a_live ? 8 * q : 0));
+                if constexpr (BD) {
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const float4_t u0 = *reinterpret_cast<const float4_t*>(xw + b * CPW * 32 + c * 32 + 8 * kq);
+                        const float4_t u1 = *reinterpret_cast<const float4_t*>(xw + b * CPW * 32 + c * 32 + 8 * kq + 4);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            xwv[b][q] = u0[q];
+                            xwv[b][4 + q] = u1[q];
+                        }
+                    }
+                }
             }
             wait_vmcnt<NLOADS - 2 * (i + 1)>();
             uint8_t* xb = wblk + (i & 1) * 2048;
@@ -248,28 +289,65 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
             const uint4_t w0 = *reinterpret_cast<const uint4_t*>(xb + rd0);
             const uint4_t w1 = *reinterpret_cast<const uint4_t*>(xb + rd1);
             const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            if constexpr (BD) {
+                // All eight MFMAs first (independent, zero accumulator), so the
+                // fp32 epilogues do not wait on each MFMA's latency.
+                float4_t dd[8];
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], gf4_word_to_b(ww[q], cst), acc[t][m], 0, 0, 0);
+                for (int q = 0; q < 8; ++q)
+                    dd[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], gf4_word_to_biased(ww[q], cst),
+                                                                   float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float s = gf4_scale_f32(ww[q]);
+                    accb[t][m][0] = __builtin_fmaf(s, (xwv[0][q] - dd[q][0]) - dd[q][1], accb[t][m][0]);
+                    if constexpr (NB == 2)
+                        accb[t][m][1] = __builtin_fmaf(s, (xwv[NB - 1][q] - dd[q][2]) - dd[q][3], accb[t][m][1]);
+                }
+                // Schedule: decode of word q (6 VALU) then its MFMA, eight times,
+                // then the epilogues.
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    acc[t][m] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], gf4_word_to_b(ww[q], cst), acc[t][m], 0, 0, 0);
+            }
         }
     });
 
-    // 5. y[b][n] = (D[2b][n] + D[2b+1][n]) / scale of this wave, summed over the
-    //    KS waves; lane group kq holds batches 2kq and 2kq+1.
+    // 5. Per-wave partials, scaled back by the wave's activation scale, into
+    //    LDS and summed over the KS waves (and, BD, the four lane groups).
+    //    Plain form: lane group kq holds batches 2kq and 2kq+1 (D rows 4kq..4kq+3).
+    if constexpr (BD) {
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
+        for (int t = 0; t < RT; ++t)
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
+            for (int m = 0; m < NM; ++m)
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int b = 2 * kq + jj;
-                float isc = 1.0f;
+                for (int b = 0; b < NB; ++b)
+                    part[((((wave * RT + t) * NM + m) * NB + b) * 4 + kq) * 16 + n] =
+                        accb[t][m][b] * (0.25f * inv_scale[b]);
+    } else {
 #pragma unroll
-                for (int bb = 0; bb < NB; ++bb)
-                    if (bb == b) isc = inv_scale[bb];
-                if (b < NB)
-                    part[(((wave * RT + t) * NM + m) * NB + b) * 16 + n] =
-                        (acc[t][m][2 * jj] + acc[t][m][2 * jj + 1]) * isc;
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int b = 2 * kq + jj;
+                    float isc = 1.0f;
+#pragma unroll
+                    for (int bb = 0; bb < NB; ++bb)
+                        if (bb == b) isc = inv_scale[bb];
+                    if (b < NB)
+                        part[(((wave * RT + t) * NM + m) * NB + b) * 16 + n] =
+                            (acc[t][m][2 * jj] + acc[t][m][2 * jj + 1]) * isc;
+                }
             }
         }
     }
@@ -284,7 +362,9 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
         for (int m = 0; m < NM; ++m) {
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < KS; ++w) sum += part[(((w * RT + t) * NM + m) * NB + b) * 16 + nn];
+            for (int w = 0; w < KS; ++w)
+#pragma unroll
+                for (int g = 0; g < NKQ; ++g) sum += part[((((w * RT + t) * NM + m) * NB + b) * NKQ + g) * 16 + nn];
             tot[m] = sum;
         }
         if (r < rows && b < n_batch) {
@@ -296,21 +376,29 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
     }
 }
 
-template <int NB, int RT, int KS, int CPW, bool SWIGLU>
+// Largest batch of the block-diagonal form (0 disables it).
+#ifndef QW35_GF4_BD_MAX_BATCH
+#define QW35_GF4_BD_MAX_BATCH 2
+#endif
+
+template <int NB, int RT, int KS, int CPW, bool SWIGLU, bool BD>
 size_t lds_bytes() {
     constexpr int NM = SWIGLU ? 2 : 1;
-    return (size_t)KS * WaveLds<NB, CPW>::kBytes + (size_t)KS * RT * NM * NB * 16 * 4;
+    return (size_t)KS * WaveLds<NB, CPW, BD>::kBytes + (size_t)KS * RT * NM * NB * (BD ? 4 : 1) * 16 * 4;
 }
 
 template <int NB, int RT, int KS, int CPW, bool SWIGLU>
 hipError_t launch_cfg(const GemvArgs& a, hipStream_t stream) {
-    const size_t lds = lds_bytes<NB, RT, KS, CPW, SWIGLU>();
+    constexpr bool BD = NB <= QW35_GF4_BD_MAX_BATCH;
+    const size_t lds = lds_bytes<NB, RT, KS, CPW, SWIGLU, BD>();
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
     const int grid = (a.rows + 16 * RT - 1) / (16 * RT);
     if (a.awq) {
-        hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds, stream, a);
+        hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, true, BD>), dim3(grid), dim3(64 * KS), lds, stream,
+                           a);
     } else {
-        hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, false>), dim3(grid), dim3(64 * KS), lds, stream, a);
+        hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, false, BD>), dim3(grid), dim3(64 * KS), lds, stream,
+                           a);
     }
     return hipGetLastError();
 }
@@ -323,26 +411,29 @@ struct Gf4Plan {
     int rt, ks, cpw;
 };
 
+// Shapes measured on MI355X (graph replays over 805 MB of rotated weights):
+// 12288 x 4096 b1 {3, 8, 2} 7.10 us; fused gate/up b1 {3, 16, 1} 11.6 us
+// ({3, 8, 2} 12.2 us); 4096 x 12288 b1 {1, 12, 4} 8.01 us ({1, 8, 6} 8.41 us).
 Gf4Plan plan_gf4(int nb, int rows, int k, bool swiglu) {
-    (void)nb;
-    (void)swiglu;
     const int chunks = k / 256;
     const int tiles = (rows + 15) / 16;
     if (chunks <= 4) return {1, 4, 1};
     if (chunks <= 8) return {1, 4, 2};
     if (chunks <= 16) {
-        if (tiles >= 768) return {3, 8, 2};
+        if (tiles >= 768) return (swiglu && nb == 1) ? Gf4Plan{3, 16, 1} : Gf4Plan{3, 8, 2};
         if (tiles >= 512) return {2, 8, 2};
         return {1, 8, 2};
     }
     if (chunks <= 32) return {1, 8, 4};
+    if (chunks <= 48 && nb == 1) return {1, 12, 4};
     return {1, 8, 6};
 }
 
 size_t plan_lds(const Gf4Plan& p, int nb, bool swiglu) {
     const int nm = swiglu ? 2 : 1;
-    const size_t per_wave = 4096 + (size_t)2 * nb * (p.cpw * 256 + 8) * 2 + 128;
-    return (size_t)p.ks * per_wave + (size_t)p.ks * p.rt * nm * nb * 16 * 4;
+    const bool bd = nb <= QW35_GF4_BD_MAX_BATCH;
+    const size_t per_wave = 4096 + (size_t)2 * nb * (p.cpw * 256 + 8) * 2 + 128 + (bd ? (size_t)nb * p.cpw * 32 * 4 : 0);
+    return (size_t)p.ks * per_wave + (size_t)p.ks * p.rt * nm * nb * (bd ? 4 : 1) * 16 * 4;
 }
 
 template <int NB, bool SWIGLU>
@@ -357,6 +448,10 @@ hipError_t launch_nb(const GemvArgs& a, hipStream_t stream) {
     QW35_GF4_PLAN(3, 8, 2)
     if constexpr (NB <= 4) { QW35_GF4_PLAN(1, 8, 4) }
     if constexpr (NB <= 2) { QW35_GF4_PLAN(1, 8, 6) }
+    if constexpr (NB == 1) {
+        QW35_GF4_PLAN(3, 16, 1)
+        QW35_GF4_PLAN(1, 12, 4)
+    }
 #undef QW35_GF4_PLAN
     return hipErrorInvalidValue;
 }

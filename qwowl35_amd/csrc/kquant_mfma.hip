@@ -423,20 +423,32 @@ struct KqPlan {
 };
 
 // KS waves x CPW chunks cover k with P chunks in flight per wave; RT row tiles
-// per workgroup amortise the per-chunk activation staging over more rows, which
-// pays from batch 4 up on matrices with enough tiles (measured on MI355X:
-// 12288 x 4096 at batch 8, q8_0 32 -> 21 us, GF4 26 -> 14 us; Q4_K prefers four
-// tiles with one chunk in flight).
+// per workgroup amortise the per-chunk activation staging over more rows.
+// Settings from launch-shape sweeps on MI355X (graph replays, rotated weights),
+// e.g. q8_0 12352 x 4096 b8 {4, 8, 2, 1} 21.5 us ({3, 8, 2, 2} 35.9 us);
+// q8_0 4096 x 4096 b1 {1, 16, 1, 1} 6.2 us ({1, 8, 2, 2} 7.2 us); Q4_K
+// 248320 x 4096 b1 {2, 16, 1, 1} 128 us ({1, 8, 2, 2} 156 us), b8
+// {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us).
 KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
     if (chunks <= 4) return {1, 4, 1, 1};
     if (chunks <= 8) return {1, 8, 1, 1};
     if (chunks <= 16) {
-        if (nb >= 4 && tiles >= 512) return fmt == kFmtQ4K ? KqPlan{4, 8, 2, 1} : KqPlan{3, 8, 2, 2};
+        if (nb >= 4) {
+            if (tiles >= 512) {
+                if (fmt == kFmtQ4K) return tiles >= 4096 ? KqPlan{2, 4, 4, 2} : KqPlan{4, 8, 2, 1};
+                if (fmt == kFmtQ8) return {4, 8, 2, 1};
+                return {3, 8, 2, 2};
+            }
+            return fmt == kFmtQ8 ? KqPlan{1, 8, 2, 1} : KqPlan{1, 8, 2, 2};
+        }
+        if (fmt == kFmtQ4K && tiles >= 4096) return {2, 16, 1, 1};
+        if (fmt == kFmtQ8 && tiles < 512) return {1, 16, 1, 1};
         return {1, 8, 2, 2};
     }
     if (chunks <= 32) return {1, 8, 4, 2};
+    if (fmt == kFmtQ4K) return nb >= 4 ? KqPlan{1, 12, 4, 2} : KqPlan{1, 16, 3, 2};
     return {1, 8, 6, 2};
 }
 
@@ -491,6 +503,22 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
     QW35_KQ_PLAN(4, 8, 2, 1)
     QW35_KQ_PLAN(1, 8, 4, 2)
     QW35_KQ_PLAN(1, 8, 6, 2)
+    if constexpr (FMT == kFmtQ8) {
+        if constexpr (NB >= 4) {
+            QW35_KQ_PLAN(1, 8, 2, 1)
+        } else {
+            QW35_KQ_PLAN(1, 16, 1, 1)
+        }
+    }
+    if constexpr (FMT == kFmtQ4K) {
+        if constexpr (NB >= 4) {
+            QW35_KQ_PLAN(2, 4, 4, 2)
+            QW35_KQ_PLAN(1, 12, 4, 2)
+        } else {
+            QW35_KQ_PLAN(2, 16, 1, 1)
+            QW35_KQ_PLAN(1, 16, 3, 2)
+        }
+    }
     // over the load budget (fused gate/up at batch 8): one tile per workgroup
     if (p.rt > 1) return kq_launch_cfg<FMT, NB, 1, 8, 2, (kq_fits<FMT, NB, 1, 2, SWIGLU>() ? 2 : 1), SWIGLU>(a, stream);
 #undef QW35_KQ_PLAN
