@@ -137,8 +137,12 @@ def stream_ceiling(b: Bench, rt, torch, bufs) -> dict:
     sink_big = rt.stream_read(big)
     ms_big, _, _ = b.time_calls([lambda s: rt.stream_read(big, sink_big, stream=s)], 40, 5)
     n = bufs[0].numel()
+    tiny = torch.zeros(16, dtype=torch.uint8, device=b.dev)
+    sink_tiny = rt.stream_read(tiny)
+    ms_tiny, _, _ = b.time_calls([lambda s: rt.stream_read(tiny, sink_tiny, stream=s)] * 32, 2000, 200)
     return {"GB/s_25MB": round(n / (ms * 1e-3) / 1e9, 1), "us_25MB": round(ms * 1e3, 3),
-            "GB/s_1GiB": round((1 << 30) / (ms_big * 1e-3) / 1e9, 1)}
+            "GB/s_1GiB": round((1 << 30) / (ms_big * 1e-3) / 1e9, 1),
+            "launch_floor_us": round(ms_tiny * 1e3, 3)}
 
 
 BF16_DENSE_PEAK_TFLOPS = 2500.0
@@ -179,6 +183,28 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
                     "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
                     "frac_of_probe": round(tflops / ceiling, 4)}
         del ws
+    return out
+
+
+def bench_q6k_head(b: Bench, rt, torch) -> dict:
+    """The 9B LM head as the reference requires it (Q6_K, 248320 x 4096,
+    qw35-server/src/metal/bridge/Qw35MetalRuntime.m:202-208): the full-logits
+    GEMV and the fused greedy head (qw35_hip_output_argmax: GEMV + per-workgroup
+    argmax + reduction, no logits written) at batch 1 and 8."""
+    vocab, hidden = 248320, 4096
+    head = b.weight(rt.TYPE_Q6_K, vocab, hidden, tile_rows=16384)
+    wbytes = head.storage.numel()
+    out = {}
+    for nb in (1, 8):
+        x = b.normal((nb, hidden))
+        y = torch.zeros((nb, vocab), dtype=torch.float32, device=b.dev)
+        m, _, _ = b.time_calls(gemv_calls(rt, [head], x, y), 200, 20)
+        out[f"q6_k_head_b{nb}_248320x4096"] = {"us": round(m * 1e3, 3),
+                                                "GB/s": round(gemv_bytes(rt.TYPE_Q6_K, vocab, hidden, nb, rt) / m / 1e6, 1)}
+        ws = rt.output_argmax_workspace(head, nb, device=b.dev)
+        m, _, _ = b.time_calls([lambda s: rt.output_argmax(head, x, workspace=ws, stream=s)], 200, 20)
+        out[f"q6_k_greedy_head_b{nb}"] = {"us_two_launches": round(m * 1e3, 3),
+                                          "GB/s": round((wbytes + 4 * nb * hidden) / m / 1e6, 1)}
     return out
 
 
@@ -287,7 +313,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--headline-only", action="store_true", help="skip the extra configs (= --extras none)")
     ap.add_argument("--extras", default="all",
-                    help="comma list of extra configs: gf4,q8,q4k,prefill,stack (or all / none)")
+                    help="comma list of extra configs: gf4,q8,q4k,q6k,prefill,stack (or all / none)")
     ap.add_argument("--cpu-reps", type=int, default=40)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -320,8 +346,12 @@ def main() -> int:
     ceil = stream_ceiling(b, rt, torch, [w.storage for w in weights])
     extra["stream_read_ceiling"] = ceil
     extra["gf4_b1_frac_of_stream_ceiling"] = round(value / ceil["GB/s_25MB"], 4)
+    # Best frac of 8 TB/s one dependent launch of these bytes could reach here:
+    # the measured per-launch floor plus the bytes at the 1 GiB read rate.
+    best_us = ceil["launch_floor_us"] + algo / (ceil["GB/s_1GiB"] * 1e3)
+    extra["single_launch_frac_bound"] = round(algo / (best_us * 1e3) / HBM_PEAK_GBS, 4)
     want = set() if args.headline_only or args.extras == "none" else (
-        {"gf4", "q8", "q4k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
+        {"gf4", "q8", "q4k", "q6k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
     if "gf4" in want:
         for nb in (2, 4, 8):
             xb = b.normal((nb, k))
@@ -368,6 +398,8 @@ def main() -> int:
             extra[f"q4_k_head_b{nb}_248320x4096"] = {
                 "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 248320, 4096, nb, rt) / m / 1e6, 1)}
         del down, head
+    if "q6k" in want:
+        extra.update(bench_q6k_head(b, rt, torch))
     if "prefill" in want:
         extra.update(bench_prefill(b, rt, torch))
     if "stack" in want:

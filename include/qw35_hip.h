@@ -16,10 +16,14 @@
  *
  * Weight formats are the reference's raw GGUF tensor bytes (no repacking):
  *   type 100  GF4   8 elems / 4 B   (tools/gguf_custom_types.py:26-30)
- *   type   8  q8_0 32 elems / 34 B  (qw35-server/src/loader/tensors.rs:144)
- *   type  12  Q4_K 256 elems / 144 B (qw35-server/src/loader/tensors.rs:148)
+ *   type   8  q8_0 32 elems / 34 B  (qw35-server/src/loader/tensors.rs:142)
+ *   type  12  Q4_K 256 elems / 144 B (qw35-server/src/loader/tensors.rs:146)
+ *   type  14  Q6_K 256 elems / 210 B (qw35-server/src/loader/tensors.rs:150;
+ *             block qw35_block_q6_k, qw35-server/src/metal/qw35_types.metal:17-22)
  * Shape limits of this build: k % 256 == 0 and 256 <= k <= 12288 (every
- * Qwen3.5-9B projection has k = 4096 or 12288), rows >= 1, n_batch 1..8.
+ * Qwen3.5-9B projection has k = 4096 or 12288; Q6_K also needs k % 2048 == 0
+ * so that its 210-byte super-block rows stay 16-byte aligned), rows >= 1,
+ * n_batch 1..8.
  */
 #ifndef QW35_HIP_H
 #define QW35_HIP_H
@@ -33,6 +37,7 @@ extern "C" {
 
 #define QW35_HIP_TYPE_Q8_0 8u
 #define QW35_HIP_TYPE_Q4_K 12u
+#define QW35_HIP_TYPE_Q6_K 14u
 #define QW35_HIP_TYPE_GF4 100u
 #define QW35_HIP_MAX_BATCH 8u
 
@@ -86,10 +91,28 @@ int qw35_hip_decode_matvec(const qw35_hip_weight *w, const float *x, const float
  *   dst[b][r] = silu(gate[r] . (awq*x[b])) * (up[r] . (awq*x[b])),  silu(v) = v / (1 + exp(-v))
  * gate and up share type and shape.  Replaces encodeGf4FusedFfn
  * (Qw35MetalRuntime+FFN.m:13-35) / qw35_ffn_gate_up_swiglu_gf4_f32
- * (qw35-server/src/metal/qw35_gf4.metal:62-96), for every supported codec. */
+ * (qw35-server/src/metal/qw35_gf4.metal:62-96), for GF4, q8_0 and Q4_K
+ * (Q6_K is rejected: the reference uses it for the LM head only). */
 int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weight *up, const float *x,
                                 const float *awq, float *dst, uint32_t n_batch, void *stream, char *err,
                                 uintptr_t err_len);
+
+/* Greedy LM head: per batch row b, the largest of
+ *   logit[r] = sum_k W[r][k] * awq[k] * x[b][k]
+ * over the rows r, written as token[b] = r (uint32) and logit[b], without
+ * materialising the logits; ties go to the smaller row, NaN is never chosen
+ * (an all-NaN row gives 0xFFFFFFFF and -inf).  Replaces the greedy path of
+ * encodeOutputHead (qw35-server/src/metal/bridge/Qw35MetalRuntime+Output.m:11-65):
+ * qw35_output_q6_k_argmax_partials_16row_f32 + qw35_output_argmax_reduce_partials_f32
+ * (qw35-server/src/metal/qw35_output.metal:2-182).  Any supported type (the
+ * reference's head is Q6_K or GF4).  For q8_0, Q4_K and Q6_K the logits are
+ * bit-identical to qw35_hip_decode_matvec's.  Two launches on `stream`;
+ * workspace: device memory of qw35_hip_output_argmax_workspace_size(w, n_batch)
+ * bytes (256-byte aligned, caller-owned, not shared by concurrent calls). */
+uint64_t qw35_hip_output_argmax_workspace_size(const qw35_hip_weight *w, uint32_t n_batch);
+int qw35_hip_output_argmax(const qw35_hip_weight *w, const float *x, const float *awq, uint32_t n_batch,
+                           uint32_t *token, float *logit, void *workspace, uint64_t workspace_bytes, void *stream,
+                           char *err, uintptr_t err_len);
 
 /* fp32 dequantisation (bit-exact statement of each format).  row_ids == NULL:
  * all rows, dst fp32 [rows][k]; otherwise dst[i] = row row_ids[i] (device
@@ -164,9 +187,9 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_
  * bytes).  col_scale (device fp32 [k], 16-byte aligned, nullable) multiplies
  * column c before encoding: the AWQ column scale of pack_ffn_gf4
  * (tools/qw35_cook_common.py:182-199).  GF4 is bit-identical to the reference
- * packer pack_gf4_prepared(rows, scale_search=False) (:83-119).  q8_0 (k % 32)
- * and Q4_K (k % 256) are this library's min/max encoders; the reference has
- * none (it reads those types through gguf-py).  src must be finite. */
+ * packer pack_gf4_prepared(rows, scale_search=False) (:83-119).  q8_0 (k % 32),
+ * Q4_K and Q6_K (k % 256) are this library's min/max encoders; the reference
+ * has none (it reads those types through gguf-py).  src must be finite. */
 int qw35_hip_quantize(uint32_t type_id, const float *src, uint64_t rows, uint64_t k, const float *col_scale,
                       void *dst, void *stream, char *err, uintptr_t err_len);
 

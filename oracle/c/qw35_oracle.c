@@ -8,6 +8,9 @@
  *   q8_0 w = d * qs[i]                                         qw35-server/src/metal/qw35_types.metal:24-36
  *   Q4_K w = d * sc_j * q - dmin * m_j                         qw35-server/src/metal/qw35_matvec.metal:2-12,
  *                                                              qw35_types.metal:70-83
+ *   Q6_K w = d * sc[e/16] * (q - 32), q = ql nibble | qh bits << 4
+ *                                                              qw35_matvec.metal:458-542 (bit extraction),
+ *                                                              qw35_types.metal:17-22 (block)
  */
 #include <math.h>
 #include <stddef.h>
@@ -77,6 +80,30 @@ void qw35o_q4_k_dequant(const uint8_t *raw, size_t n_blocks, float *out) {
             const float dsc = d * (float)sc;
             const float mm = dmin * (float)m;
             out[256 * b + e] = dsc * (float)q - mm;
+        }
+    }
+}
+
+/* Q6_K, written from the reference GEMV's extraction: for each half ip and
+ * position l in 0..31, bytes ql[64ip + l], ql[64ip + 32 + l], qh[32ip + l]
+ * give elements 128ip + l + {0, 32, 64, 96}. */
+void qw35o_q6_k_dequant(const uint8_t *raw, size_t n_blocks, float *out) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t *blk = raw + 210 * b;
+        const uint8_t *ql = blk;
+        const uint8_t *qh = blk + 128;
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        const float d = half_bits_to_float(rd16(blk + 208));
+        for (int ip = 0; ip < 2; ++ip) {
+            for (int l = 0; l < 32; ++l) {
+                const int a = ql[64 * ip + l], c = ql[64 * ip + 32 + l], h = qh[32 * ip + l];
+                const int q[4] = {(a & 15) | ((h & 3) << 4), (c & 15) | (((h >> 2) & 3) << 4),
+                                  (a >> 4) | (((h >> 4) & 3) << 4), (c >> 4) | (((h >> 6) & 3) << 4)};
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 128 * ip + 32 * j + l;
+                    out[256 * b + e] = (d * (float)sc[e / 16]) * (float)(q[j] - 32);
+                }
+            }
         }
     }
 }

@@ -19,11 +19,12 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import gf4, q4_k, q8_0
+from . import gf4, q4_k, q6_k, q8_0
 
 TYPE_GF4 = gf4.GF4_TYPE_ID
 TYPE_Q8_0 = q8_0.Q8_0_TYPE_ID
 TYPE_Q4_K = q4_k.Q4_K_TYPE_ID
+TYPE_Q6_K = q6_k.Q6_K_TYPE_ID
 
 
 def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
@@ -34,6 +35,9 @@ def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
         return q8_0.q8_0_nbytes(rows, k)
     if type_id == TYPE_Q4_K:
         return q4_k.q4_k_nbytes(rows, k)
+    if type_id == TYPE_Q6_K:
+        assert k % q6_k.Q6_K_BLOCK_ELEMS == 0
+        return rows * (k // q6_k.Q6_K_BLOCK_ELEMS) * q6_k.Q6_K_BLOCK_BYTES
     raise ValueError(f"unsupported type id {type_id}")
 
 
@@ -45,6 +49,8 @@ def quantize(type_id: int, w: np.ndarray) -> np.ndarray:
         return q8_0.q8_0_quantize(w)
     if type_id == TYPE_Q4_K:
         return q4_k.q4_k_quantize(w)
+    if type_id == TYPE_Q6_K:
+        return q6_k.q6_k_quantize(w).reshape(w.shape[0], -1)
     raise ValueError(f"unsupported type id {type_id}")
 
 
@@ -57,6 +63,8 @@ def dequant(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
         return q8_0.q8_0_dequant(raw)
     if type_id == TYPE_Q4_K:
         return q4_k.q4_k_dequant(raw)
+    if type_id == TYPE_Q6_K:
+        return q6_k.q6_k_dequant(raw, rows, raw.size // rows // q6_k.Q6_K_BLOCK_BYTES * q6_k.Q6_K_BLOCK_ELEMS)
     raise ValueError(f"unsupported type id {type_id}")
 
 
@@ -118,3 +126,22 @@ def prefill_f64(w: np.ndarray, a_bits: np.ndarray, awq: np.ndarray | None = None
     """fp64 C[M, rows] = A' @ W^T on the exact bf16 operands the kernel consumes."""
     a_eff = prefill_operand(a_bits, awq).astype(np.float64)
     return a_eff @ np.asarray(w, dtype=np.float64).T
+
+
+def argmax_rule(logits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Greedy head reduction of the reference (``qw35_output.metal:120-182``):
+    starting from (-inf, 0xFFFFFFFF), a value replaces the best when it is
+    larger, or equal with a smaller row id.  So per batch row: the largest
+    logit, ties to the smaller id, NaN never selected (an all-NaN row gives
+    0xFFFFFFFF and -inf).  Returns (ids uint32, logits fp32) over ``logits[b, r]``."""
+    lg = np.atleast_2d(np.asarray(logits, dtype=np.float32))
+    ids = np.full(lg.shape[0], 0xFFFFFFFF, dtype=np.uint32)
+    best = np.full(lg.shape[0], -np.inf, dtype=np.float32)
+    for b in range(lg.shape[0]):
+        row = lg[b]
+        ok = ~np.isnan(row)
+        if ok.any():
+            m = row[ok].max()
+            ids[b] = np.flatnonzero(ok & (row == m))[0]
+            best[b] = m
+    return ids, best

@@ -1,7 +1,7 @@
 """ggml Q4_K codec — numpy restatement.  Test infrastructure only.
 
 Super-block of 256 weights = 144 bytes (``qw35_types.metal:2-7``;
-``tensor_nbytes(12, n)`` = ``(256, 144)`` at ``loader/tensors.rs:148``):
+``tensor_nbytes(12, n)`` = ``(256, 144)`` at ``loader/tensors.rs:146``):
 
 * ``d``, ``dmin``  — little-endian binary16 super-scales,
 * ``scales[12]``   — eight (6-bit scale, 6-bit min) pairs, packed as

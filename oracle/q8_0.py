@@ -2,7 +2,7 @@
 
 Block of 32 weights = 34 bytes: little-endian binary16 ``d`` followed by 32
 int8 ``qs`` (``qw35_types.metal:24-27``; ``tensor_nbytes(8, n)`` =
-``(32, 34)`` at ``qw35-server/src/loader/tensors.rs:144``).  A row of ``k``
+``(32, 34)`` at ``qw35-server/src/loader/tensors.rs:142``).  A row of ``k``
 columns is ``k/32`` consecutive blocks.  Dequantisation is ``fp32(d) * qs[j]``
 (``qw35_matvec.metal:136-149``, ``:630-654``) — exact in fp32.
 

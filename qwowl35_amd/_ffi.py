@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libqw35_hip.so"
 
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
+TYPE_Q6_K = 14
 TYPE_GF4 = 100
 MAX_BATCH = 8
 DTYPE_F32 = 0
@@ -81,6 +82,12 @@ PROTOTYPES: dict[str, tuple] = {
         C.c_int,
         [C.POINTER(Weight), C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
          C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_output_argmax_workspace_size": (C.c_uint64, [C.POINTER(Weight), C.c_uint32]),
+    "qw35_hip_output_argmax": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
+         C.c_void_p, C.c_char_p, C.c_size_t],
     ),
     "qw35_hip_dequantize": (
         C.c_int,

@@ -1,6 +1,7 @@
 // extern "C" entry points of include/qw35_hip.h: argument validation, the
 // type-id -> kernel dispatch of encodeDecodeMatvecTensor
-// (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:184-256) and the
+// (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:184-256), the greedy
+// head of encodeOutputHead (Qw35MetalRuntime+Output.m:11-65) and the
 // 0 + err[err_len] error convention of Qw35FFI.m:15-22.
 #include <stdarg.h>
 #include <stdio.h>
@@ -20,7 +21,7 @@ void set_err(char* err, uintptr_t err_len, const char* fmt, ...) {
 }
 
 bool type_supported(uint32_t t) {
-    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K;
+    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K || t == qw35::kTypeQ6_K;
 }
 
 uint64_t row_bytes(uint32_t t, uint64_t k) {
@@ -28,6 +29,7 @@ uint64_t row_bytes(uint32_t t, uint64_t k) {
         case qw35::kTypeGF4: return (k + 7) / 8 * 4;
         case qw35::kTypeQ8_0: return (k + 31) / 32 * 34;
         case qw35::kTypeQ4_K: return (k + 255) / 256 * 144;
+        case qw35::kTypeQ6_K: return (k + 255) / 256 * 210;
         default: return 0;
     }
 }
@@ -37,6 +39,7 @@ const char* type_name(uint32_t t) {
         case qw35::kTypeGF4: return "gf4";
         case qw35::kTypeQ8_0: return "q8_0";
         case qw35::kTypeQ4_K: return "q4_k";
+        case qw35::kTypeQ6_K: return "q6_k";
         default: return "unsupported";
     }
 }
@@ -65,6 +68,12 @@ bool check_weight(const qw35_hip_weight* w, const char* what, char* err, uintptr
                 (unsigned long long)w->k, (unsigned long long)kMaxK);
         return false;
     }
+    if (w->type_id == qw35::kTypeQ6_K && w->k % 2048 != 0) {
+        // 210-byte super-blocks: rows are 16-byte aligned only for k % 2048 == 0
+        set_err(err, err_len, "%s: q6_k needs k %% 2048 == 0 (16-byte aligned rows), got k=%llu", what,
+                (unsigned long long)w->k);
+        return false;
+    }
     if (w->rows == 0 || w->rows > 0x7fffffffull) {
         set_err(err, err_len, "%s: rows=%llu out of range", what, (unsigned long long)w->rows);
         return false;
@@ -89,6 +98,7 @@ hipError_t dispatch_gemv(uint32_t type_id, const qw35::GemvArgs& a, hipStream_t 
     switch (type_id) {
         case qw35::kTypeGF4: return qw35::launch_gf4_gemv(a, s);
         case qw35::kTypeQ8_0: return qw35::launch_q8_0_gemv(a, s);
+        case qw35::kTypeQ6_K: return qw35::launch_q6_k_gemv(a, s);
         default: return qw35::launch_q4_k_gemv(a, s);
     }
 }
@@ -117,6 +127,10 @@ bool check_swiglu(const qw35_hip_weight* gate, const qw35_hip_weight* up, const 
     if (!check_weight(up, what, err, err_len)) return false;
     if (gate->type_id != up->type_id || gate->k != up->k || gate->rows != up->rows) {
         set_err(err, err_len, "%s: gate and up must share type and shape", what);
+        return false;
+    }
+    if (gate->type_id == qw35::kTypeQ6_K) {
+        set_err(err, err_len, "%s: q6_k has no fused gate/up form", what);
         return false;
     }
     return true;
@@ -433,6 +447,50 @@ int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_
     return check_hip(qw35::launch_quantize(type_id, src, (int)rows, (int)k, col_scale, dst,
                                            static_cast<hipStream_t>(stream)),
                      "quantize", err, err_len)
+               ? 1
+               : 0;
+}
+
+// Greedy head workspace: per batch row, one (token, logit) partial per
+// workgroup of the GEMV launch; tokens first, logits at a 256-byte boundary.
+static uint64_t argmax_ws_part(const qw35_hip_weight* w, uint32_t n_batch) {
+    const uint64_t n = (uint64_t)qw35::argmax_groups(w->type_id, (int)w->rows, (int)w->k, (int)n_batch) * n_batch;
+    return (n * 4 + 255) / 256 * 256;
+}
+
+uint64_t qw35_hip_output_argmax_workspace_size(const qw35_hip_weight* w, uint32_t n_batch) {
+    char msg[8];
+    if (!check_weight(w, "output_argmax", msg, sizeof msg) || n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) return 0;
+    return 2 * argmax_ws_part(w, n_batch);
+}
+
+int qw35_hip_output_argmax(const qw35_hip_weight* w, const float* x, const float* awq, uint32_t n_batch,
+                           uint32_t* token, float* logit, void* workspace, uint64_t workspace_bytes, void* stream,
+                           char* err, uintptr_t err_len) {
+    if (!check_weight(w, "output_argmax", err, err_len)) return 0;
+    if (!x || !token || !logit || !workspace) {
+        set_err(err, err_len, "output_argmax: null input, output or workspace");
+        return 0;
+    }
+    if (((uintptr_t)x & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)token & 3u) || ((uintptr_t)logit & 3u)) {
+        set_err(err, err_len, "output_argmax: x/awq must be 16-byte aligned, token/logit 4-byte aligned");
+        return 0;
+    }
+    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
+        set_err(err, err_len, "output_argmax: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);
+        return 0;
+    }
+    const uint64_t part = argmax_ws_part(w, n_batch);
+    if (workspace_bytes < 2 * part || ((uintptr_t)workspace & 255u)) {
+        set_err(err, err_len, "output_argmax: workspace must be 256-byte aligned and >= %llu bytes, got %llu",
+                (unsigned long long)(2 * part), (unsigned long long)workspace_bytes);
+        return 0;
+    }
+    qw35::GemvArgs a = gemv_args(w, nullptr, x, awq, nullptr, n_batch, 0);
+    a.am_token = static_cast<uint32_t*>(workspace);
+    a.am_logit = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + part);
+    return check_hip(qw35::launch_argmax_gemv(w->type_id, a, token, logit, static_cast<hipStream_t>(stream)),
+                     "output_argmax", err, err_len)
                ? 1
                : 0;
 }

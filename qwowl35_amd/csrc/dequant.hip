@@ -1,4 +1,4 @@
-// fp32 dequantisation of GF4 / q8_0 / Q4_K tensors, optionally gathering rows.
+// fp32 dequantisation of GF4 / q8_0 / Q4_K / Q6_K tensors, optionally gathering rows.
 //
 // This is the library's bit-exact statement of each format (every weight of
 // all three codecs is exact in fp32, so results are compared bit-for-bit with
@@ -8,6 +8,9 @@
 //   GF4  (tools/qw35_cook_common.py:79):  w = (4 - (c ^ 4)) * 0.25 * s, s = fp16(b << 8)
 //   q8_0 (qw35_types.metal:24-36):        w = fp32(d) * qs[i]
 //   Q4_K (qw35_matvec.metal:2-12):        w = d * sc_j * q - dmin * m_j
+//   Q6_K (qw35_matvec.metal:458-542):     w = (d * sc[e/16]) * (q - 32), q = ql nibble | qh 2 bits << 4
+//                                         (exact; the reference tile form qw35_dequantize_q6_k,
+//                                         :65-98, agrees in value)
 #include "qw35_device.h"
 #include "qw35_kernels.h"
 
@@ -48,6 +51,21 @@ __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const ui
         const float d = f16_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = d * (float)(int8_t)blk[2 + (col & 31) + i];
+    } else if (type_id == kTypeQ6_K) {
+        const uint8_t* row = w + src_row * (size_t)(k >> 8) * 210;
+        const int col = 8 * g;
+        const uint8_t* blk = row + (size_t)(col >> 8) * 210;
+        const int e0 = col & 255;
+        const float d = f16_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+        const float dsc = d * (float)(int8_t)blk[192 + (e0 >> 4)];  // 8 columns within one sub-block
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + i;
+            const int h = e >> 7, gg = (e & 127) >> 5, l = e & 31;
+            const uint32_t lo = (blk[64 * h + 32 * (gg & 1) + l] >> (4 * (gg >> 1))) & 15u;
+            const uint32_t hi = (blk[128 + 32 * h + l] >> (2 * gg)) & 3u;
+            v[i] = dsc * (float)((int)(lo | (hi << 4)) - 32);
+        }
     } else {  // Q4_K
         const uint8_t* row = w + src_row * (size_t)(k >> 8) * 144;
         const int col = 8 * g;

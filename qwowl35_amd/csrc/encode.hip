@@ -1,4 +1,4 @@
-// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K tensor bytes, on the GPU.
+// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K / Q6_K tensor bytes, on the GPU.
 //
 // GF4 is the reference packer pack_gf4_prepared(rows, scale_search=False)
 // (tools/qw35_cook_common.py:83-119), including the optional AWQ column
@@ -10,8 +10,8 @@
 //   s     = fp16(b << 8)                                (:54-56)
 //   q_raw = clip(rint(fl(x / s) * -4 + 4), 0, 7), 0 where s == 0   (:67-80)
 //   word  = b | sum_i (q_raw_i ^ 4) << (8 + 3 i)        (:113-118)
-// q8_0 and Q4_K have no encoder in the reference (it reads them through the
-// external gguf-py); these are this library's own min/max encoders, the GPU
+// q8_0, Q4_K and Q6_K have no encoder in the reference (it reads them through
+// the external gguf-py); these are this library's own min/max encoders, the GPU
 // statement of the ones the tests use, producing valid GGUF blocks.
 //
 // Inputs must be finite: NaN ordering in numpy's argmax and its float->int
@@ -204,6 +204,67 @@ __global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const flo
     }
 }
 
+// One thread per Q6_K super-block (256 columns, 16 sub-blocks of 16), the
+// statement of oracle q6_k_quantize:
+//   sub_s = max|x| / 31, d = fp16(max_s sub_s / 127), sc_s = clip(rint(sub_s / d), 0, 127)
+//   q = clip(rint(x / (d * sc_s)), -32, 31) + 32
+// stored as ggml lays Q6_K out (qw35_types.metal:17-22): element
+// 128h + 32g + l has its low nibble in ql[64h + 32(g&1) + l] (high nibble for
+// g >= 2) and its top two bits at bit 2g of qh[32h + l].  Super-blocks are
+// 210 bytes (2-byte aligned), so the bytes are stored one at a time.
+__global__ __launch_bounds__(kEncodeThreads) void q6_k_quantize_kernel(const float* __restrict__ src,
+                                                                       const float* __restrict__ col_scale,
+                                                                       uint8_t* __restrict__ dst, uint64_t n_blocks,
+                                                                       uint32_t blocks_per_row) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_blocks;
+         i += (uint64_t)gridDim.x * kEncodeThreads) {
+        const float* x = src + 256 * i;
+        const float* cs = col_scale ? col_scale + 256u * (uint32_t)(i % blocks_per_row) : nullptr;
+        auto val = [&](int e) { return cs ? __fmul_rn(x[e], cs[e]) : x[e]; };
+        float sub[16];
+        float smax = 0.0f;
+#pragma unroll
+        for (int sb = 0; sb < 16; ++sb) {
+            float amax = 0.0f;
+            for (int l = 0; l < 16; ++l) amax = fmaxf(amax, fabsf(val(16 * sb + l)));
+            sub[sb] = __fdiv_rn(amax, 31.0f);
+            smax = fmaxf(smax, sub[sb]);
+        }
+        const uint32_t d_bits = f32_to_f16_bits(__fdiv_rn(smax, 127.0f));
+        const float df = f16_bits_to_f32(d_bits);
+        float step[16];
+        uint8_t* blk = dst + 210 * i;
+#pragma unroll
+        for (int sb = 0; sb < 16; ++sb) {
+            const float a = (df != 0.0f) ? rintf(__fdiv_rn(sub[sb], df)) : 0.0f;
+            const float scq = fminf(fmaxf(a, 0.0f), 127.0f);
+            step[sb] = __fmul_rn(df, scq);
+            blk[192 + sb] = (uint8_t)(int)scq;
+        }
+        auto code = [&](int e) {
+            const float st = step[e >> 4];
+            const float qf = (st != 0.0f) ? rintf(__fdiv_rn(val(e), st)) : 0.0f;
+            return (uint32_t)(int)(fminf(fmaxf(qf, -32.0f), 31.0f) + 32.0f);
+        };
+#pragma unroll
+        for (int j = 0; j < 128; ++j) {
+            const int h = j >> 6, gp = (j >> 5) & 1, l = j & 31;
+            const int e = 128 * h + 32 * gp + l;
+            blk[j] = (uint8_t)((code(e) & 15u) | ((code(e + 64) & 15u) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            const int h = j >> 5, l = j & 31;
+            uint32_t b = 0;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) b |= (code(128 * h + 32 * g + l) >> 4) << (2 * g);
+            blk[128 + j] = (uint8_t)b;
+        }
+        blk[208] = (uint8_t)(d_bits & 0xFFu);
+        blk[209] = (uint8_t)(d_bits >> 8);
+    }
+}
+
 unsigned grid_for(uint64_t n) {
     const uint64_t g = (n + kEncodeThreads - 1) / kEncodeThreads;
     return (unsigned)(g < (uint64_t)kEncodeBlocks ? g : (uint64_t)kEncodeBlocks);
@@ -225,6 +286,12 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
             const uint64_t n = r * (uint64_t)(k / 32);
             hipLaunchKernelGGL(q8_0_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
                                col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 32));
+            break;
+        }
+        case kTypeQ6_K: {
+            const uint64_t n = r * (uint64_t)(k / 256);
+            hipLaunchKernelGGL(q6_k_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
+                               col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
             break;
         }
         default: {

@@ -30,6 +30,21 @@
 // chunk's eight MFMAs accumulate in one register set; lane group kq takes words
 // 8kq..8kq+7 of a row (two 16-byte LDS reads) and the activation operand
 // follows that k order and the (0,4)(1,5)(2,6)(3,7) pairing within each word.
+//
+// Q6_K (qw35_types.metal:17-22; GEMV qw35_decode_matmul_q6_k_llama_f32,
+// qw35_matvec.metal:458-542): a 210-byte super-block per 256 columns, so a
+// chunk starts at byte 210c of the row, 2-byte aligned; it is loaded as the 14
+// aligned 16-byte segments that cover it and realigned in registers
+// (v_alignbyte).  Its 16 sub-blocks of 16 weights each have an int8 scale, so
+// the contraction runs on v_mfma_f32_16x16x16_f16, one MFMA per sub-block:
+//   B: the 6-bit code (ql nibble | qh 2 bits << 4) -> exact fp16 q - 32;
+//   y += d * sc_s * sum (q - 32) x.
+//
+// Greedy head (qw35_output_q6_k_argmax_partials_16row_f32 +
+// qw35_output_argmax_reduce_partials_f32, qw35_output.metal:2-182): with
+// GemvArgs::am_token set, the workgroup keeps the largest result of its rows
+// per batch row instead of writing y (ties to the smaller row id, NaN never
+// chosen), and argmax_reduce_kernel reduces those partials.
 #include "gf4_decode.h"
 #include "qw35_device.h"
 #include "qw35_kernels.h"
@@ -42,6 +57,7 @@ namespace {
 constexpr int kFmtQ8 = 0;
 constexpr int kFmtQ4K = 1;
 constexpr int kFmtGF4 = 2;
+constexpr int kFmtQ6K = 3;
 
 template <int FMT>
 struct Fmt;
@@ -67,6 +83,41 @@ struct Fmt<kFmtGF4> {
     static constexpr int kStride = 144;
     static constexpr int kTypeId = 100;
 };
+template <>
+struct Fmt<kFmtQ6K> {
+    static constexpr int kChunkBytes = 210;  // one super-block = 256 columns
+    static constexpr int kSegs = 14;         // aligned segments covering bytes [210c, 210c + 210)
+    static constexpr int kStride = 240;
+    static constexpr int kTypeId = 14;
+};
+
+// Byte offset of chunk c's first loaded segment within its row (16-byte
+// aligned), and of the chunk's data within that segment (Q6_K only).
+template <int FMT>
+__device__ __forceinline__ size_t chunk_seg_base(int c) {
+    if constexpr (FMT == kFmtQ6K) return (size_t)(c * 210) & ~(size_t)15;
+    return (size_t)c * Fmt<FMT>::kChunkBytes;
+}
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+// Largest (value, id) under the reference's rule: a candidate wins when it is
+// larger, or equal with a smaller id; NaN values enter as (-inf, 0xFFFFFFFF).
+__device__ __forceinline__ void argmax_take(float& v, uint32_t& id, float ov, uint32_t oid) {
+    if (ov > v || (ov == v && oid < id)) {
+        v = ov;
+        id = oid;
+    }
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& id) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const uint32_t oid = (uint32_t)__shfl_xor((int)id, o);
+        argmax_take(v, id, ov, oid);
+    }
+}
 
 template <int N>
 __device__ __forceinline__ void kq_wait_vmcnt() {
@@ -198,7 +249,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                     int r = row0 + 16 * t + s / F::kSegs;
                     r = r < rows ? r : rows - 1;
                     wv[sl][t * NM + m][i] = load_stream16(
-                        wbase + (size_t)r * row_bytes + (size_t)chunk * F::kChunkBytes + 16 * (s % F::kSegs));
+                        wbase + (size_t)r * row_bytes + chunk_seg_base<FMT>(chunk) + 16 * (s % F::kSegs));
                 }
             }
         }
@@ -206,7 +257,9 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
 
     kq_static_for<P>([&](auto CI) { issue(CI); });
 
-    const half2_t bias = FMT == kFmtQ8 ? h2(-1152.0f, -1152.0f) : h2(-1024.0f, -1024.0f);
+    const half2_t bias = FMT == kFmtQ8    ? h2(-1152.0f, -1152.0f)
+                         : FMT == kFmtQ6K ? h2(-1056.0f, -1056.0f)
+                                          : h2(-1024.0f, -1024.0f);
     const Gf4Consts gc = gf4_consts();
     float acc[RT][NM][2];
 #pragma unroll
@@ -332,6 +385,38 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                             acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
                             acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
                         }
+                    } else if constexpr (FMT == kFmtQ6K) {
+                        // The super-block starts `off` bytes into the row buffer
+                        // (even); words are read 4-aligned and realigned by sh.
+                        const int off = ((wave * CPW + c) * 210) & 15;
+                        const int sh = off & 3;
+                        const uint8_t* sb = wrow + (off & ~3);
+                        auto ld = [&](int o) {
+                            const uint32_t* p = reinterpret_cast<const uint32_t*>(sb + o);
+                            return __builtin_amdgcn_alignbyte(p[1], p[0], sh);
+                        };
+                        const float d =
+                            (float)__builtin_bit_cast(_Float16, (uint16_t)(ld(208) & 0xFFFFu));
+                        uint32_t scw[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) scw[q] = ld(192 + 4 * q);
+#pragma unroll
+                        for (int sbk = 0; sbk < 16; ++sbk) {
+                            const int h = sbk >> 3, g = (sbk & 7) >> 1, p = sbk & 1;
+                            const uint32_t qlw = ld(64 * h + 32 * (g & 1) + 16 * p + 4 * kq);
+                            const uint32_t qhw = ld(128 + 32 * h + 16 * p + 4 * kq);
+                            const uint32_t nib = ((g >> 1) ? (qlw >> 4) : qlw) & 0x0F0F0F0Fu;
+                            const uint32_t qv = nib | (((qhw >> (2 * g)) & 0x03030303u) << 4);
+                            uint32_t b0, b1;
+                            u4x4_to_h(qv, bias, b0, b1);
+                            const half4_t bop = __builtin_bit_cast(half4_t, uint2_t_{b0, b1});
+                            const half4_t aop = *reinterpret_cast<const half4_t*>(arow + (a_live ? 16 * sbk + 4 * kq : 0));
+                            const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                                aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            const float dsc = d * (float)(int)(int8_t)((scw[sbk >> 2] >> (8 * (sbk & 3))) & 0xFFu);
+                            acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
+                            acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
+                        }
                     } else {
                         const uint4_t hd = *reinterpret_cast<const uint4_t*>(wrow);
                         const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)hd.x);
@@ -396,6 +481,28 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                 if (b < NB) part[(((wave * RT + t) * NM + m) * NB + b) * 16 + n] = acc[t][m][jj];
             }
     __syncthreads();
+    if (args.am_token) {
+        // Greedy head: wave b' reduces batch rows b', b' + KS, ...; lane l takes
+        // rows l, l + 64, ... of the workgroup (same sums as the y path).
+        for (int b = wave; b < n_batch; b += KS) {
+            float best = -__builtin_inff();
+            uint32_t best_id = 0xFFFFFFFFu;
+            for (int o = lane; o < RT * 16; o += 64) {
+                const int t = o >> 4, nn = o & 15;
+                const int r = row0 + o;
+                float sum = 0.0f;
+#pragma unroll
+                for (int w = 0; w < KS; ++w) sum += part[(((w * RT + t) * NM) * NB + b) * 16 + nn];
+                if (r < rows && !__builtin_isnan(sum)) argmax_take(best, best_id, sum, (uint32_t)r);
+            }
+            wave_argmax(best, best_id);
+            if (lane == 0) {
+                args.am_logit[(size_t)blockIdx.x * n_batch + b] = best;
+                args.am_token[(size_t)blockIdx.x * n_batch + b] = best_id;
+            }
+        }
+        return;
+    }
     for (int o = threadIdx.x; o < RT * NB * 16; o += 64 * KS) {
         const int t = o / (NB * 16);
         const int b = (o / 16) % NB;
@@ -418,6 +525,34 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     }
 }
 
+// Final reduction of the greedy-head partials: block b reduces batch row b.
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint32_t* __restrict__ pt,
+                                                            const float* __restrict__ pv, int n_groups, int n_batch,
+                                                            uint32_t* __restrict__ token, float* __restrict__ logit) {
+    __shared__ float sv[4];
+    __shared__ uint32_t sid[4];
+    const int b = blockIdx.x;
+    float best = -__builtin_inff();
+    uint32_t best_id = 0xFFFFFFFFu;
+    for (int g = threadIdx.x; g < n_groups; g += 256) {
+        const float v = pv[(size_t)g * n_batch + b];
+        if (!__builtin_isnan(v)) argmax_take(best, best_id, v, pt[(size_t)g * n_batch + b]);
+    }
+    wave_argmax(best, best_id);
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        sid[threadIdx.x >> 6] = best_id;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = sv[0];
+        uint32_t id = sid[0];
+        for (int w = 1; w < 4; ++w) argmax_take(v, id, sv[w], sid[w]);
+        token[b] = id;
+        logit[b] = v;
+    }
+}
+
 struct KqPlan {
     int rt, ks, cpw, p;
 };
@@ -437,18 +572,18 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     if (chunks <= 16) {
         if (nb >= 4) {
             if (tiles >= 512) {
-                if (fmt == kFmtQ4K) return tiles >= 4096 ? KqPlan{2, 4, 4, 2} : KqPlan{4, 8, 2, 1};
+                if (fmt == kFmtQ4K || fmt == kFmtQ6K) return tiles >= 4096 ? KqPlan{2, 4, 4, 2} : KqPlan{4, 8, 2, 1};
                 if (fmt == kFmtQ8) return {4, 8, 2, 1};
                 return {3, 8, 2, 2};
             }
             return fmt == kFmtQ8 ? KqPlan{1, 8, 2, 1} : KqPlan{1, 8, 2, 2};
         }
-        if (fmt == kFmtQ4K && tiles >= 4096) return {2, 16, 1, 1};
+        if ((fmt == kFmtQ4K || fmt == kFmtQ6K) && tiles >= 4096) return {2, 16, 1, 1};
         if (fmt == kFmtQ8 && tiles < 512) return {1, 16, 1, 1};
         return {1, 8, 2, 2};
     }
     if (chunks <= 32) return {1, 8, 4, 2};
-    if (fmt == kFmtQ4K) return nb >= 4 ? KqPlan{1, 12, 4, 2} : KqPlan{1, 16, 3, 2};
+    if (fmt == kFmtQ4K || fmt == kFmtQ6K) return nb >= 4 ? KqPlan{1, 12, 4, 2} : KqPlan{1, 16, 3, 2};
     return {1, 8, 6, 2};
 }
 
@@ -510,7 +645,7 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
             QW35_KQ_PLAN(1, 16, 1, 1)
         }
     }
-    if constexpr (FMT == kFmtQ4K) {
+    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ6K) {
         if constexpr (NB >= 4) {
             QW35_KQ_PLAN(2, 4, 4, 2)
             QW35_KQ_PLAN(1, 12, 4, 2)
@@ -545,6 +680,46 @@ hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream) {
 
 hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream) {
     return a.w_up ? kq_launch_any<kFmtGF4, true>(a, stream) : kq_launch_any<kFmtGF4, false>(a, stream);
+}
+
+// Q6_K has no fused gate/up form (the reference uses it for the LM head only).
+hipError_t launch_q6_k_gemv(const GemvArgs& a, hipStream_t stream) {
+    if (a.w_up) return hipErrorInvalidValue;
+    return kq_launch_any<kFmtQ6K, false>(a, stream);
+}
+
+namespace {
+int fmt_of(uint32_t type_id) {
+    switch (type_id) {
+        case kTypeQ8_0: return kFmtQ8;
+        case kTypeQ4_K: return kFmtQ4K;
+        case kTypeQ6_K: return kFmtQ6K;
+        default: return kFmtGF4;
+    }
+}
+}  // namespace
+
+int argmax_groups(uint32_t type_id, int rows, int k, int n_batch) {
+    const int nb = n_batch <= 1 ? 1 : n_batch == 2 ? 2 : n_batch <= 4 ? 4 : 8;
+    const KqPlan p = plan_kq(fmt_of(type_id), rows, k, nb);
+    return (rows + 16 * p.rt - 1) / (16 * p.rt);
+}
+
+hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* token, float* logit,
+                              hipStream_t stream) {
+    if (!a.am_token || !a.am_logit || a.w_up || a.n_seg > 1) return hipErrorInvalidValue;
+    hipError_t e;
+    switch (type_id) {
+        case kTypeQ8_0: e = kq_launch_any<kFmtQ8, false>(a, stream); break;
+        case kTypeQ4_K: e = kq_launch_any<kFmtQ4K, false>(a, stream); break;
+        case kTypeQ6_K: e = kq_launch_any<kFmtQ6K, false>(a, stream); break;
+        default: e = kq_launch_any<kFmtGF4, false>(a, stream); break;
+    }
+    if (e != hipSuccess) return e;
+    const int groups = argmax_groups(type_id, a.rows, a.k, a.n_batch);
+    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(a.n_batch), dim3(256), 0, stream, a.am_token, a.am_logit, groups,
+                       a.n_batch, token, logit);
+    return hipGetLastError();
 }
 
 }  // namespace qw35

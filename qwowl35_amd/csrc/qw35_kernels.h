@@ -10,6 +10,7 @@ namespace qw35 {
 // GGUF tensor type-ids handled by this library.
 constexpr uint32_t kTypeQ8_0 = 8;
 constexpr uint32_t kTypeQ4_K = 12;
+constexpr uint32_t kTypeQ6_K = 14;
 constexpr uint32_t kTypeGF4 = 100;
 
 // Largest decode batch of the GEMV kernels.
@@ -33,12 +34,27 @@ struct GemvArgs {
     const void* seg_w[kMaxSegments];
     float* seg_y[kMaxSegments];
     int seg_rows[kMaxSegments];
+    // Greedy head (q8_0 / Q4_K / Q6_K / GF4 chunked kernel only): when am_token
+    // is set, y is not written; each workgroup writes the largest of its rows'
+    // results per batch row b (ties to the smaller row, NaN never chosen) to
+    // am_logit / am_token[blockIdx.x * n_batch + b].
+    uint32_t* am_token;
+    float* am_logit;
 };
 
 // Each launcher validates nothing (the C ABI does) and returns the launch status.
 hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream);
+hipError_t launch_q6_k_gemv(const GemvArgs& a, hipStream_t stream);
+
+// Greedy head: workgroups of the GEMV launch that launch_argmax_gemv makes for
+// (type_id, rows, k, n_batch) -- the number of partials per batch row.
+int argmax_groups(uint32_t type_id, int rows, int k, int n_batch);
+// GEMV with the argmax epilogue (a.am_token / a.am_logit hold
+// argmax_groups(...) * n_batch partials), then the reduction of the partials to
+// token[b], logit[b].
+hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* token, float* logit, hipStream_t stream);
 // GF4 on the chunked k-quant kernel structure (rolling prefetch, per-chunk
 // activation staging); launch_gf4_gemv picks between the two.
 hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream);

@@ -7,6 +7,7 @@ Names and argument meaning follow the reference runtime's encoders
 * ``ffn_gate_up_swiglu``  <- ``encodeGf4FusedFfn`` / ``qw35_ffn_gate_up_swiglu_gf4_f32`` (:13-35)
 * ``matvec_batch``        <- ``encodeMatvecBatch`` (:260-306)
 * ``matmul_prefill``      <- ``encodeTiledKMatmul`` / ``qw35_mul_mm_gf4_f32`` (:309-366)
+* ``output_argmax``       <- the greedy path of ``encodeOutputHead`` (Qw35MetalRuntime+Output.m:11-65)
 * ``dequantize``          <- the per-codec dequant helpers / ``qw35_get_rows_*`` gathers
 * ``DecodePlan``          <- the per-token recording of ``evalToken`` (Qw35MetalRuntime.m:807-880)
 * ``quantize``            <- ``pack_ffn_gf4`` / ``pack_gf4_prepared`` (tools/qw35_cook_common.py:83-119,182-199)
@@ -23,12 +24,13 @@ from dataclasses import dataclass
 import torch
 
 from . import _ffi
-from ._ffi import Qw35Error, TYPE_GF4, TYPE_Q4_K, TYPE_Q8_0  # noqa: F401
+from ._ffi import Qw35Error, TYPE_GF4, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
 
 _ROW_BYTES = {
     TYPE_GF4: lambda k: (k + 7) // 8 * 4,
     TYPE_Q8_0: lambda k: (k + 31) // 32 * 34,
     TYPE_Q4_K: lambda k: (k + 255) // 256 * 144,
+    TYPE_Q6_K: lambda k: (k + 255) // 256 * 210,
 }
 
 
@@ -126,6 +128,37 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
     _ffi.call("qw35_hip_ffn_gate_up_swiglu", C.byref(gate.view), C.byref(up.view), _ptr(x), _ptr(awq), _ptr(dst),
               nb, _stream(stream))
     return dst
+
+
+def output_argmax_workspace(w: HipWeight, n_batch: int, device="cuda") -> torch.Tensor:
+    """Device bytes for ``output_argmax`` (size from the C ABI, +256 for alignment)."""
+    need = int(_ffi.load().qw35_hip_output_argmax_workspace_size(C.byref(w.view), n_batch))
+    if need == 0:
+        raise Qw35Error("output_argmax: invalid weight or batch")
+    return torch.empty(need + 256, dtype=torch.uint8, device=device)
+
+
+def output_argmax(w: HipWeight, x: torch.Tensor, awq: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None, stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Greedy head: per batch row, (token, logit) of the largest ``W @ (awq * x)``
+    entry (ties to the smaller row, NaN never chosen), without materialising
+    the logits.  Returns (tokens [n_batch] int32 holding the uint32 row ids --
+    0xFFFFFFFF reads as -1 -- and fp32 logits [n_batch]), written on ``stream``."""
+    nb = _check_act(x, w.k, "x")
+    need = int(_ffi.load().qw35_hip_output_argmax_workspace_size(C.byref(w.view), nb))
+    if need == 0:
+        raise Qw35Error("output_argmax: invalid weight or batch")
+    if workspace is None:
+        workspace = output_argmax_workspace(w, nb, device=x.device)
+    base = workspace.data_ptr()
+    pad = (-base) % 256
+    if workspace.numel() - pad < need:
+        raise Qw35Error(f"output_argmax: workspace needs {need} bytes after 256-byte alignment")
+    token = torch.empty(nb, dtype=torch.int32, device=x.device)
+    logit = torch.empty(nb, dtype=torch.float32, device=x.device)
+    _ffi.call("qw35_hip_output_argmax", C.byref(w.view), _ptr(x), _ptr(awq), nb, _ptr(token), _ptr(logit),
+              C.c_void_p(base + pad), C.c_uint64(workspace.numel() - pad), _stream(stream))
+    return token, logit
 
 
 def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tensor:

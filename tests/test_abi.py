@@ -63,7 +63,7 @@ def _weight(type_id=100, k=4096, rows=16, data=4096, nbytes=None):
     w.data = data
     w.k = k
     w.rows = rows
-    rb = {100: k // 8 * 4, 8: k // 32 * 34, 12: k // 256 * 144}.get(type_id, 0)
+    rb = {100: k // 8 * 4, 8: k // 32 * 34, 12: k // 256 * 144, 14: k // 256 * 210}.get(type_id, 0)
     w.bytes = nbytes if nbytes is not None else rb * rows
     w.type_id = type_id
     return w
@@ -77,7 +77,7 @@ def _call_matvec(w, x=4096, dst=4096, nb=1, awq=None):
 @pytest.mark.parametrize(
     "kwargs,needle",
     [
-        (dict(type_id=14), "unsupported tensor type 14"),
+        (dict(type_id=13), "unsupported tensor type 13"),
         (dict(k=100), "multiple of 256"),
         (dict(k=16384), "<= 12288"),
         (dict(rows=0), "rows=0"),
@@ -131,7 +131,7 @@ def test_weight_view_validates_descriptor(lib):
 
 
 def test_error_buffer_truncates_safely(lib):
-    w = _weight(type_id=14)
+    w = _weight(type_id=13)
     err = C.create_string_buffer(8)
     rc = lib.qw35_hip_decode_matvec(C.byref(w), C.c_void_p(4096), None, C.c_void_p(4096), 1, 0, None, err, 8)
     assert rc == 0 and len(err.value) == 7
@@ -140,7 +140,8 @@ def test_error_buffer_truncates_safely(lib):
 @pytest.mark.parametrize(
     "type_id,k,rows,needle",
     [
-        (14, 256, 1, "unsupported tensor type 14"),
+        (13, 256, 1, "unsupported tensor type 13"),
+        (14, 512 + 32, 1, "multiple of 256 for q6_k"),
         (100, 12, 1, "multiple of 8 for gf4"),
         (8, 48, 1, "multiple of 32 for q8_0"),
         (12, 512 + 32, 1, "multiple of 256 for q4_k"),
@@ -178,7 +179,7 @@ def _plan_op(kind=0, w=None, up=None, x=4096, dst=4096, nb=1, residual=0):
         ([], "no ops"),
         ([dict(kind=7)], "op 0: unknown kind 7"),
         ([dict(), dict(nb=9)], "op 1: n_batch=9"),
-        ([dict(), dict(wkw=dict(type_id=14))], "op 1: unsupported tensor type 14"),
+        ([dict(), dict(wkw=dict(type_id=13))], "op 1: unsupported tensor type 13"),
         ([dict(kind=0, up=True)], "op 0: a MATVEC op takes no w_up"),
         ([dict(kind=1, up=True, residual=1)], "op 0: a SWIGLU op has no residual form"),
         ([dict(kind=1, up=True, upkw=dict(k=8192))], "op 0: gate and up must share type and shape"),
@@ -220,3 +221,52 @@ def test_stream_read_validates(lib):
         _ffi.call("qw35_hip_stream_read", C.c_void_p(4096), 0, C.c_void_p(4096), None)
     with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
         _ffi.call("qw35_hip_stream_read", C.c_void_p(4096), 24, C.c_void_p(4096), None)
+
+
+def test_q6k_weight_needs_aligned_rows(lib):
+    with pytest.raises(_ffi.Qw35Error, match=re.escape("q6_k needs k % 2048 == 0")):
+        _call_matvec(_weight(type_id=14, k=1280))
+    _ffi.call("qw35_hip_weight_view", C.byref(_q6k_desc(4096)), C.c_void_p(1 << 20), C.byref(_ffi.Weight()))
+
+
+def _q6k_desc(k, rows=8):
+    d = _ffi.TensorDesc()
+    d.dims[0], d.dims[1], d.dims[2], d.dims[3] = k, rows, 1, 1
+    d.n_dims = 2
+    d.type_id = 14
+    d.abs_offset = 0
+    d.bytes = rows * k // 256 * 210
+    d.elements = k * rows
+    return d
+
+
+def test_swiglu_rejects_q6k(lib):
+    g = _weight(type_id=14)
+    with pytest.raises(_ffi.Qw35Error, match="no fused gate/up"):
+        _ffi.call("qw35_hip_ffn_gate_up_swiglu", C.byref(g), C.byref(g), C.c_void_p(4096), None, C.c_void_p(4096), 1,
+                  None)
+
+
+def test_output_argmax_workspace_and_validation(lib):
+    w = _weight(type_id=14, k=4096, rows=248320)
+    n1 = lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 1)
+    n8 = lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 8)
+    assert n1 > 0 and n8 > n1 and n1 % 256 == 0 and n8 % 256 == 0
+    assert lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 0) == 0
+    assert lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 9) == 0
+    assert lib.qw35_hip_output_argmax_workspace_size(C.byref(_weight(type_id=13)), 1) == 0
+
+    def call(x=4096, tok=4096, lg=4096, ws=1 << 20, ws_bytes=None, nb=1):
+        return _ffi.call("qw35_hip_output_argmax", C.byref(w), C.c_void_p(x), None, nb, C.c_void_p(tok),
+                         C.c_void_p(lg), C.c_void_p(ws), C.c_uint64(n1 if ws_bytes is None else ws_bytes), None)
+
+    with pytest.raises(_ffi.Qw35Error, match="null input, output or workspace"):
+        call(ws=0)
+    with pytest.raises(_ffi.Qw35Error, match="n_batch=9"):
+        call(nb=9)
+    with pytest.raises(_ffi.Qw35Error, match="workspace must be 256-byte aligned"):
+        call(ws_bytes=n1 - 256)
+    with pytest.raises(_ffi.Qw35Error, match="workspace must be 256-byte aligned"):
+        call(ws=(1 << 20) + 16)
+    with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
+        call(x=4100)
