@@ -526,17 +526,32 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
 }
 
 // Final reduction of the greedy-head partials: block b reduces batch row b.
-__global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint32_t* __restrict__ pt,
-                                                            const float* __restrict__ pv, int n_groups, int n_batch,
-                                                            uint32_t* __restrict__ token, float* __restrict__ logit) {
-    __shared__ float sv[4];
-    __shared__ uint32_t sid[4];
+// Each thread issues kArgmaxLoads loads before comparing, so one pass over
+// the partials costs one memory latency (a 248320-row head has 7760 groups).
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxLoads = 8;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_reduce_kernel(const uint32_t* __restrict__ pt,
+                                                                       const float* __restrict__ pv, int n_groups,
+                                                                       int n_batch, uint32_t* __restrict__ token,
+                                                                       float* __restrict__ logit) {
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ uint32_t sid[kArgmaxThreads / 64];
     const int b = blockIdx.x;
     float best = -__builtin_inff();
     uint32_t best_id = 0xFFFFFFFFu;
-    for (int g = threadIdx.x; g < n_groups; g += 256) {
-        const float v = pv[(size_t)g * n_batch + b];
-        if (!__builtin_isnan(v)) argmax_take(best, best_id, v, pt[(size_t)g * n_batch + b]);
+    for (int g0 = threadIdx.x; g0 < n_groups; g0 += kArgmaxThreads * kArgmaxLoads) {
+        float v[kArgmaxLoads];
+        uint32_t id[kArgmaxLoads];
+#pragma unroll
+        for (int u = 0; u < kArgmaxLoads; ++u) {
+            const int g = g0 + u * kArgmaxThreads;
+            v[u] = g < n_groups ? pv[(size_t)g * n_batch + b] : -__builtin_inff();
+            id[u] = g < n_groups ? pt[(size_t)g * n_batch + b] : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int u = 0; u < kArgmaxLoads; ++u)
+            if (!__builtin_isnan(v[u])) argmax_take(best, best_id, v[u], id[u]);
     }
     wave_argmax(best, best_id);
     if ((threadIdx.x & 63) == 0) {
@@ -547,7 +562,7 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint32_t* __re
     if (threadIdx.x == 0) {
         float v = sv[0];
         uint32_t id = sid[0];
-        for (int w = 1; w < 4; ++w) argmax_take(v, id, sv[w], sid[w]);
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_take(v, id, sv[w], sid[w]);
         token[b] = id;
         logit[b] = v;
     }
@@ -717,8 +732,8 @@ hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* tok
     }
     if (e != hipSuccess) return e;
     const int groups = argmax_groups(type_id, a.rows, a.k, a.n_batch);
-    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(a.n_batch), dim3(256), 0, stream, a.am_token, a.am_logit, groups,
-                       a.n_batch, token, logit);
+    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(a.n_batch), dim3(kArgmaxThreads), 0, stream, a.am_token,
+                       a.am_logit, groups, a.n_batch, token, logit);
     return hipGetLastError();
 }
 
