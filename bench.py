@@ -162,8 +162,9 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
     """Config 4: GF4 prefill dequant-matmul, W 12288x4096 and 4096x12288 (12
     rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out; the staged
     path (workspace, fp16 MFMA; the time includes the staging pass) and the
-    direct path (bf16 MFMA).  Utilisation is reported against the nominal
-    2.5 PFLOP/s and against the MFMA probe's sustained rate on this box."""
+    direct path (bf16 MFMA).  Then the q8_0 projections through their fp16
+    prefill image (6 rotated copies).  Utilisation is reported against the
+    nominal 2.5 PFLOP/s and against the MFMA probe's sustained rate on this box."""
     ceiling = mfma_ceiling(b, rt, torch)
     out = {"mfma_probe_TFLOP/s": round(ceiling, 1)}
     for rows, k in ((12288, 4096), (4096, 12288)):
@@ -183,6 +184,28 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
                     "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
                     "frac_of_probe": round(tflops / ceiling, 4)}
         del ws
+    # k-quant projections (q8_0 attention/SSM q, out): the F16 prefill image,
+    # made once per weight at load time, contracted on fp16 MFMA.
+    for rows, k in ((8192, 4096), (4096, 4096)):
+        q8 = [b.weight(rt.TYPE_Q8_0, rows, k) for _ in range(6)]
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        imgs = [w.prefill for w in q8]
+        ev1.record()
+        torch.cuda.synchronize()
+        out[f"prefill_image_q8_0_{rows}x{k}_us"] = round(ev0.elapsed_time(ev1) * 1e3 / len(q8), 2)
+        for m in (128, 512, 2048):
+            a = b.normal((m, k)).to(torch.bfloat16)
+            c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
+            wsp = rt.prefill_workspace(imgs[0], m, device=b.dev)
+            calls = [lambda s, w=w: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in imgs]
+            ms, _, _ = b.time_calls(calls, max(24, 4800 // m), 12)
+            tflops = 2.0 * m * rows * k / (ms * 1e-3) / 1e12
+            out[f"prefill_q8_0_f16img_m{m}_{rows}x{k}"] = {
+                "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
+                "frac_of_probe": round(tflops / ceiling, 4)}
+        del q8, imgs
     return out
 
 

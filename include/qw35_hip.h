@@ -18,8 +18,11 @@
  *   type 100  GF4   8 elems / 4 B   (tools/gguf_custom_types.py:26-30)
  *   type   8  q8_0 32 elems / 34 B  (qw35-server/src/loader/tensors.rs:142)
  *   type  12  Q4_K 256 elems / 144 B (qw35-server/src/loader/tensors.rs:146)
- *   type  14  Q6_K 256 elems / 210 B (qw35-server/src/loader/tensors.rs:150;
+ *   type  14  Q6_K 256 elems / 210 B (qw35-server/src/loader/tensors.rs:148;
  *             block qw35_block_q6_k, qw35-server/src/metal/qw35_types.metal:17-22)
+ *   type   1  F16  1 elem / 2 B (tensors.rs:137): the prefill matmul's weight
+ *             form for the k-quants (see qw35_hip_dequantize_f16); the GEMVs
+ *             reject it
  * Shape limits of this build: k % 256 == 0 and 256 <= k <= 12288 (every
  * Qwen3.5-9B projection has k = 4096 or 12288; Q6_K also needs k % 2048 == 0
  * so that its 210-byte super-block rows stay 16-byte aligned), rows >= 1,
@@ -35,6 +38,7 @@
 extern "C" {
 #endif
 
+#define QW35_HIP_TYPE_F16 1u
 #define QW35_HIP_TYPE_Q8_0 8u
 #define QW35_HIP_TYPE_Q4_K 12u
 #define QW35_HIP_TYPE_Q6_K 14u
@@ -122,6 +126,16 @@ int qw35_hip_output_argmax(const qw35_hip_weight *w, const float *x, const float
 int qw35_hip_dequantize(const qw35_hip_weight *w, const uint32_t *row_ids, uint32_t n_rows, float *dst,
                         void *stream, char *err, uintptr_t err_len);
 
+/* fp16 prefill image of a weight: dst (device, 16-byte aligned, rows * k
+ * halves, row-major) = fp16_rne(dequantised W), the exact value for GF4 and
+ * the rounding the reference's tiled matmul applies when it dequantises a
+ * k-quant weight tile to half (qw35_kernel_mul_mm, qw35-server/src/metal/
+ * qw35_tiled_mm.metal:199-255).  Viewed as a type-1 (F16) weight it is the
+ * operand of qw35_hip_matmul_prefill for q8_0 / Q4_K / Q6_K projections; made
+ * once and kept resident (2 bytes per weight: about 4.2 GB for the 9B's q8_0
+ * projections). */
+int qw35_hip_dequantize_f16(const qw35_hip_weight *w, void *dst, void *stream, char *err, uintptr_t err_len);
+
 /* Decode-step plan: a fixed sequence of projection GEMVs recorded once into a
  * hipGraph and replayed per token.  Replaces the per-token recording of the
  * projection dispatches in evalToken / encodeDecodeLayers
@@ -153,14 +167,16 @@ int qw35_hip_plan_launch(void *plan, void *stream, char *err, uintptr_t err_len)
 uint32_t qw35_hip_plan_size(const void *plan);
 void qw35_hip_plan_destroy(void *plan);
 
-/* Multi-token (prefill) matmul of a GF4 weight on MFMA:
+/* Multi-token (prefill) matmul of a GF4 or F16 weight on MFMA:
  *   c[t][r] = sum_k bf16_rne(awq[k] * a[t][k]) * W[r][k]    (awq == NULL: a[t][k] as bf16)
  * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32
  * (fp32 input is rounded to bf16 after the AWQ multiply); c: device
  * [n_tokens][rows], c_dtype QW35_HIP_DTYPE_BF16 (round-to-nearest-even) or
  * QW35_HIP_DTYPE_F32; fp32 accumulation.  Replaces encodeMatvecBatch /
  * encodeTiledKMatmul for type 100 (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366,
- * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255).  GF4 only;
+ * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255) and, through
+ * an F16 weight (the prefill image of qw35_hip_dequantize_f16), for the
+ * q8_0 / Q4_K / Q6_K projections (qw35_mul_mm_{q4_k,q6_k,q8_0}_f32, :209-214,243-255).
  * 1 <= n_tokens <= 65536, rows <= 2^24. */
 #define QW35_HIP_DTYPE_F32 0u
 #define QW35_HIP_DTYPE_BF16 1u
@@ -176,7 +192,8 @@ void qw35_hip_plan_destroy(void *plan);
  * on the weight's shape and n_tokens (0: invalid weight or n_tokens); a
  * smaller workspace that still holds the staged activations (2 bytes per
  * activation plus 4 per token, each part rounded up to 256 bytes) is
- * accepted and splits K less. */
+ * accepted and splits K less.  F16 weights always take the staged path (the
+ * workspace is required, and the staged activations are all it holds). */
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight *w, uint32_t n_tokens);
 int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
                             uint32_t c_dtype, uint32_t n_tokens, void *workspace, uint64_t workspace_bytes,

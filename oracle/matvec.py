@@ -25,6 +25,7 @@ TYPE_GF4 = gf4.GF4_TYPE_ID
 TYPE_Q8_0 = q8_0.Q8_0_TYPE_ID
 TYPE_Q4_K = q4_k.Q4_K_TYPE_ID
 TYPE_Q6_K = q6_k.Q6_K_TYPE_ID
+TYPE_F16 = 1
 
 
 def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
@@ -38,6 +39,8 @@ def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
     if type_id == TYPE_Q6_K:
         assert k % q6_k.Q6_K_BLOCK_ELEMS == 0
         return rows * (k // q6_k.Q6_K_BLOCK_ELEMS) * q6_k.Q6_K_BLOCK_BYTES
+    if type_id == TYPE_F16:
+        return rows * k * 2
     raise ValueError(f"unsupported type id {type_id}")
 
 
@@ -51,6 +54,8 @@ def quantize(type_id: int, w: np.ndarray) -> np.ndarray:
         return q4_k.q4_k_quantize(w)
     if type_id == TYPE_Q6_K:
         return q6_k.q6_k_quantize(w).reshape(w.shape[0], -1)
+    if type_id == TYPE_F16:
+        return np.asarray(w, dtype=np.float32).astype(np.float16).view(np.uint8).reshape(w.shape[0], -1)
     raise ValueError(f"unsupported type id {type_id}")
 
 
@@ -65,6 +70,8 @@ def dequant(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
         return q4_k.q4_k_dequant(raw)
     if type_id == TYPE_Q6_K:
         return q6_k.q6_k_dequant(raw, rows, raw.size // rows // q6_k.Q6_K_BLOCK_BYTES * q6_k.Q6_K_BLOCK_ELEMS)
+    if type_id == TYPE_F16:
+        return raw.view("<f2").astype(np.float32)
     raise ValueError(f"unsupported type id {type_id}")
 
 
@@ -145,3 +152,10 @@ def argmax_rule(logits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
             ids[b] = np.flatnonzero(ok & (row == m))[0]
             best[b] = m
     return ids, best
+
+
+def prefill_image(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """The fp16 prefill image of a weight: fp16_rne of the exact dequantised
+    value (numpy's float32 -> float16 cast rounds to nearest even), the half
+    dequantisation of the reference's tiled matmul (qw35_tiled_mm.metal:199-255)."""
+    return dequant(type_id, raw, rows, k).astype(np.float16)

@@ -12,6 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libqw35_hip.so"
 
+TYPE_F16 = 1
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
 TYPE_Q6_K = 14
@@ -93,6 +94,7 @@ PROTOTYPES: dict[str, tuple] = {
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
     ),
+    "qw35_hip_dequantize_f16": (C.c_int, [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
     "qw35_hip_plan_create": (C.c_void_p, [C.POINTER(PlanOp), C.c_uint32, C.c_char_p, C.c_size_t]),
     "qw35_hip_plan_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
     "qw35_hip_plan_size": (C.c_uint32, [C.c_void_p]),

@@ -21,7 +21,8 @@ void set_err(char* err, uintptr_t err_len, const char* fmt, ...) {
 }
 
 bool type_supported(uint32_t t) {
-    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K || t == qw35::kTypeQ6_K;
+    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K || t == qw35::kTypeQ6_K ||
+           t == qw35::kTypeF16;
 }
 
 uint64_t row_bytes(uint32_t t, uint64_t k) {
@@ -30,6 +31,7 @@ uint64_t row_bytes(uint32_t t, uint64_t k) {
         case qw35::kTypeQ8_0: return (k + 31) / 32 * 34;
         case qw35::kTypeQ4_K: return (k + 255) / 256 * 144;
         case qw35::kTypeQ6_K: return (k + 255) / 256 * 210;
+        case qw35::kTypeF16: return k * 2;
         default: return 0;
     }
 }
@@ -40,6 +42,7 @@ const char* type_name(uint32_t t) {
         case qw35::kTypeQ8_0: return "q8_0";
         case qw35::kTypeQ4_K: return "q4_k";
         case qw35::kTypeQ6_K: return "q6_k";
+        case qw35::kTypeF16: return "f16";
         default: return "unsupported";
     }
 }
@@ -103,9 +106,19 @@ hipError_t dispatch_gemv(uint32_t type_id, const qw35::GemvArgs& a, hipStream_t 
     }
 }
 
+// F16 tensors are prefill images: the GEMV kernels take the quantised bytes.
+bool check_gemv_type(const qw35_hip_weight* w, const char* what, char* err, uintptr_t err_len) {
+    if (w->type_id == qw35::kTypeF16) {
+        set_err(err, err_len, "%s: f16 weights serve the prefill matmul only (the GEMVs take gf4/q8_0/q4_k/q6_k)",
+                what);
+        return false;
+    }
+    return true;
+}
+
 bool check_matvec(const qw35_hip_weight* w, const float* x, const float* awq, const float* dst, uint32_t n_batch,
                   const char* what, char* err, uintptr_t err_len) {
-    if (!check_weight(w, what, err, err_len)) return false;
+    if (!check_weight(w, what, err, err_len) || !check_gemv_type(w, what, err, err_len)) return false;
     if (!x || !dst) {
         set_err(err, err_len, "%s: null input or output", what);
         return false;
@@ -360,17 +373,30 @@ int qw35_hip_dequantize(const qw35_hip_weight* w, const uint32_t* row_ids, uint3
         return 0;
     }
     return check_hip(qw35::launch_dequant(w->type_id, w->data, (int)w->rows, (int)w->k, row_ids, out_rows, dst,
-                                          static_cast<hipStream_t>(stream)),
+                                          false, static_cast<hipStream_t>(stream)),
                      "dequantize", err, err_len)
+               ? 1
+               : 0;
+}
+
+int qw35_hip_dequantize_f16(const qw35_hip_weight* w, void* dst, void* stream, char* err, uintptr_t err_len) {
+    if (!check_weight(w, "dequantize_f16", err, err_len)) return 0;
+    if (!dst || ((uintptr_t)dst & 15u)) {
+        set_err(err, err_len, "dequantize_f16: dst must be non-null and 16-byte aligned");
+        return 0;
+    }
+    return check_hip(qw35::launch_dequant(w->type_id, w->data, (int)w->rows, (int)w->k, nullptr, (int)w->rows, dst,
+                                          true, static_cast<hipStream_t>(stream)),
+                     "dequantize_f16", err, err_len)
                ? 1
                : 0;
 }
 
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
     char msg[8];
-    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || w->type_id != qw35::kTypeGF4 || n_tokens < 1 ||
-        n_tokens > 65536)
-        return 0;
+    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || n_tokens < 1 || n_tokens > 65536) return 0;
+    if (w->type_id == qw35::kTypeF16) return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->k);
+    if (w->type_id != qw35::kTypeGF4) return 0;
     return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
 }
 
@@ -378,8 +404,10 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
                             uint32_t c_dtype, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes,
                             void* stream, char* err, uintptr_t err_len) {
     if (!check_weight(w, "matmul_prefill", err, err_len)) return 0;
-    if (w->type_id != qw35::kTypeGF4) {
-        set_err(err, err_len, "matmul_prefill: only GF4 (type 100) weights are supported, got %s",
+    if (w->type_id != qw35::kTypeGF4 && w->type_id != qw35::kTypeF16) {
+        set_err(err, err_len,
+                "matmul_prefill: GF4 (type 100) or F16 (type 1) weights, got %s; make the fp16 prefill image of a "
+                "k-quant weight with qw35_hip_dequantize_f16",
                 type_name(w->type_id));
         return 0;
     }
@@ -402,6 +430,20 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
     if (((uintptr_t)a & 15u) || (awq && ((uintptr_t)awq & 15u)) || ((uintptr_t)c & 3u)) {
         set_err(err, err_len, "matmul_prefill: a/awq must be 16-byte aligned and c 4-byte aligned");
         return 0;
+    }
+    if (w->type_id == qw35::kTypeF16) {
+        const uint64_t need = qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->k);
+        if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
+            set_err(err, err_len, "matmul_prefill: f16 weights need a 256-byte aligned workspace of >= %llu bytes",
+                    (unsigned long long)need);
+            return 0;
+        }
+        return check_hip(qw35::launch_f16w_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
+                                                   awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace,
+                                                   static_cast<hipStream_t>(stream)),
+                         "matmul_prefill", err, err_len)
+                   ? 1
+                   : 0;
     }
     if (workspace) {
         const uint64_t need =
@@ -426,7 +468,8 @@ int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_
         set_err(err, err_len, "quantize: unsupported tensor type %u", type_id);
         return 0;
     }
-    const uint64_t block = type_id == qw35::kTypeGF4 ? 8 : type_id == qw35::kTypeQ8_0 ? 32 : 256;
+    const uint64_t block =
+        (type_id == qw35::kTypeGF4 || type_id == qw35::kTypeF16) ? 8 : type_id == qw35::kTypeQ8_0 ? 32 : 256;
     if (k == 0 || k % block != 0 || k > 0x7fffffffull) {
         set_err(err, err_len, "quantize: k=%llu must be a positive multiple of %llu for %s",
                 (unsigned long long)k, (unsigned long long)block, type_name(type_id));
@@ -460,14 +503,17 @@ static uint64_t argmax_ws_part(const qw35_hip_weight* w, uint32_t n_batch) {
 
 uint64_t qw35_hip_output_argmax_workspace_size(const qw35_hip_weight* w, uint32_t n_batch) {
     char msg[8];
-    if (!check_weight(w, "output_argmax", msg, sizeof msg) || n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) return 0;
+    if (!check_weight(w, "output_argmax", msg, sizeof msg) || w->type_id == qw35::kTypeF16 || n_batch < 1 ||
+        n_batch > QW35_HIP_MAX_BATCH)
+        return 0;
     return 2 * argmax_ws_part(w, n_batch);
 }
 
 int qw35_hip_output_argmax(const qw35_hip_weight* w, const float* x, const float* awq, uint32_t n_batch,
                            uint32_t* token, float* logit, void* workspace, uint64_t workspace_bytes, void* stream,
                            char* err, uintptr_t err_len) {
-    if (!check_weight(w, "output_argmax", err, err_len)) return 0;
+    if (!check_weight(w, "output_argmax", err, err_len) || !check_gemv_type(w, "output_argmax", err, err_len))
+        return 0;
     if (!x || !token || !logit || !workspace) {
         set_err(err, err_len, "output_argmax: null input, output or workspace");
         return 0;

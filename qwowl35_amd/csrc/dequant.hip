@@ -1,4 +1,5 @@
-// fp32 dequantisation of GF4 / q8_0 / Q4_K / Q6_K tensors, optionally gathering rows.
+// fp32 (or fp16) dequantisation of GF4 / q8_0 / Q4_K / Q6_K / F16 tensors,
+// optionally gathering rows.
 //
 // This is the library's bit-exact statement of each format (every weight of
 // all three codecs is exact in fp32, so results are compared bit-for-bit with
@@ -21,11 +22,13 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
-// One thread per output group of 8 columns.
+// One thread per output group of 8 columns; F16_OUT writes fp16 RNE of the
+// same values (the prefill image of a quantised weight).
 // A gathered row id >= rows yields a row of zeros (no out-of-bounds read).
+template <bool F16_OUT>
 __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const uint8_t* __restrict__ w, int rows,
                                                       int k, const uint32_t* __restrict__ row_ids, int n_out_rows,
-                                                      float* __restrict__ dst) {
+                                                      void* __restrict__ dst) {
     const int groups = k >> 3;
     const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= (size_t)n_out_rows * groups) return;
@@ -51,6 +54,14 @@ __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const ui
         const float d = f16_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = d * (float)(int8_t)blk[2 + (col & 31) + i];
+    } else if (type_id == kTypeF16) {
+        const uint4_t u = *reinterpret_cast<const uint4_t*>(w + (src_row * (size_t)k + 8 * g) * 2);
+        const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = f16_to_f32(h[i] & 0xFFFFu);
+            v[2 * i + 1] = f16_to_f32(h[i] >> 16);
+        }
     } else if (type_id == kTypeQ6_K) {
         const uint8_t* row = w + src_row * (size_t)(k >> 8) * 210;
         const int col = 8 * g;
@@ -92,20 +103,30 @@ __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const ui
             v[i] = dsc * (float)q - mm;
         }
     }
-    float* o = dst + (size_t)out_row * k + 8 * g;
-    *reinterpret_cast<float4_t*>(o) = float4_t{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<float4_t*>(o + 4) = float4_t{v[4], v[5], v[6], v[7]};
+    if constexpr (F16_OUT) {
+        uint16_t* o = static_cast<uint16_t*>(dst) + (size_t)out_row * k + 8 * g;
+        *reinterpret_cast<uint4_t*>(o) =
+            uint4_t{as_u32(h2(v[0], v[1])), as_u32(h2(v[2], v[3])), as_u32(h2(v[4], v[5])), as_u32(h2(v[6], v[7]))};
+    } else {
+        float* o = static_cast<float*>(dst) + (size_t)out_row * k + 8 * g;
+        *reinterpret_cast<float4_t*>(o) = float4_t{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<float4_t*>(o + 4) = float4_t{v[4], v[5], v[6], v[7]};
+    }
 }
 
 }  // namespace
 
 hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, const uint32_t* row_ids,
-                          int n_out_rows, float* dst, hipStream_t stream) {
+                          int n_out_rows, void* dst, bool f16_out, hipStream_t stream) {
     const size_t total = (size_t)n_out_rows * (size_t)(k >> 3);
     if (total == 0) return hipSuccess;
     const unsigned grid = (unsigned)((total + 255) / 256);
-    hipLaunchKernelGGL(dequant_kernel, dim3(grid), dim3(256), 0, stream, type_id, static_cast<const uint8_t*>(w), rows, k,
-                       row_ids, n_out_rows, dst);
+    if (f16_out)
+        hipLaunchKernelGGL((dequant_kernel<true>), dim3(grid), dim3(256), 0, stream, type_id,
+                           static_cast<const uint8_t*>(w), rows, k, row_ids, n_out_rows, dst);
+    else
+        hipLaunchKernelGGL((dequant_kernel<false>), dim3(grid), dim3(256), 0, stream, type_id,
+                           static_cast<const uint8_t*>(w), rows, k, row_ids, n_out_rows, dst);
     return hipGetLastError();
 }
 

@@ -1,4 +1,4 @@
-// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K / Q6_K tensor bytes, on the GPU.
+// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K / Q6_K / F16 tensor bytes, on the GPU.
 //
 // GF4 is the reference packer pack_gf4_prepared(rows, scale_search=False)
 // (tools/qw35_cook_common.py:83-119), including the optional AWQ column
@@ -265,6 +265,31 @@ __global__ __launch_bounds__(kEncodeThreads) void q6_k_quantize_kernel(const flo
     }
 }
 
+// F16 (GGUF type 1): fp16 round-to-nearest-even of (col_scale *) x, 8 per thread.
+__global__ __launch_bounds__(kEncodeThreads) void f16_quantize_kernel(const float* __restrict__ src,
+                                                                      const float* __restrict__ col_scale,
+                                                                      uint16_t* __restrict__ dst, uint64_t n_groups,
+                                                                      uint32_t groups_per_row) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_groups;
+         i += (uint64_t)gridDim.x * kEncodeThreads) {
+        float v[8];
+        const float4_t a = *reinterpret_cast<const float4_t*>(src + 8 * i);
+        const float4_t b = *reinterpret_cast<const float4_t*>(src + 8 * i + 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[q] = a[q];
+            v[4 + q] = b[q];
+        }
+        if (col_scale) {
+            const float* cs = col_scale + 8u * (uint32_t)(i % groups_per_row);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = __fmul_rn(v[q], cs[q]);
+        }
+        *reinterpret_cast<uint4_t*>(dst + 8 * i) =
+            uint4_t{as_u32(h2(v[0], v[1])), as_u32(h2(v[2], v[3])), as_u32(h2(v[4], v[5])), as_u32(h2(v[6], v[7]))};
+    }
+}
+
 unsigned grid_for(uint64_t n) {
     const uint64_t g = (n + kEncodeThreads - 1) / kEncodeThreads;
     return (unsigned)(g < (uint64_t)kEncodeBlocks ? g : (uint64_t)kEncodeBlocks);
@@ -286,6 +311,12 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
             const uint64_t n = r * (uint64_t)(k / 32);
             hipLaunchKernelGGL(q8_0_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
                                col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 32));
+            break;
+        }
+        case kTypeF16: {
+            const uint64_t n = r * (uint64_t)(k / 8);
+            hipLaunchKernelGGL(f16_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
+                               col_scale, static_cast<uint16_t*>(dst), n, (uint32_t)(k / 8));
             break;
         }
         case kTypeQ6_K: {

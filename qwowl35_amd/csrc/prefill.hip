@@ -22,7 +22,15 @@
 //   (the format of tools/qw35_cook_common.py:79 with c = q_raw ^ 4).
 // * Blocks are assigned XCD by XCD (consecutive block ids land on different
 //   XCDs), M-tile fastest, so the blocks that share a W tile share an L2.
+//
+// F16 weights (GGUF type 1) take a third kernel, f16w_prefill_kernel: the
+// staged fp16 tokens against fp16 weight tiles, both staged through LDS.  It
+// serves the q8_0 / Q4_K / Q6_K projections through their fp16 prefill image
+// (qw35_hip_dequantize_f16: fp16_rne of the exact dequantised weight), which
+// is the precision of the reference's tiled matmul: qw35_kernel_mul_mm
+// dequantises its weight tiles to half (qw35_tiled_mm.metal:199-255).
 #include <cmath>
+#include <type_traits>
 
 #include "gf4_decode.h"
 #include "qw35_device.h"
@@ -73,10 +81,11 @@ __device__ __forceinline__ uint4_t gf4_word_to_bf16x8(uint32_t w) {
 // exact in fp16 (smaller ones round at 2^-39 of the maximum), so the matmul
 // can contract on fp16 MFMA with the GF4 weights decoded by the 15-op fp16
 // decode of gf4_decode.h.  Each group of 8 columns is stored in the decode's
-// column order 0,4,1,5,2,6,3,7.
+// column order 0,4,1,5,2,6,3,7 (GF4_ORDER), or in column order for the F16
+// weight kernel.
 constexpr int kStageThreads = 256;
 
-template <bool A_F32, bool HAS_AWQ>
+template <bool A_F32, bool HAS_AWQ, bool GF4_ORDER = true>
 __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void* __restrict__ a,
                                                                       const float* __restrict__ awq, int k,
                                                                       uint16_t* __restrict__ a16,
@@ -141,8 +150,10 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
         const int g = threadIdx.x + j * kStageThreads;
         if (g >= groups) break;
         const float* x = v[j];
-        const uint4_t out{as_u32(h2(x[0] * sc, x[4] * sc)), as_u32(h2(x[1] * sc, x[5] * sc)),
-                          as_u32(h2(x[2] * sc, x[6] * sc)), as_u32(h2(x[3] * sc, x[7] * sc))};
+        const uint4_t out = GF4_ORDER ? uint4_t{as_u32(h2(x[0] * sc, x[4] * sc)), as_u32(h2(x[1] * sc, x[5] * sc)),
+                                                as_u32(h2(x[2] * sc, x[6] * sc)), as_u32(h2(x[3] * sc, x[7] * sc))}
+                                      : uint4_t{as_u32(h2(x[0] * sc, x[1] * sc)), as_u32(h2(x[2] * sc, x[3] * sc)),
+                                                as_u32(h2(x[4] * sc, x[5] * sc)), as_u32(h2(x[6] * sc, x[7] * sc))};
         *reinterpret_cast<uint4_t*>(a16 + (size_t)row * k + 8 * g) = out;
     }
 }
@@ -550,6 +561,157 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     }
 }
 
+// F16-weight path: fp16 A'' (prefill_stage_kernel, column order) against an
+// fp16 weight tensor [N][K] on v_mfma_f32_16x16x32_f16.
+//
+// * The layout of the direct path: a BM x BN tile per block, WGM x WGN waves,
+//   both operand tiles staged through LDS per 64-wide k step (double buffered,
+//   16-byte row padding), global loads two steps ahead in two register stages,
+//   one barrier per step; no conversion is left to do in the loader.
+// * The W tile is the MFMA's first operand: lane l accumulates
+//   D[n = 4 (l / 16) + r][m = l % 16], four consecutive outputs of one token
+//   row, scaled by the token's row_scale on the way out.
+template <int BM, int BN, int WGM, int WGN, bool OUT_F32>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2))) void f16w_prefill_kernel(
+    PrefillArgs p) {
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int WTM = BM / WGM;
+    constexpr int WTN = BN / WGN;
+    constexpr int FM = WTM / 16;
+    constexpr int FN = WTN / 16;
+    constexpr int AC = BM * 8 / NT;  // 16-byte token chunks per thread per step
+    constexpr int WC = BN * 8 / NT;  // 16-byte weight chunks per thread per step
+    constexpr int BUF = (BM + BN) * kLdsRow;
+    static_assert(AC >= 1 && WC >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tiles must split over the threads");
+    static_assert(FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "wave tile shape");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WGN;
+    const int wn = wave % WGN;
+    const int tiles = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if (tiles % kXcds == 0) t = (t % kXcds) * (tiles / kXcds) + t / kXcds;
+    const int m0 = (t % p.tiles_m) * BM;
+    const int n0 = (t / p.tiles_m) * BN;
+    const int K = p.k;
+    const uint16_t* a16 = static_cast<const uint16_t*>(p.a);
+    const uint16_t* w16 = reinterpret_cast<const uint16_t*>(p.w);
+
+    const uint16_t* a_src[AC];
+    const uint16_t* w_src[WC];
+    int a_lds[AC], w_lds[WC];
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+        const int c = tid + i * NT;
+        a_src[i] = a16 + (size_t)min(m0 + (c >> 3), p.m - 1) * K + (c & 7) * 8;
+        a_lds[i] = (c >> 3) * kLdsRow + (c & 7) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < WC; ++i) {
+        const int c = tid + i * NT;
+        w_src[i] = w16 + (size_t)min(n0 + (c >> 3), p.n - 1) * K + (c & 7) * 8;
+        w_lds[i] = (BM + (c >> 3)) * kLdsRow + (c & 7) * 16;
+    }
+    struct Regs {
+        uint4_t a[AC];
+        uint4_t w[WC];
+    };
+    auto load_step = [&](int kt, Regs& r) {
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int i = 0; i < AC; ++i) r.a[i] = *reinterpret_cast<const uint4_t*>(a_src[i] + k0);
+#pragma unroll
+        for (int i = 0; i < WC; ++i) r.w[i] = load_stream16(w_src[i] + k0);
+    };
+    auto store_step = [&](const Regs& r, uint8_t* buf) {
+#pragma unroll
+        for (int i = 0; i < AC; ++i) *reinterpret_cast<uint4_t*>(buf + a_lds[i]) = r.a[i];
+#pragma unroll
+        for (int i = 0; i < WC; ++i) *reinterpret_cast<uint4_t*>(buf + w_lds[i]) = r.w[i];
+    };
+
+    float4_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int a_rd = (wm * WTM + (lane & 15)) * kLdsRow + (lane >> 4) * 16;
+    const int b_rd = (BM + wn * WTN + (lane & 15)) * kLdsRow + (lane >> 4) * 16;
+    auto compute = [&](const uint8_t* cur) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            half8_t af[FM], wf[FN];
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                wf[j] = *reinterpret_cast<const half8_t*>(cur + b_rd + j * 16 * kLdsRow + ks * 64);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[i] = *reinterpret_cast<const half8_t*>(cur + a_rd + i * 16 * kLdsRow + ks * 64);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], af[i], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int KT = K / kBK;
+    uint8_t* buf0 = smem;
+    uint8_t* buf1 = smem + BUF;
+    Regs r0, r1;
+    load_step(0, r0);
+    if (KT > 1) load_step(1, r1);
+    store_step(r0, buf0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; kt += 2) {
+        if (kt + 2 < KT) load_step(kt + 2, r0);
+        compute(buf0);
+        if (kt + 1 < KT) store_step(r1, buf1);
+        __syncthreads();
+        if (kt + 1 >= KT) break;
+        if (kt + 3 < KT) load_step(kt + 3, r1);
+        compute(buf1);
+        if (kt + 2 < KT) store_step(r0, buf0);
+        __syncthreads();
+    }
+
+    const bool vec_ok = (p.n & 3) == 0 && ((uintptr_t)p.c & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int gm = m0 + wm * WTM + i * 16 + (lane & 15);
+        if (gm >= p.m) continue;
+        const float rs = p.row_scale[gm];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int gn = n0 + wn * WTN + j * 16 + (lane >> 4) * 4;
+            const size_t o = (size_t)gm * p.n + gn;
+            const float4_t d = acc[i][j] * rs;
+            if (vec_ok && gn + 3 < p.n) {
+                if constexpr (OUT_F32) {
+                    *reinterpret_cast<float4_t*>(static_cast<float*>(p.c) + o) = d;
+                } else {
+                    typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+                    *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(p.c) + o) =
+                        uint2_t{pack_bf16(d.x, d.y), pack_bf16(d.z, d.w)};
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (gn + r < p.n) {
+                        if constexpr (OUT_F32)
+                            static_cast<float*>(p.c)[o + r] = d[r];
+                        else
+                            static_cast<uint16_t*>(p.c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+                    }
+                }
+            }
+        }
+    }
+}
+
 // C[m][n] = row_scale[m] * sum_s partial[s][m][n], splits summed in order.
 // One thread per 4 consecutive outputs of a row.
 constexpr int kReduceThreads = 256;
@@ -800,6 +962,58 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     if (!af && tiles(256, 128) >= cus) return launch_tile<256, 128, 4, 2>(p, af, aw, of, stream);
     if (tiles(128, 128) >= cus) return launch_tile<128, 128, 2, 2>(p, af, aw, of, stream);
     return launch_tile<64, 64, 2, 2>(p, af, aw, of, stream);
+}
+
+size_t f16w_prefill_workspace_bytes(int m, int k) { return round256((size_t)m * k * 2) + round256((size_t)m * 4); }
+
+hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
+                               int m, int out_f32, void* workspace, hipStream_t stream) {
+    if (!workspace) return hipErrorInvalidValue;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
+    float* rs = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2));
+    const bool af = a_f32 != 0, aw = awq != nullptr;
+#define QW35_STAGE(AF, AW) \
+    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, false>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, a16, rs)
+    if (af) {
+        if (aw) QW35_STAGE(true, true); else QW35_STAGE(true, false);
+    } else {
+        if (aw) QW35_STAGE(false, true); else QW35_STAGE(false, false);
+    }
+#undef QW35_STAGE
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    PrefillArgs p{};
+    p.w = static_cast<const uint32_t*>(w);
+    p.a = a16;
+    p.c = c;
+    p.row_scale = rs;
+    p.m = m;
+    p.n = rows;
+    p.k = k;
+    p.splits = 1;
+    p.k_len = k;
+    // Largest tile that still gives every CU a block.
+    const long cus = num_cus();
+    auto ntiles = [&](int bm, int bn) { return (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn); };
+    auto go = [&](auto bm_c, auto bn_c) {
+        constexpr int BM = decltype(bm_c)::value, BN = decltype(bn_c)::value;
+        PrefillArgs q = p;
+        q.tiles_m = (m + BM - 1) / BM;
+        q.tiles_n = (rows + BN - 1) / BN;
+        const size_t lds = 2 * (size_t)(BM + BN) * kLdsRow;
+        const dim3 grid(q.tiles_m * q.tiles_n);
+        if (out_f32)
+            hipLaunchKernelGGL((f16w_prefill_kernel<BM, BN, 2, 2, true>), grid, dim3(256), lds, stream, q);
+        else
+            hipLaunchKernelGGL((f16w_prefill_kernel<BM, BN, 2, 2, false>), grid, dim3(256), lds, stream, q);
+        return hipGetLastError();
+    };
+    using I128 = std::integral_constant<int, 128>;
+    using I64 = std::integral_constant<int, 64>;
+    if (ntiles(128, 128) >= cus) return go(I128{}, I128{});
+    if (ntiles(64, 128) >= cus) return go(I64{}, I128{});
+    return go(I64{}, I64{});
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {

@@ -8,6 +8,7 @@
 namespace qw35 {
 
 // GGUF tensor type-ids handled by this library.
+constexpr uint32_t kTypeF16 = 1;
 constexpr uint32_t kTypeQ8_0 = 8;
 constexpr uint32_t kTypeQ4_K = 12;
 constexpr uint32_t kTypeQ6_K = 14;
@@ -59,9 +60,10 @@ hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* tok
 // activation staging); launch_gf4_gemv picks between the two.
 hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream);
 
-// Full or row-gathered fp32 dequantisation (row_ids == nullptr: all rows).
+// Full or row-gathered dequantisation (row_ids == nullptr: all rows), to fp32
+// or (f16_out) to fp16 round-to-nearest-even of the same value.
 hipError_t launch_dequant(uint32_t type_id, const void* w, int rows, int k, const uint32_t* row_ids,
-                          int n_out_rows, float* dst, hipStream_t stream);
+                          int n_out_rows, void* dst, bool f16_out, hipStream_t stream);
 
 // fp32 [rows][k] -> tensor bytes of type_id (GF4 packer / q8_0 / Q4_K encoders);
 // col_scale (nullable) multiplies column c first.
@@ -97,5 +99,12 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream);
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// F16-weight prefill (GGUF type 1, e.g. the fp16 prefill image of a q8_0 /
+// Q4_K / Q6_K projection): the same contract as the GF4 staged path, with
+// w fp16 [rows][k]; workspace (required) holds the staged tokens.
+size_t f16w_prefill_workspace_bytes(int m, int k);
+hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
+                               int m, int out_f32, void* workspace, hipStream_t stream);
 
 }  // namespace qw35

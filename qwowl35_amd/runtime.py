@@ -9,6 +9,8 @@ Names and argument meaning follow the reference runtime's encoders
 * ``matmul_prefill``      <- ``encodeTiledKMatmul`` / ``qw35_mul_mm_gf4_f32`` (:309-366)
 * ``output_argmax``       <- the greedy path of ``encodeOutputHead`` (Qw35MetalRuntime+Output.m:11-65)
 * ``dequantize``          <- the per-codec dequant helpers / ``qw35_get_rows_*`` gathers
+* ``prefill_image``       <- the half dequantisation of ``qw35_kernel_mul_mm``'s weight tiles
+  (qw35_tiled_mm.metal:199-255), made once: an F16 weight for ``matmul_prefill``
 * ``DecodePlan``          <- the per-token recording of ``evalToken`` (Qw35MetalRuntime.m:807-880)
 * ``quantize``            <- ``pack_ffn_gf4`` / ``pack_gf4_prepared`` (tools/qw35_cook_common.py:83-119,182-199)
 
@@ -24,13 +26,14 @@ from dataclasses import dataclass
 import torch
 
 from . import _ffi
-from ._ffi import Qw35Error, TYPE_GF4, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
+from ._ffi import Qw35Error, TYPE_F16, TYPE_GF4, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
 
 _ROW_BYTES = {
     TYPE_GF4: lambda k: (k + 7) // 8 * 4,
     TYPE_Q8_0: lambda k: (k + 31) // 32 * 34,
     TYPE_Q4_K: lambda k: (k + 255) // 256 * 144,
     TYPE_Q6_K: lambda k: (k + 255) // 256 * 210,
+    TYPE_F16: lambda k: 2 * k,
 }
 
 
@@ -59,6 +62,18 @@ class HipWeight:
     @property
     def k(self) -> int:
         return int(self.view.k)
+
+    @property
+    def prefill(self) -> "HipWeight":
+        """The weight ``matmul_prefill`` takes: itself for GF4 / F16, else its fp16
+        prefill image (``prefill_image``), made on first use and kept."""
+        if self.type_id in (TYPE_GF4, TYPE_F16):
+            return self
+        img = getattr(self, "_prefill", None)
+        if img is None:
+            img = prefill_image(self)
+            self._prefill = img
+        return img
 
     @classmethod
     def upload(cls, raw, type_id: int, rows: int, k: int, device="cuda") -> "HipWeight":
@@ -172,7 +187,8 @@ def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tenso
 def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = None,
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
                    workspace: torch.Tensor | None | bool = True, stream=None) -> torch.Tensor:
-    """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4 weight (``encodeTiledKMatmul``).
+    """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4 or F16 weight (``encodeTiledKMatmul``;
+    a q8_0 / Q4_K / Q6_K weight enters as its fp16 image, ``w.prefill``).
 
     ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
     ``out_dtype`` (bfloat16, rounded to nearest even, or float32).
@@ -205,17 +221,24 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
 def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Multi-token matvec of fp32 activations [n_tokens, k] (``encodeMatvecBatch``, +FFN.m:260-306).
 
-    1..8 tokens run the decode GEMV (fp32 activations); longer GF4 chunks run
-    the bf16-MFMA prefill matmul with fp32 output, as the reference switches
-    to its tiled matmul for multi-token chunks.
+    1..8 tokens run the decode GEMV (fp32 activations); longer chunks run the
+    prefill matmul with fp32 output (GF4 directly, q8_0 / Q4_K / Q6_K through
+    their fp16 prefill image), as the reference switches to its tiled matmul
+    for multi-token chunks.
     """
     if x.dim() != 2:
         raise Qw35Error("matvec_batch takes [n_tokens, k] activations")
-    if x.shape[0] <= _ffi.MAX_BATCH:
+    if x.shape[0] <= _ffi.MAX_BATCH and w.type_id != TYPE_F16:
         return decode_matvec(w, x, dst, residual=False, stream=stream)
-    if w.type_id != TYPE_GF4:
-        raise Qw35Error("matvec_batch: chunks of more than 8 tokens need a GF4 weight (prefill matmul)")
-    return matmul_prefill(w, x, out_dtype=torch.float32, dst=dst, stream=stream)
+    return matmul_prefill(w.prefill, x, out_dtype=torch.float32, dst=dst, stream=stream)
+
+
+def prefill_image(w: HipWeight, stream=None) -> HipWeight:
+    """fp16_rne of the dequantised weight as a new F16 ``HipWeight``
+    (``qw35_hip_dequantize_f16``), the operand of ``matmul_prefill``."""
+    dst = torch.empty(w.rows * w.k * 2, dtype=torch.uint8, device=w.storage.device)
+    _ffi.call("qw35_hip_dequantize_f16", C.byref(w.view), _ptr(dst), _stream(stream))
+    return HipWeight.from_device(dst, TYPE_F16, w.rows, w.k)
 
 
 def dequantize(w: HipWeight, row_ids: torch.Tensor | None = None, stream=None) -> torch.Tensor:
