@@ -395,7 +395,8 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight* w, void* dst, void* stream, c
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
     char msg[8];
     if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || n_tokens < 1 || n_tokens > 65536) return 0;
-    if (w->type_id == qw35::kTypeF16) return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->k);
+    if (w->type_id == qw35::kTypeF16)
+        return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
     if (w->type_id != qw35::kTypeGF4) return 0;
     return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
 }
@@ -432,7 +433,8 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         return 0;
     }
     if (w->type_id == qw35::kTypeF16) {
-        const uint64_t need = qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->k);
+        const uint64_t need =
+            qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, qw35::PrefillCfg{32, 2, 1});
         if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
             set_err(err, err_len, "matmul_prefill: f16 weights need a 256-byte aligned workspace of >= %llu bytes",
                     (unsigned long long)need);
@@ -440,7 +442,7 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         }
         return check_hip(qw35::launch_f16w_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
                                                    awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace,
-                                                   static_cast<hipStream_t>(stream)),
+                                                   workspace_bytes, static_cast<hipStream_t>(stream)),
                          "matmul_prefill", err, err_len)
                    ? 1
                    : 0;

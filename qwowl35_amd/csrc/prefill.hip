@@ -23,9 +23,9 @@
 // * Blocks are assigned XCD by XCD (consecutive block ids land on different
 //   XCDs), M-tile fastest, so the blocks that share a W tile share an L2.
 //
-// F16 weights (GGUF type 1) take a third kernel, f16w_prefill_kernel: the
-// staged fp16 tokens against fp16 weight tiles, both staged through LDS.  It
-// serves the q8_0 / Q4_K / Q6_K projections through their fp16 prefill image
+// F16 weights (GGUF type 1) take the staged kernel with fp16 weight loads in
+// place of the GF4 decode (gf4_prefill_f16_kernel<..., F16W>).  They serve the
+// q8_0 / Q4_K / Q6_K projections through their fp16 prefill image
 // (qw35_hip_dequantize_f16: fp16_rne of the exact dequantised weight), which
 // is the precision of the reference's tiled matmul: qw35_kernel_mul_mm
 // dequantises its weight tiles to half (qw35_tiled_mm.metal:199-255).
@@ -385,7 +385,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   column order, which the staging pass already wrote).
 // * Global loads run two steps ahead in two register stages; the token tile
 //   is double buffered in LDS, one barrier per step.
-template <int BM, int NW, int FN, int WPE, bool OUT_F32>
+// * F16W: the weights are an fp16 tensor [N][K] (the prefill image of a
+//   k-quant projection) instead of GF4 words.  A lane's 32 columns of a step
+//   are four 16-byte loads, each the MFMA operand of one sub-step as it is:
+//   no decode, and the token tile is staged in column order.
+template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
     constexpr int NT = 64 * NW;
@@ -430,23 +434,29 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         a_off[i] = ((uint32_t)gm * (uint32_t)K + (uint32_t)k_begin + (uint32_t)col * 8u) * 2u;
         a_lds[i] = row * kLdsRow + col * 16;
     }
-    const uint32_t* w_src[FN];
+    constexpr int WCH = F16W ? 4 : 1;  // 16-byte weight loads per lane per 32-row tile per step
+    const uint8_t* w_src[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-        w_src[j] = p.w + (size_t)min(n0 + 32 * j + l32, p.n - 1) * words_per_row + (k_begin >> 3) + 4 * half;
+    for (int j = 0; j < FN; ++j) {
+        const size_t row = (size_t)min(n0 + 32 * j + l32, p.n - 1);
+        w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(p.w) + (row * K + k_begin + 32 * half) * 2
+                        : reinterpret_cast<const uint8_t*>(p.w + row * words_per_row + (k_begin >> 3) + 4 * half);
+    }
     const uint8_t* a_base = static_cast<const uint8_t*>(p.a);
 
     typedef uint4_t Tokens[A_CHUNKS];
-    typedef uint4_t Words[FN];
+    typedef uint4_t Words[FN][WCH];
     auto load_tokens = [&](int kt, Tokens& a) {
         const uint32_t k0 = (uint32_t)kt * kBK;
 #pragma unroll
         for (int i = 0; i < A_CHUNKS; ++i) a[i] = *reinterpret_cast<const uint4_t*>(a_base + a_off[i] + k0 * 2);
     };
     auto load_words = [&](int kt, Words& w) {
-        const uint32_t k0 = (uint32_t)kt * kBK;
+        const size_t k0 = (size_t)kt * kBK;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) w[j] = load_stream16(w_src[j] + (k0 >> 3));
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int c = 0; c < WCH; ++c) w[j][c] = load_stream16(w_src[j] + (F16W ? k0 * 2 + 16 * c : k0 / 2));
     };
     auto store_tokens = [&](const Tokens& a, uint8_t* buf) {
 #pragma unroll
@@ -468,8 +478,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             half8_t wf[FN], af[FM];
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const uint32_t word = kk == 0 ? w[j].x : kk == 1 ? w[j].y : kk == 2 ? w[j].z : w[j].w;
-                wf[j] = gf4_word_to_b(word, gc);
+                if constexpr (F16W) {
+                    wf[j] = __builtin_bit_cast(half8_t, w[j][kk]);
+                } else {
+                    const uint32_t word = kk == 0 ? w[j][0].x : kk == 1 ? w[j][0].y : kk == 2 ? w[j][0].z : w[j][0].w;
+                    wf[j] = gf4_word_to_b(word, gc);
+                }
             }
 #pragma unroll
             for (int i = 0; i < FM; ++i)
@@ -561,157 +575,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     }
 }
 
-// F16-weight path: fp16 A'' (prefill_stage_kernel, column order) against an
-// fp16 weight tensor [N][K] on v_mfma_f32_16x16x32_f16.
-//
-// * The layout of the direct path: a BM x BN tile per block, WGM x WGN waves,
-//   both operand tiles staged through LDS per 64-wide k step (double buffered,
-//   16-byte row padding), global loads two steps ahead in two register stages,
-//   one barrier per step; no conversion is left to do in the loader.
-// * The W tile is the MFMA's first operand: lane l accumulates
-//   D[n = 4 (l / 16) + r][m = l % 16], four consecutive outputs of one token
-//   row, scaled by the token's row_scale on the way out.
-template <int BM, int BN, int WGM, int WGN, bool OUT_F32>
-__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2))) void f16w_prefill_kernel(
-    PrefillArgs p) {
-    constexpr int NT = 64 * WGM * WGN;
-    constexpr int WTM = BM / WGM;
-    constexpr int WTN = BN / WGN;
-    constexpr int FM = WTM / 16;
-    constexpr int FN = WTN / 16;
-    constexpr int AC = BM * 8 / NT;  // 16-byte token chunks per thread per step
-    constexpr int WC = BN * 8 / NT;  // 16-byte weight chunks per thread per step
-    constexpr int BUF = (BM + BN) * kLdsRow;
-    static_assert(AC >= 1 && WC >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tiles must split over the threads");
-    static_assert(FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "wave tile shape");
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WGN;
-    const int wn = wave % WGN;
-    const int tiles = p.tiles_m * p.tiles_n;
-    int t = blockIdx.x;
-    if (tiles % kXcds == 0) t = (t % kXcds) * (tiles / kXcds) + t / kXcds;
-    const int m0 = (t % p.tiles_m) * BM;
-    const int n0 = (t / p.tiles_m) * BN;
-    const int K = p.k;
-    const uint16_t* a16 = static_cast<const uint16_t*>(p.a);
-    const uint16_t* w16 = reinterpret_cast<const uint16_t*>(p.w);
-
-    const uint16_t* a_src[AC];
-    const uint16_t* w_src[WC];
-    int a_lds[AC], w_lds[WC];
-#pragma unroll
-    for (int i = 0; i < AC; ++i) {
-        const int c = tid + i * NT;
-        a_src[i] = a16 + (size_t)min(m0 + (c >> 3), p.m - 1) * K + (c & 7) * 8;
-        a_lds[i] = (c >> 3) * kLdsRow + (c & 7) * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < WC; ++i) {
-        const int c = tid + i * NT;
-        w_src[i] = w16 + (size_t)min(n0 + (c >> 3), p.n - 1) * K + (c & 7) * 8;
-        w_lds[i] = (BM + (c >> 3)) * kLdsRow + (c & 7) * 16;
-    }
-    struct Regs {
-        uint4_t a[AC];
-        uint4_t w[WC];
-    };
-    auto load_step = [&](int kt, Regs& r) {
-        const int k0 = kt * kBK;
-#pragma unroll
-        for (int i = 0; i < AC; ++i) r.a[i] = *reinterpret_cast<const uint4_t*>(a_src[i] + k0);
-#pragma unroll
-        for (int i = 0; i < WC; ++i) r.w[i] = load_stream16(w_src[i] + k0);
-    };
-    auto store_step = [&](const Regs& r, uint8_t* buf) {
-#pragma unroll
-        for (int i = 0; i < AC; ++i) *reinterpret_cast<uint4_t*>(buf + a_lds[i]) = r.a[i];
-#pragma unroll
-        for (int i = 0; i < WC; ++i) *reinterpret_cast<uint4_t*>(buf + w_lds[i]) = r.w[i];
-    };
-
-    float4_t acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int a_rd = (wm * WTM + (lane & 15)) * kLdsRow + (lane >> 4) * 16;
-    const int b_rd = (BM + wn * WTN + (lane & 15)) * kLdsRow + (lane >> 4) * 16;
-    auto compute = [&](const uint8_t* cur) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            half8_t af[FM], wf[FN];
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                wf[j] = *reinterpret_cast<const half8_t*>(cur + b_rd + j * 16 * kLdsRow + ks * 64);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                af[i] = *reinterpret_cast<const half8_t*>(cur + a_rd + i * 16 * kLdsRow + ks * 64);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], af[i], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    const int KT = K / kBK;
-    uint8_t* buf0 = smem;
-    uint8_t* buf1 = smem + BUF;
-    Regs r0, r1;
-    load_step(0, r0);
-    if (KT > 1) load_step(1, r1);
-    store_step(r0, buf0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; kt += 2) {
-        if (kt + 2 < KT) load_step(kt + 2, r0);
-        compute(buf0);
-        if (kt + 1 < KT) store_step(r1, buf1);
-        __syncthreads();
-        if (kt + 1 >= KT) break;
-        if (kt + 3 < KT) load_step(kt + 3, r1);
-        compute(buf1);
-        if (kt + 2 < KT) store_step(r0, buf0);
-        __syncthreads();
-    }
-
-    const bool vec_ok = (p.n & 3) == 0 && ((uintptr_t)p.c & 15) == 0;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int gm = m0 + wm * WTM + i * 16 + (lane & 15);
-        if (gm >= p.m) continue;
-        const float rs = p.row_scale[gm];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int gn = n0 + wn * WTN + j * 16 + (lane >> 4) * 4;
-            const size_t o = (size_t)gm * p.n + gn;
-            const float4_t d = acc[i][j] * rs;
-            if (vec_ok && gn + 3 < p.n) {
-                if constexpr (OUT_F32) {
-                    *reinterpret_cast<float4_t*>(static_cast<float*>(p.c) + o) = d;
-                } else {
-                    typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
-                    *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(p.c) + o) =
-                        uint2_t{pack_bf16(d.x, d.y), pack_bf16(d.z, d.w)};
-                }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (gn + r < p.n) {
-                        if constexpr (OUT_F32)
-                            static_cast<float*>(p.c)[o + r] = d[r];
-                        else
-                            static_cast<uint16_t*>(p.c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
-                    }
-                }
-            }
-        }
-    }
-}
-
 // C[m][n] = row_scale[m] * sum_s partial[s][m][n], splits summed in order.
 // One thread per 4 consecutive outputs of a row.
 constexpr int kReduceThreads = 256;
@@ -764,7 +627,7 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     }
 }
 
-template <int BM, int NW, int FN, int WPE>
+template <int BM, int NW, int FN, int WPE, bool F16W = false>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     constexpr int BN = 32 * FN * NW;
     const size_t lds = 2 * (size_t)BM * kLdsRow;
@@ -773,9 +636,9 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (out_f32)
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W>), grid, dim3(64 * NW), lds, s, p);
     else
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W>), grid, dim3(64 * NW), lds, s, p);
     return hipGetLastError();
 }
 
@@ -860,15 +723,19 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // slab once); a K split adds 0.5 us per MB of fp32 partial sums (written,
 // read back by the reduction, one more launch).  Over the measured shapes the
 // pick is the fastest or within 5% of it.
-PrefillCfg plan_gf4_prefill(int m, int rows, int k) {
+// F16 weights (2 bytes per weight against GF4's half byte) use FN = 2 only:
+// their four-slot register ring of 16-byte loads is four times GF4's.
+PrefillCfg plan_prefill(int m, int rows, int k, bool f16w) {
     constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9, kUsPerPartialMB = 0.5;
     const int cus = num_cus();
     const int chunks = k / 256;
+    const double w_bytes = f16w ? 2.0 : 0.5;
     static constexpr int kShapes[][2] = {{128, 4}, {128, 2}, {64, 4}, {64, 2}, {32, 2}};
     PrefillCfg best{32, 2, 1};
     double best_us = 0;
     for (const auto& sh : kShapes) {
         const int bm = sh[0], fn = sh[1], bn = 128 * fn;
+        if (f16w && fn != 2) continue;
         if (bm > 32 && m <= bm / 2) continue;  // half the token tile or more would be padding
         const long tiles = (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn);
         for (int sp = 1; sp <= 16 && sp <= chunks; ++sp) {
@@ -876,7 +743,7 @@ PrefillCfg plan_gf4_prefill(int m, int rows, int k) {
             const long blocks = tiles * sp;
             const double rounds = (double)((blocks + cus - 1) / cus);
             const double k_len = (double)k / sp;
-            double us = rounds * (kUsPerMflop * 2.0 * bm * bn * k_len * 1e-6 + kUsPerMB * k_len * (2.0 * bm + 0.5 * bn) * 1e-6);
+            double us = rounds * (kUsPerMflop * 2.0 * bm * bn * k_len * 1e-6 + kUsPerMB * k_len * (2.0 * bm + w_bytes * bn) * 1e-6);
             if (sp > 1) us += kUsPerPartialMB * 4.0 * sp * m * rows * 1e-6;
             if (best_us == 0 || us < best_us) {
                 best_us = us;
@@ -887,6 +754,8 @@ PrefillCfg plan_gf4_prefill(int m, int rows, int k) {
     }
     return best;
 }
+
+PrefillCfg plan_gf4_prefill(int m, int rows, int k) { return plan_prefill(m, rows, k, false); }
 
 size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg) {
     size_t b = round256((size_t)m * k * 2) + round256((size_t)m * 4);
@@ -900,7 +769,7 @@ size_t gf4_prefill_workspace_bytes(int m, int rows, int k) {
 
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, bool f16w) {
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
     p.a = a;
@@ -919,12 +788,21 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
         float* rs = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2));
         float* partial = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2) + round256((size_t)m * 4));
-#define QW35_STAGE(AF, AW) \
-    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, a16, rs)
-        if (af) {
-            if (aw) QW35_STAGE(true, true); else QW35_STAGE(true, false);
+#define QW35_STAGE(AF, AW, ORD)                                                                          \
+    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, ORD>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, \
+                       a16, rs)
+        if (f16w) {
+            if (af) {
+                if (aw) QW35_STAGE(true, true, false); else QW35_STAGE(true, false, false);
+            } else {
+                if (aw) QW35_STAGE(false, true, false); else QW35_STAGE(false, false, false);
+            }
         } else {
-            if (aw) QW35_STAGE(false, true); else QW35_STAGE(false, false);
+            if (af) {
+                if (aw) QW35_STAGE(true, true, true); else QW35_STAGE(true, false, true);
+            } else {
+                if (aw) QW35_STAGE(false, true, true); else QW35_STAGE(false, false, true);
+            }
         }
 #undef QW35_STAGE
         hipError_t e = hipGetLastError();
@@ -937,7 +815,14 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const bool split = cfg.splits > 1;
         if (split) p.c = partial;
         const bool kf32 = of || split;
-        switch (cfg.bm * 10 + cfg.fn) {
+        if (f16w) {
+            switch (cfg.bm * 10 + cfg.fn) {
+                case 1282: e = launch_f16_tile<128, 4, 2, 1, true>(p, kf32, stream); break;
+                case 642: e = launch_f16_tile<64, 4, 2, 2, true>(p, kf32, stream); break;
+                case 322: e = launch_f16_tile<32, 4, 2, 2, true>(p, kf32, stream); break;
+                default: return hipErrorInvalidValue;
+            }
+        } else switch (cfg.bm * 10 + cfg.fn) {
             case 1282: e = launch_f16_tile<128, 4, 2, 2>(p, kf32, stream); break;
             case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
             case 642: e = launch_f16_tile<64, 4, 2, 2>(p, kf32, stream); break;
@@ -964,56 +849,19 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     return launch_tile<64, 64, 2, 2>(p, af, aw, of, stream);
 }
 
-size_t f16w_prefill_workspace_bytes(int m, int k) { return round256((size_t)m * k * 2) + round256((size_t)m * 4); }
+size_t f16w_prefill_workspace_bytes(int m, int rows, int k) {
+    return gf4_prefill_workspace_bytes(m, rows, k, plan_prefill(m, rows, k, true));
+}
 
 hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                               int m, int out_f32, void* workspace, hipStream_t stream) {
+                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (!workspace) return hipErrorInvalidValue;
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
-    float* rs = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2));
-    const bool af = a_f32 != 0, aw = awq != nullptr;
-#define QW35_STAGE(AF, AW) \
-    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, false>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, a16, rs)
-    if (af) {
-        if (aw) QW35_STAGE(true, true); else QW35_STAGE(true, false);
-    } else {
-        if (aw) QW35_STAGE(false, true); else QW35_STAGE(false, false);
+    PrefillCfg cfg = plan_prefill(m, rows, k, true);
+    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
+        do --cfg.splits;
+        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
     }
-#undef QW35_STAGE
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    PrefillArgs p{};
-    p.w = static_cast<const uint32_t*>(w);
-    p.a = a16;
-    p.c = c;
-    p.row_scale = rs;
-    p.m = m;
-    p.n = rows;
-    p.k = k;
-    p.splits = 1;
-    p.k_len = k;
-    // Largest tile that still gives every CU a block.
-    const long cus = num_cus();
-    auto ntiles = [&](int bm, int bn) { return (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn); };
-    auto go = [&](auto bm_c, auto bn_c) {
-        constexpr int BM = decltype(bm_c)::value, BN = decltype(bn_c)::value;
-        PrefillArgs q = p;
-        q.tiles_m = (m + BM - 1) / BM;
-        q.tiles_n = (rows + BN - 1) / BN;
-        const size_t lds = 2 * (size_t)(BM + BN) * kLdsRow;
-        const dim3 grid(q.tiles_m * q.tiles_n);
-        if (out_f32)
-            hipLaunchKernelGGL((f16w_prefill_kernel<BM, BN, 2, 2, true>), grid, dim3(256), lds, stream, q);
-        else
-            hipLaunchKernelGGL((f16w_prefill_kernel<BM, BN, 2, 2, false>), grid, dim3(256), lds, stream, q);
-        return hipGetLastError();
-    };
-    using I128 = std::integral_constant<int, 128>;
-    using I64 = std::integral_constant<int, 64>;
-    if (ntiles(128, 128) >= cus) return go(I128{}, I128{});
-    if (ntiles(64, 128) >= cus) return go(I64{}, I128{});
-    return go(I64{}, I64{});
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, true);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {
@@ -1030,7 +878,7 @@ hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int
         do --cfg.splits;
         while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
     }
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream);
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, false);
 }
 
 }  // namespace qw35

@@ -96,15 +96,17 @@ PrefillCfg plan_gf4_prefill(int m, int rows, int k);
 size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg);
 size_t gf4_prefill_workspace_bytes(int m, int rows, int k);
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
-                                  void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream);
+                                  void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
+                                  bool f16w = false);
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // F16-weight prefill (GGUF type 1, e.g. the fp16 prefill image of a q8_0 /
-// Q4_K / Q6_K projection): the same contract as the GF4 staged path, with
-// w fp16 [rows][k]; workspace (required) holds the staged tokens.
-size_t f16w_prefill_workspace_bytes(int m, int k);
+// Q4_K / Q6_K projection): the staged GF4 path with w fp16 [rows][k]; the
+// workspace is required (at least the staged tokens and scales; its full
+// size, f16w_prefill_workspace_bytes, also holds the K-split partials).
+size_t f16w_prefill_workspace_bytes(int m, int rows, int k);
 hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                               int m, int out_f32, void* workspace, hipStream_t stream);
+                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace qw35
