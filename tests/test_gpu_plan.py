@@ -122,7 +122,7 @@ def test_plan_reads_inputs_updated_in_place(cuda):
     plan.close()
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k"])
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("nb", [1, 5])
 def test_plan_merges_projections_sharing_inputs(cuda, name, nb):
     """Consecutive k-quant matvecs over one input (a mixer's q/k/v or
@@ -132,7 +132,7 @@ def test_plan_merges_projections_sharing_inputs(cuda, name, nb):
 
     rt = _rt()
     t = TYPES[name]
-    k = 512
+    k = 2048 if name == "q6_k" else 512  # Q6_K rows are 16-byte aligned for k % 2048 == 0
     rng = np.random.default_rng(40 + nb)
     rows = [160, 32, 48, 7, 96]
     ws = [rt.HipWeight.upload(make_weight(t, r, k, seed=100 + i)[0], t, r, k, device=cuda)
