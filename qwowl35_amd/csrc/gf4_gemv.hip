@@ -198,7 +198,7 @@ __global__ __launch_bounds__(64 * KS) void gf4_mfma_gemv(GemvArgs args) {
             }
         }
         const float sc = fp16_range_scale(wave_max_abs(mx));
-        inv_scale[b] = 1.0f / sc;
+        inv_scale[b] = pow2_inverse(sc);
 #pragma unroll
         for (int j = 0; j < GPL; ++j) {
             const int g = lane + 64 * j;

@@ -13,19 +13,21 @@
 // coalesced 16-byte segments, pass through a per-wave LDS transpose, and each
 // lane then reads the bytes of its MFMA operand.  v_mfma_f32_16x16x32_f16:
 //   * B (weights): lane l holds 8 consecutive k of weight row n = l % 16 of one
-//     32-element block, as exact fp16 integers (q8_0: int8; Q4_K: 4-bit q);
+//     32-element block, as exact fp16 integers (q8_0: int8 q; Q4_K: sc_j * q);
 //   * A (activations): row 2b = fp16 hi, row 2b+1 = fp16 lo of awq*x of batch
 //     row b, scaled per chunk by a power of two (max |v| in [2^13, 2^14));
-//   * one MFMA per 32-element block with a zero accumulator gives the 16x16
-//     block partial; the block's scales are applied to it in fp32:
-//       q8_0 (qw35_types.metal:24-36):  y += d * sum q x
-//       Q4_K (qw35_matvec.metal:2-38):   y += d*sc_j * sum q x - dmin*m_j * sum x
-//     with the chunk's inverse activation scale folded into the same multiply.
+//   * q8_0 (qw35_types.metal:24-36): one MFMA per 32-element block with a zero
+//     accumulator gives the block partial, scaled in fp32: y += d * sum q x;
+//   * Q4_K (qw35_matvec.metal:2-38): the 6-bit sub-block scale rides in the
+//     fp16 operand, so the super-block's eight MFMAs accumulate in one register
+//     set and y += d * sum_j sc_j sum q x - dmin * sum_j m_j sum x;
+//     the chunk's inverse activation scale is folded into the last multiply.
 //
 // Byte -> fp16 integer decode (exact, integers below 2048):
 //   int8 q:   perm into 0x64XX halves after flipping the sign bit -> 1152 + q,
 //             then one v_pk_add_f16 of -1152;
-//   nibble q: mask (and shift) -> 0x64XX halves -> 1024 + q, v_pk_add_f16 of -1024.
+//   nibble q: mask (and shift) -> 0x64XX halves -> 1024 + q, then v_pk_add_f16
+//             of -1024, or (Q4_K) v_pk_fma_f16 (1024 + q) * sc - 1024 sc = sc q.
 // GF4 words carry their scale inside the exact fp16 operand (gf4_decode.h), so a
 // chunk's eight MFMAs accumulate in one register set; lane group kq takes words
 // 8kq..8kq+7 of a row (two 16-byte LDS reads) and the activation operand
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     const int k = args.k;
     const int n_batch = args.n_batch;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15;
     const int kq = lane >> 4;
     // Segment of this workgroup (uniform): its matrix, output and row count.
@@ -225,34 +227,43 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     float4_t av[P];
     uint4_t wv[P][RT * NM][LPT];
 
+    // Byte offset of each lane's 16-byte segments from the tile's first row
+    // (rows past the matrix re-read its last row); the per-chunk base is uniform.
+    uint32_t loff[RT][LPT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            int s = lane + 64 * i;
+            s = s < 16 * F::kSegs ? s : 0;
+            int r = 16 * t + s / F::kSegs;
+            r = r < rows - row0 ? r : rows - 1 - row0;
+            loff[t][i] = (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)(s % F::kSegs);
+        }
+
     auto issue = [&](auto CI) {
         constexpr int c = decltype(CI)::value;
         constexpr int sl = c % P;
         int chunk = wave * CPW + c;
         chunk = chunk < chunks ? chunk : 0;
-        const int col = chunk * 256 + 4 * lane;
+        const float* xc = args.x + (size_t)chunk * 256;
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int bb = b < n_batch ? b : 0;
-            xv[sl][b] = *reinterpret_cast<const float4_t*>(args.x + (size_t)bb * k + col);
+            xv[sl][b] = *reinterpret_cast<const float4_t*>(xc + (size_t)bb * k + 4 * lane);
         }
-        if (HAS_AWQ) av[sl] = *reinterpret_cast<const float4_t*>(args.awq + col);
+        if (HAS_AWQ) av[sl] = *reinterpret_cast<const float4_t*>(args.awq + (size_t)chunk * 256 + 4 * lane);
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
+        for (int m = 0; m < NM; ++m) {
+            const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? wmat : args.w_up) +
+                                   (size_t)row0 * row_bytes + chunk_seg_base<FMT>(chunk);
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? wmat : args.w_up);
+            for (int t = 0; t < RT; ++t)
 #pragma unroll
-                for (int i = 0; i < LPT; ++i) {
-                    int s = lane + 64 * i;
-                    s = s < 16 * F::kSegs ? s : 0;
-                    int r = row0 + 16 * t + s / F::kSegs;
-                    r = r < rows ? r : rows - 1;
-                    wv[sl][t * NM + m][i] = load_stream16(
-                        wbase + (size_t)r * row_bytes + chunk_seg_base<FMT>(chunk) + 16 * (s % F::kSegs));
-                }
-            }
+                for (int i = 0; i < LPT; ++i) wv[sl][t * NM + m][i] = load_stream16(wbase + loff[t][i]);
         }
+        // loads complete in issue order: keep chunk c's ahead of chunk c + 1's
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     kq_static_for<P>([&](auto CI) { issue(CI); });
@@ -282,7 +293,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                 if (HAS_AWQ) v *= av[sl];
                 const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
                 const float sc = fp16_range_scale(wave_max_abs(mx));
-                isc[b] = 1.0f / sc;
+                isc[b] = pow2_inverse(sc);
                 v *= sc;
                 float e[4] = {v[0], v[1], v[2], v[3]};
                 if constexpr (FMT == kFmtGF4) {
@@ -434,6 +445,20 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                         const float4_t sxd = *reinterpret_cast<const float4_t*>(sx + b1 * 8 + 4);
                         const float sx0[8] = {sxa[0], sxa[1], sxa[2], sxa[3], sxb[0], sxb[1], sxb[2], sxb[3]};
                         const float sx1[8] = {sxc[0], sxc[1], sxc[2], sxc[3], sxd[0], sxd[1], sxd[2], sxd[3]};
+                        // Sub-block scales as exact fp16 pairs (sc_2i, sc_2i+1) and their
+                        // -1024 multiples (|sc| < 64, so -1024 sc is exact).
+                        half2_t scp[4], nbp[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint32_t w = i < 2 ? sc_lo : sc_hi;
+                            scp[i] = as_half2(__builtin_amdgcn_perm(0x64646464u, w, (i & 1) ? 0x04030402u : 0x04010400u)) +
+                                     h2(-1024.0f, -1024.0f);
+                            nbp[i] = scp[i] * h2(-1024.0f, -1024.0f);
+                        }
+                        // B = sc_j * q as one fused multiply-add of the biased 1024 + q:
+                        // (1024 + q) sc - 1024 sc = sc q <= 945, exact; the eight MFMAs then
+                        // accumulate sum_j sc_j sum q x in one register set.
+                        float4_t dd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int cc = 0; cc < 4; ++cc) {
                             const uint2_t_ qd = *reinterpret_cast<const uint2_t_*>(wrow + 16 + 32 * cc + 8 * kq);
@@ -442,24 +467,37 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                                 const int j = 2 * cc + hi;
                                 const uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
                                 const uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
+                                const half2_t sp = scp[j >> 1], np = nbp[j >> 1];
+                                const half2_t s2 = (j & 1) ? half2_t{sp.y, sp.y} : half2_t{sp.x, sp.x};
+                                const half2_t n2 = (j & 1) ? half2_t{np.y, np.y} : half2_t{np.x, np.x};
                                 uint32_t b4[4];
-                                u4x4_to_h(t0, bias, b4[0], b4[1]);
-                                u4x4_to_h(t1, bias, b4[2], b4[3]);
+                                b4[0] = as_u32(__builtin_elementwise_fma(
+                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04010400u)), s2, n2));
+                                b4[1] = as_u32(__builtin_elementwise_fma(
+                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04030402u)), s2, n2));
+                                b4[2] = as_u32(__builtin_elementwise_fma(
+                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04010400u)), s2, n2));
+                                b4[3] = as_u32(__builtin_elementwise_fma(
+                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04030402u)), s2, n2));
                                 const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
                                 const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
-                                const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                    aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                                const uint32_t scw = j < 4 ? sc_lo : sc_hi;
-                                const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
-                                const float scj = (float)((scw >> (8 * (j & 3))) & 0xFFu);
-                                const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
-                                const float ds = d * scj;
-                                const float dm = dmin * mnj;
-                                const float v0 = __builtin_fmaf(-dm, sx0[j], ds * (dd[0] + dd[1]));
-                                const float v1 = __builtin_fmaf(-dm, sx1[j], ds * (dd[2] + dd[3]));
-                                acc[t][m][0] = __builtin_fmaf(inv_sc[0], v0, acc[t][m][0]);
-                                acc[t][m][1] = __builtin_fmaf(inv_sc[1], v1, acc[t][m][1]);
+                                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, dd, 0, 0, 0);
                             }
+                        }
+                        // y += d sum_j sc_j sum q x - dmin sum_j m_j sum x
+                        float ms0 = 0.0f, ms1 = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
+                            const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
+                            ms0 = __builtin_fmaf(mnj, sx0[j], ms0);
+                            if constexpr (NB > 1) ms1 = __builtin_fmaf(mnj, sx1[j], ms1);
+                        }
+                        const float v0 = __builtin_fmaf(-dmin, ms0, d * (dd[0] + dd[1]));
+                        acc[t][m][0] = __builtin_fmaf(inv_sc[0], v0, acc[t][m][0]);
+                        if constexpr (NB > 1) {
+                            const float v1 = __builtin_fmaf(-dmin, ms1, d * (dd[2] + dd[3]));
+                            acc[t][m][1] = __builtin_fmaf(inv_sc[1], v1, acc[t][m][1]);
                         }
                     }
                     // The next tile (or chunk) rewrites the transpose and activation buffers.

@@ -144,7 +144,7 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float sc = 2.0f * fp16_range_scale(mx);  // max in [2^14, 2^15)
-    if (threadIdx.x == 0) row_scale[row] = 1.0f / sc;
+    if (threadIdx.x == 0) row_scale[row] = pow2_inverse(sc);
 #pragma unroll
     for (int j = 0; j < kMaxGroups; ++j) {
         const int g = threadIdx.x + j * kStageThreads;

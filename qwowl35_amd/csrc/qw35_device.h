@@ -45,15 +45,25 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v, uint32_t moved) { return v > moved ? v : moved; }
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// max |v| over the 64 lanes, broadcast.  |v| is compared as its bit pattern
+// (ordered like the value for non-NaN; a NaN lane makes the result NaN), with
+// 0 as the identity so each step is one DPP-modified v_max_u32.
 __device__ __forceinline__ float wave_max_abs(float v) {
-    v = fabsf(v);
-    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
-    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
-    v = fmaxf(v, dpp_f32<kDppRowHalfMirror>(v));
-    v = fmaxf(v, dpp_f32<kDppRowMirror>(v));
-    v = fmaxf(v, dpp_f32<kDppRowBcast15, 0xA>(v));
-    v = fmaxf(v, dpp_f32<kDppRowBcast31, 0xC>(v));
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    uint32_t u = __builtin_bit_cast(uint32_t, v) & 0x7FFFFFFFu;
+    u = dpp_max_u32(u, dpp_u32<kDppQuadXor1>(u));
+    u = dpp_max_u32(u, dpp_u32<kDppQuadXor2>(u));
+    u = dpp_max_u32(u, dpp_u32<kDppRowHalfMirror>(u));
+    u = dpp_max_u32(u, dpp_u32<kDppRowMirror>(u));
+    u = dpp_max_u32(u, dpp_u32<kDppRowBcast15, 0xA>(u));
+    u = dpp_max_u32(u, dpp_u32<kDppRowBcast31, 0xC>(u));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)u, 63));
 }
 
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
@@ -88,6 +98,12 @@ __device__ __forceinline__ float fp16_range_scale(float max_abs) {
     if (shift > 24) shift = 24;
     if (shift < -24) shift = -24;
     return ldexpf(1.0f, shift);
+}
+
+// 1 / s for s = 2^e, |e| <= 24 (what fp16_range_scale returns): the exponent
+// field is mirrored about 127, so the result is exact.
+__device__ __forceinline__ float pow2_inverse(float s) {
+    return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, s));
 }
 
 }  // namespace qw35
