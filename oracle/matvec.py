@@ -19,11 +19,12 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import gf4, q4_k, q6_k, q8_0
+from . import gf4, q4_k, q5_k, q6_k, q8_0
 
 TYPE_GF4 = gf4.GF4_TYPE_ID
 TYPE_Q8_0 = q8_0.Q8_0_TYPE_ID
 TYPE_Q4_K = q4_k.Q4_K_TYPE_ID
+TYPE_Q5_K = q5_k.Q5_K_TYPE_ID
 TYPE_Q6_K = q6_k.Q6_K_TYPE_ID
 TYPE_F16 = 1
 
@@ -36,6 +37,8 @@ def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
         return q8_0.q8_0_nbytes(rows, k)
     if type_id == TYPE_Q4_K:
         return q4_k.q4_k_nbytes(rows, k)
+    if type_id == TYPE_Q5_K:
+        return q5_k.q5_k_nbytes(rows, k)
     if type_id == TYPE_Q6_K:
         assert k % q6_k.Q6_K_BLOCK_ELEMS == 0
         return rows * (k // q6_k.Q6_K_BLOCK_ELEMS) * q6_k.Q6_K_BLOCK_BYTES
@@ -52,6 +55,8 @@ def quantize(type_id: int, w: np.ndarray) -> np.ndarray:
         return q8_0.q8_0_quantize(w)
     if type_id == TYPE_Q4_K:
         return q4_k.q4_k_quantize(w)
+    if type_id == TYPE_Q5_K:
+        return q5_k.q5_k_quantize(w)
     if type_id == TYPE_Q6_K:
         return q6_k.q6_k_quantize(w).reshape(w.shape[0], -1)
     if type_id == TYPE_F16:
@@ -68,6 +73,8 @@ def dequant(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
         return q8_0.q8_0_dequant(raw)
     if type_id == TYPE_Q4_K:
         return q4_k.q4_k_dequant(raw)
+    if type_id == TYPE_Q5_K:
+        return q5_k.q5_k_dequant(raw)
     if type_id == TYPE_Q6_K:
         return q6_k.q6_k_dequant(raw, rows, raw.size // rows // q6_k.Q6_K_BLOCK_BYTES * q6_k.Q6_K_BLOCK_ELEMS)
     if type_id == TYPE_F16:

@@ -21,7 +21,8 @@ void set_err(char* err, uintptr_t err_len, const char* fmt, ...) {
 }
 
 bool type_supported(uint32_t t) {
-    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K || t == qw35::kTypeQ6_K ||
+    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K || t == qw35::kTypeQ5_K ||
+           t == qw35::kTypeQ6_K ||
            t == qw35::kTypeF16;
 }
 
@@ -30,6 +31,7 @@ uint64_t row_bytes(uint32_t t, uint64_t k) {
         case qw35::kTypeGF4: return (k + 7) / 8 * 4;
         case qw35::kTypeQ8_0: return (k + 31) / 32 * 34;
         case qw35::kTypeQ4_K: return (k + 255) / 256 * 144;
+        case qw35::kTypeQ5_K: return (k + 255) / 256 * 176;
         case qw35::kTypeQ6_K: return (k + 255) / 256 * 210;
         case qw35::kTypeF16: return k * 2;
         default: return 0;
@@ -41,6 +43,7 @@ const char* type_name(uint32_t t) {
         case qw35::kTypeGF4: return "gf4";
         case qw35::kTypeQ8_0: return "q8_0";
         case qw35::kTypeQ4_K: return "q4_k";
+        case qw35::kTypeQ5_K: return "q5_k";
         case qw35::kTypeQ6_K: return "q6_k";
         case qw35::kTypeF16: return "f16";
         default: return "unsupported";
@@ -101,6 +104,7 @@ hipError_t dispatch_gemv(uint32_t type_id, const qw35::GemvArgs& a, hipStream_t 
     switch (type_id) {
         case qw35::kTypeGF4: return qw35::launch_gf4_gemv(a, s);
         case qw35::kTypeQ8_0: return qw35::launch_q8_0_gemv(a, s);
+        case qw35::kTypeQ5_K: return qw35::launch_q5_k_gemv(a, s);
         case qw35::kTypeQ6_K: return qw35::launch_q6_k_gemv(a, s);
         default: return qw35::launch_q4_k_gemv(a, s);
     }
@@ -308,7 +312,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
             const bool sw = o.kind == QW35_HIP_OP_SWIGLU;
             qw35::GemvArgs a = gemv_args(o.w, sw ? o.w_up : nullptr, o.x, o.awq, o.dst, o.n_batch,
                                          sw ? 0 : o.residual);
-            // Consecutive q8_0 / Q4_K matvecs over the same activations share one launch.
+            // Consecutive k-quant matvecs over the same activations share one launch.
             uint32_t j = i + 1;
             if (!sw && o.w->type_id != qw35::kTypeGF4) {
                 while (j < n_ops && j - i < (uint32_t)qw35::kMaxSegments) {

@@ -1,4 +1,4 @@
-// fp32 (or fp16) dequantisation of GF4 / q8_0 / Q4_K / Q6_K / F16 tensors,
+// fp32 (or fp16) dequantisation of GF4 / q8_0 / Q4_K / Q5_K / Q6_K / F16 tensors,
 // optionally gathering rows.
 //
 // This is the library's bit-exact statement of each format (every weight of
@@ -9,6 +9,7 @@
 //   GF4  (tools/qw35_cook_common.py:79):  w = (4 - (c ^ 4)) * 0.25 * s, s = fp16(b << 8)
 //   q8_0 (qw35_types.metal:24-36):        w = fp32(d) * qs[i]
 //   Q4_K (qw35_matvec.metal:2-12):        w = d * sc_j * q - dmin * m_j
+//   Q5_K (qw35_matvec.metal:40-62):       the same with q = nibble | (bit j of qh[e % 32]) << 4
 //   Q6_K (qw35_matvec.metal:458-542):     w = (d * sc[e/16]) * (q - 32), q = ql nibble | qh 2 bits << 4
 //                                         (exact; the reference tile form qw35_dequantize_q6_k,
 //                                         :65-98, agrees in value)
@@ -77,10 +78,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const ui
             const uint32_t hi = (blk[128 + 32 * h + l] >> (2 * gg)) & 3u;
             v[i] = dsc * (float)((int)(lo | (hi << 4)) - 32);
         }
-    } else {  // Q4_K
-        const uint8_t* row = w + src_row * (size_t)(k >> 8) * 144;
+    } else {  // Q4_K, Q5_K
+        const bool q5 = type_id == kTypeQ5_K;
+        const size_t bb = q5 ? 176 : 144;
+        const uint8_t* row = w + src_row * (size_t)(k >> 8) * bb;
         const int col = 8 * g;
-        const uint8_t* blk = row + (size_t)(col >> 8) * 144;
+        const uint8_t* blk = row + (size_t)(col >> 8) * bb;
         const int e = col & 255;
         const int j = e >> 5;
         const uint8_t* sc = blk + 4;
@@ -96,10 +99,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const ui
         const float dmin = f16_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
         const float dsc = d * (float)s6;
         const float mm = dmin * (float)m6;
-        const uint8_t* qs = blk + 16 + (j >> 1) * 32 + (e & 31);
+        const uint8_t* qs = blk + (q5 ? 48 : 16) + (j >> 1) * 32 + (e & 31);
+        const uint8_t* qh = blk + 16 + (e & 31);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 0x0F);
+            uint32_t q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 0x0F);
+            if (q5) q |= ((qh[i] >> j) & 1u) << 4;
             v[i] = dsc * (float)q - mm;
         }
     }

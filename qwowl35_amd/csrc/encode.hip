@@ -1,4 +1,4 @@
-// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K / Q6_K / F16 tensor bytes, on the GPU.
+// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K / Q5_K / Q6_K / F16 tensor bytes, on the GPU.
 //
 // GF4 is the reference packer pack_gf4_prepared(rows, scale_search=False)
 // (tools/qw35_cook_common.py:83-119), including the optional AWQ column
@@ -10,7 +10,7 @@
 //   s     = fp16(b << 8)                                (:54-56)
 //   q_raw = clip(rint(fl(x / s) * -4 + 4), 0, 7), 0 where s == 0   (:67-80)
 //   word  = b | sum_i (q_raw_i ^ 4) << (8 + 3 i)        (:113-118)
-// q8_0, Q4_K and Q6_K have no encoder in the reference (it reads them through
+// q8_0, Q4_K, Q5_K and Q6_K have no encoder in the reference (it reads them through
 // the external gguf-py); these are this library's own min/max encoders, the GPU
 // statement of the ones the tests use, producing valid GGUF blocks.
 //
@@ -123,18 +123,25 @@ __global__ __launch_bounds__(kEncodeThreads) void q8_0_quantize_kernel(const flo
     }
 }
 
-// One thread per Q4_K super-block (256 columns, 8 sub-blocks of 32):
-//   lo_j = min(min(x), 0), hi_j = max(x), scale_j = (hi_j - lo_j) / 15, min_j = -lo_j
+// One thread per Q4_K (Q5_K) super-block (256 columns, 8 sub-blocks of 32),
+// with L = 15 (31) code levels:
+//   lo_j = min(min(x), 0), hi_j = max(x), scale_j = (hi_j - lo_j) / L, min_j = -lo_j
 //   d = fp16(max_j scale_j / 63), dmin = fp16(max_j min_j / 63)
 //   sc_j = clip(rint(scale_j / d), 0, 63), m_j = clip(rint(min_j / dmin), 0, 63)
-//   q = clip(rint((x + dmin*m_j) / (d*sc_j)), 0, 15)
+//   q = clip(rint((x + dmin*m_j) / (d*sc_j)), 0, L)
 // with the 12-byte 6-bit scale packing of get_scale_min_k4
 // (qw35-server/src/metal/qw35_matvec.metal:2-12) and the nibble layout
-// qs[32c + l] = q[64c + l] | q[64c + 32 + l] << 4.
-__global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const float* __restrict__ src,
-                                                                       const float* __restrict__ col_scale,
-                                                                       uint8_t* __restrict__ dst, uint64_t n_blocks,
-                                                                       uint32_t blocks_per_row) {
+// qs[32c + l] = q[64c + l] | q[64c + 32 + l] << 4 (low nibbles only for Q5_K,
+// whose qs starts at byte 48; bit 4 of q for element 32j + l is bit j of qh[l],
+// qh at byte 16; qw35_types.metal:9-15).
+template <bool Q5>
+__global__ __launch_bounds__(kEncodeThreads) void k_quantize_kernel(const float* __restrict__ src,
+                                                                    const float* __restrict__ col_scale,
+                                                                    uint8_t* __restrict__ dst, uint64_t n_blocks,
+                                                                    uint32_t blocks_per_row) {
+    constexpr float kLevels = Q5 ? 31.0f : 15.0f;
+    constexpr int kBlockBytes = Q5 ? 176 : 144;
+    constexpr int kQs = Q5 ? 48 : 16;
     for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_blocks;
          i += (uint64_t)gridDim.x * kEncodeThreads) {
         const float* x = src + 256 * i;
@@ -148,7 +155,7 @@ __global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const flo
                 hi = fmaxf(hi, v);
             }
             lo = fminf(lo, 0.0f);
-            scale[j] = __fdiv_rn(__fsub_rn(hi, lo), 15.0f);
+            scale[j] = __fdiv_rn(__fsub_rn(hi, lo), kLevels);
             mins[j] = -lo;
         }
         float smax = scale[0], mmax = mins[0];
@@ -170,7 +177,7 @@ __global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const flo
             step[j] = __fmul_rn(df, (float)sc[j]);
             offs[j] = __fmul_rn(dminf, (float)mq[j]);
         }
-        uint8_t* blk = dst + 144 * i;  // 144-byte blocks: 16-byte aligned
+        uint8_t* blk = dst + kBlockBytes * i;  // 144- or 176-byte blocks: 16-byte aligned
         uint32_t head[4];
         head[0] = d_bits | (dmin_bits << 16);
         uint8_t scales[12];
@@ -183,6 +190,7 @@ __global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const flo
             head[1 + w] = (uint32_t)scales[4 * w] | ((uint32_t)scales[4 * w + 1] << 8) |
                           ((uint32_t)scales[4 * w + 2] << 16) | ((uint32_t)scales[4 * w + 3] << 24);
         *reinterpret_cast<uint4_t*>(blk) = uint4_t{head[0], head[1], head[2], head[3]};
+        uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // Q5_K: 32 bytes
         for (int c = 0; c < 4; ++c) {
             for (int l4 = 0; l4 < 32; l4 += 16) {
                 uint32_t packed[4] = {0, 0, 0, 0};
@@ -193,13 +201,19 @@ __global__ __launch_bounds__(kEncodeThreads) void q4_k_quantize_kernel(const flo
                         const int e = 32 * j + l4 + l;
                         const float v = cs ? __fmul_rn(x[e], cs[e]) : x[e];
                         const float qf = (step[j] != 0.0f) ? __fdiv_rn(__fadd_rn(v, offs[j]), step[j]) : 0.0f;
-                        nib[h] = (uint32_t)fminf(fmaxf(rintf(qf), 0.0f), 15.0f);
+                        const uint32_t q = (uint32_t)fminf(fmaxf(rintf(qf), 0.0f), kLevels);
+                        nib[h] = q & 15u;
+                        if (Q5) qh[(l4 + l) >> 2] |= ((q >> 4) << j) << (8 * ((l4 + l) & 3));
                     }
                     packed[l >> 2] |= (nib[0] | (nib[1] << 4)) << (8 * (l & 3));
                 }
-                *reinterpret_cast<uint4_t*>(blk + 16 + 32 * c + l4) =
+                *reinterpret_cast<uint4_t*>(blk + kQs + 32 * c + l4) =
                     uint4_t{packed[0], packed[1], packed[2], packed[3]};
             }
+        }
+        if (Q5) {
+            *reinterpret_cast<uint4_t*>(blk + 16) = uint4_t{qh[0], qh[1], qh[2], qh[3]};
+            *reinterpret_cast<uint4_t*>(blk + 32) = uint4_t{qh[4], qh[5], qh[6], qh[7]};
         }
     }
 }
@@ -325,9 +339,15 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
                                col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
             break;
         }
+        case kTypeQ5_K: {
+            const uint64_t n = r * (uint64_t)(k / 256);
+            hipLaunchKernelGGL(k_quantize_kernel<true>, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
+                               col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
+            break;
+        }
         default: {
             const uint64_t n = r * (uint64_t)(k / 256);
-            hipLaunchKernelGGL(q4_k_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
+            hipLaunchKernelGGL(k_quantize_kernel<false>, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
                                col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
             break;
         }

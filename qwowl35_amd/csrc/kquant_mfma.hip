@@ -1,10 +1,11 @@
-// q8_0, Q4_K and GF4 decode GEMV / fused gate-up-SwiGLU for gfx950, batch 1..8, on MFMA.
+// q8_0, Q4_K, Q5_K, Q6_K and GF4 decode GEMV / fused gate-up-SwiGLU for gfx950, batch 1..8, on MFMA.
 //
 //   y[b][r] (+)= sum_k W[r][k] * a[k] * x[b][k]
 //
 // Reference kernels replaced:
 //   qw35_decode_matmul_q8_0{,_residual}_f32      (qw35-server/src/metal/qw35_matvec.metal:630-683)
 //   qw35_decode_matmul_q4_k_2row{,_residual}_f32 (qw35-server/src/metal/qw35_matvec.metal:171-353)
+//   qw35_decode_matmul_q5_k_2row_f32             (qw35-server/src/metal/qw35_matvec.metal:355-456)
 //   qw35_decode_matmul_gf4_2row{,_residual}_f32, qw35_ffn_gate_up_swiglu_gf4_f32
 //                                                (qw35-server/src/metal/qw35_gf4.metal:62-136,209-246)
 //
@@ -18,8 +19,9 @@
 //     row b, scaled per chunk by a power of two (max |v| in [2^13, 2^14));
 //   * q8_0 (qw35_types.metal:24-36): one MFMA per 32-element block with a zero
 //     accumulator gives the block partial, scaled in fp32: y += d * sum q x;
-//   * Q4_K (qw35_matvec.metal:2-38): the 6-bit sub-block scale rides in the
-//     fp16 operand, so the super-block's eight MFMAs accumulate in one register
+//   * Q4_K (qw35_matvec.metal:2-38) and Q5_K (qw35_matvec.metal:40-62,355-456;
+//     fifth code bit from qh): the 6-bit sub-block scale rides in the fp16
+//     operand, so the super-block's eight MFMAs accumulate in one register
 //     set and y += d * sum_j sc_j sum q x - dmin * sum_j m_j sum x;
 //     the chunk's inverse activation scale is folded into the last multiply.
 //
@@ -60,6 +62,7 @@ constexpr int kFmtQ8 = 0;
 constexpr int kFmtQ4K = 1;
 constexpr int kFmtGF4 = 2;
 constexpr int kFmtQ6K = 3;
+constexpr int kFmtQ5K = 4;
 
 template <int FMT>
 struct Fmt;
@@ -84,6 +87,13 @@ struct Fmt<kFmtGF4> {
     static constexpr int kSegs = 8;
     static constexpr int kStride = 144;
     static constexpr int kTypeId = 100;
+};
+template <>
+struct Fmt<kFmtQ5K> {
+    static constexpr int kChunkBytes = 176;  // one super-block = 256 columns
+    static constexpr int kSegs = 11;
+    static constexpr int kStride = 192;
+    static constexpr int kTypeId = 13;
 };
 template <>
 struct Fmt<kFmtQ6K> {
@@ -165,7 +175,7 @@ struct KqLds {
     static constexpr int kXpose = 16 * Fmt<FMT>::kStride;
     static constexpr int kActStride = 264;  // halves per activation row
     static constexpr int kAct = 2 * NB * kActStride * 2;
-    static constexpr int kSx = FMT == kFmtQ4K ? NB * 8 * 4 : 0;
+    static constexpr int kSx = (FMT == kFmtQ4K || FMT == kFmtQ5K) ? NB * 8 * 4 : 0;
     static constexpr int kXposeOff = 0;
     static constexpr int kActOff = kXpose;
     static constexpr int kZeroOff = kActOff + kAct;
@@ -316,7 +326,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                     uint2_t_{as_u32(hi0), as_u32(hi1)};
                 *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + 4 * lane) =
                     uint2_t_{as_u32(lo0), as_u32(lo1)};
-                if constexpr (FMT == kFmtQ4K) {
+                if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K) {
                     // sum of the scaled activations of each 32-column sub-block (8 lanes)
                     float s4 = (v[0] + v[1]) + (v[2] + v[3]);
                     s4 += dpp_f32<kDppQuadXor1>(s4);
@@ -428,7 +438,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                             acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
                             acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
                         }
-                    } else {
+                    } else {  // Q4_K, Q5_K
                         const uint4_t hd = *reinterpret_cast<const uint4_t*>(wrow);
                         const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)hd.x);
                         const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x >> 16));
@@ -456,17 +466,27 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                             nbp[i] = scp[i] * h2(-1024.0f, -1024.0f);
                         }
                         // B = sc_j * q as one fused multiply-add of the biased 1024 + q:
-                        // (1024 + q) sc - 1024 sc = sc q <= 945, exact; the eight MFMAs then
-                        // accumulate sum_j sc_j sum q x in one register set.
+                        // (1024 + q) sc - 1024 sc = sc q <= 63 * 31, exact; the eight MFMAs
+                        // then accumulate sum_j sc_j sum q x in one register set.
+                        // Q5_K: bit j of qh byte l (bytes 8kq.. of this lane) is bit 4 of q.
+                        constexpr int kQs = FMT == kFmtQ5K ? 48 : 16;
+                        const uint2_t_ qh = FMT == kFmtQ5K ? *reinterpret_cast<const uint2_t_*>(wrow + 16 + 8 * kq)
+                                                           : uint2_t_{0u, 0u};
                         float4_t dd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int cc = 0; cc < 4; ++cc) {
-                            const uint2_t_ qd = *reinterpret_cast<const uint2_t_*>(wrow + 16 + 32 * cc + 8 * kq);
+                            const uint2_t_ qd = *reinterpret_cast<const uint2_t_*>(wrow + kQs + 32 * cc + 8 * kq);
 #pragma unroll
                             for (int hi = 0; hi < 2; ++hi) {
                                 const int j = 2 * cc + hi;
-                                const uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
-                                const uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
+                                uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
+                                uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
+                                if constexpr (FMT == kFmtQ5K) {
+                                    const uint32_t h0 = j <= 4 ? qh.x << (4 - j) : qh.x >> (j - 4);
+                                    const uint32_t h1 = j <= 4 ? qh.y << (4 - j) : qh.y >> (j - 4);
+                                    t0 |= h0 & 0x10101010u;
+                                    t1 |= h1 & 0x10101010u;
+                                }
                                 const half2_t sp = scp[j >> 1], np = nbp[j >> 1];
                                 const half2_t s2 = (j & 1) ? half2_t{sp.y, sp.y} : half2_t{sp.x, sp.x};
                                 const half2_t n2 = (j & 1) ? half2_t{np.y, np.y} : half2_t{np.x, np.x};
@@ -625,18 +645,18 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     if (chunks <= 16) {
         if (nb >= 4) {
             if (tiles >= 512) {
-                if (fmt == kFmtQ4K || fmt == kFmtQ6K) return tiles >= 4096 ? KqPlan{2, 4, 4, 2} : KqPlan{4, 8, 2, 1};
+                if (fmt != kFmtQ8 && fmt != kFmtGF4) return tiles >= 4096 ? KqPlan{2, 4, 4, 2} : KqPlan{4, 8, 2, 1};
                 if (fmt == kFmtQ8) return {4, 8, 2, 1};
                 return {3, 8, 2, 2};
             }
             return fmt == kFmtQ8 ? KqPlan{1, 8, 2, 1} : KqPlan{1, 8, 2, 2};
         }
-        if ((fmt == kFmtQ4K || fmt == kFmtQ6K) && tiles >= 4096) return {2, 16, 1, 1};
+        if (fmt != kFmtQ8 && fmt != kFmtGF4 && tiles >= 4096) return {2, 16, 1, 1};
         if (fmt == kFmtQ8 && tiles < 512) return {1, 16, 1, 1};
         return {1, 8, 2, 2};
     }
     if (chunks <= 32) return {1, 8, 4, 2};
-    if (fmt == kFmtQ4K || fmt == kFmtQ6K) return nb >= 4 ? KqPlan{1, 12, 4, 2} : KqPlan{1, 16, 3, 2};
+    if (fmt != kFmtQ8 && fmt != kFmtGF4) return nb >= 4 ? KqPlan{1, 12, 4, 2} : KqPlan{1, 16, 3, 2};
     return {1, 8, 6, 2};
 }
 
@@ -698,7 +718,7 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
             QW35_KQ_PLAN(1, 16, 1, 1)
         }
     }
-    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ6K) {
+    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtQ6K) {
         if constexpr (NB >= 4) {
             QW35_KQ_PLAN(2, 4, 4, 2)
             QW35_KQ_PLAN(1, 12, 4, 2)
@@ -731,6 +751,10 @@ hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream) {
     return a.w_up ? kq_launch_any<kFmtQ4K, true>(a, stream) : kq_launch_any<kFmtQ4K, false>(a, stream);
 }
 
+hipError_t launch_q5_k_gemv(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? kq_launch_any<kFmtQ5K, true>(a, stream) : kq_launch_any<kFmtQ5K, false>(a, stream);
+}
+
 hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream) {
     return a.w_up ? kq_launch_any<kFmtGF4, true>(a, stream) : kq_launch_any<kFmtGF4, false>(a, stream);
 }
@@ -746,6 +770,7 @@ int fmt_of(uint32_t type_id) {
     switch (type_id) {
         case kTypeQ8_0: return kFmtQ8;
         case kTypeQ4_K: return kFmtQ4K;
+        case kTypeQ5_K: return kFmtQ5K;
         case kTypeQ6_K: return kFmtQ6K;
         default: return kFmtGF4;
     }
@@ -765,6 +790,7 @@ hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* tok
     switch (type_id) {
         case kTypeQ8_0: e = kq_launch_any<kFmtQ8, false>(a, stream); break;
         case kTypeQ4_K: e = kq_launch_any<kFmtQ4K, false>(a, stream); break;
+        case kTypeQ5_K: e = kq_launch_any<kFmtQ5K, false>(a, stream); break;
         case kTypeQ6_K: e = kq_launch_any<kFmtQ6K, false>(a, stream); break;
         default: e = kq_launch_any<kFmtGF4, false>(a, stream); break;
     }

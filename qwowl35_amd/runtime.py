@@ -26,12 +26,13 @@ from dataclasses import dataclass
 import torch
 
 from . import _ffi
-from ._ffi import Qw35Error, TYPE_F16, TYPE_GF4, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
+from ._ffi import Qw35Error, TYPE_F16, TYPE_GF4, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
 
 _ROW_BYTES = {
     TYPE_GF4: lambda k: (k + 7) // 8 * 4,
     TYPE_Q8_0: lambda k: (k + 31) // 32 * 34,
     TYPE_Q4_K: lambda k: (k + 255) // 256 * 144,
+    TYPE_Q5_K: lambda k: (k + 255) // 256 * 176,
     TYPE_Q6_K: lambda k: (k + 255) // 256 * 210,
     TYPE_F16: lambda k: 2 * k,
 }
@@ -188,7 +189,7 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
                    workspace: torch.Tensor | None | bool = True, stream=None) -> torch.Tensor:
     """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4 or F16 weight (``encodeTiledKMatmul``;
-    a q8_0 / Q4_K / Q6_K weight enters as its fp16 image, ``w.prefill``).
+    a k-quant weight enters as its fp16 image, ``w.prefill``).
 
     ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
     ``out_dtype`` (bfloat16, rounded to nearest even, or float32).
@@ -222,7 +223,7 @@ def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None,
     """Multi-token matvec of fp32 activations [n_tokens, k] (``encodeMatvecBatch``, +FFN.m:260-306).
 
     1..8 tokens run the decode GEMV (fp32 activations); longer chunks run the
-    prefill matmul with fp32 output (GF4 directly, q8_0 / Q4_K / Q6_K through
+    prefill matmul with fp32 output (GF4 directly, the k-quants through
     their fp16 prefill image), as the reference switches to its tiled matmul
     for multi-token chunks.
     """

@@ -77,7 +77,7 @@ def _call_matvec(w, x=4096, dst=4096, nb=1, awq=None):
 @pytest.mark.parametrize(
     "kwargs,needle",
     [
-        (dict(type_id=13), "unsupported tensor type 13"),
+        (dict(type_id=15), "unsupported tensor type 15"),
         (dict(k=100), "multiple of 256"),
         (dict(k=16384), "<= 12288"),
         (dict(rows=0), "rows=0"),
@@ -131,7 +131,7 @@ def test_weight_view_validates_descriptor(lib):
 
 
 def test_error_buffer_truncates_safely(lib):
-    w = _weight(type_id=13)
+    w = _weight(type_id=15)
     err = C.create_string_buffer(8)
     rc = lib.qw35_hip_decode_matvec(C.byref(w), C.c_void_p(4096), None, C.c_void_p(4096), 1, 0, None, err, 8)
     assert rc == 0 and len(err.value) == 7
@@ -140,7 +140,7 @@ def test_error_buffer_truncates_safely(lib):
 @pytest.mark.parametrize(
     "type_id,k,rows,needle",
     [
-        (13, 256, 1, "unsupported tensor type 13"),
+        (15, 256, 1, "unsupported tensor type 15"),
         (14, 512 + 32, 1, "multiple of 256 for q6_k"),
         (100, 12, 1, "multiple of 8 for gf4"),
         (8, 48, 1, "multiple of 32 for q8_0"),
@@ -179,7 +179,7 @@ def _plan_op(kind=0, w=None, up=None, x=4096, dst=4096, nb=1, residual=0):
         ([], "no ops"),
         ([dict(kind=7)], "op 0: unknown kind 7"),
         ([dict(), dict(nb=9)], "op 1: n_batch=9"),
-        ([dict(), dict(wkw=dict(type_id=13))], "op 1: unsupported tensor type 13"),
+        ([dict(), dict(wkw=dict(type_id=15))], "op 1: unsupported tensor type 15"),
         ([dict(kind=0, up=True)], "op 0: a MATVEC op takes no w_up"),
         ([dict(kind=1, up=True, residual=1)], "op 0: a SWIGLU op has no residual form"),
         ([dict(kind=1, up=True, upkw=dict(k=8192))], "op 0: gate and up must share type and shape"),
@@ -254,7 +254,7 @@ def test_output_argmax_workspace_and_validation(lib):
     assert n1 > 0 and n8 > n1 and n1 % 256 == 0 and n8 % 256 == 0
     assert lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 0) == 0
     assert lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 9) == 0
-    assert lib.qw35_hip_output_argmax_workspace_size(C.byref(_weight(type_id=13)), 1) == 0
+    assert lib.qw35_hip_output_argmax_workspace_size(C.byref(_weight(type_id=15)), 1) == 0
 
     def call(x=4096, tok=4096, lg=4096, ws=1 << 20, ws_bytes=None, nb=1):
         return _ffi.call("qw35_hip_output_argmax", C.byref(w), C.c_void_p(x), None, nb, C.c_void_p(tok),

@@ -40,7 +40,7 @@ def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     return bool(np.all(same | both_nan))
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("rows,k", [(3, 256), (64, 4096), (37, 12288)])
 def test_dequant_bit_exact(cuda, name, rows, k):
     type_id = TYPES[name]
@@ -69,7 +69,7 @@ def test_dequant_row_gather(cuda):
     assert _bits_equal(got, want)
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("rows,k", [(1, 256), (37, 4096), (130, 12288), (5, 8192), (64, 1024)])
 @pytest.mark.parametrize("nb", [1, 2, 3, 8])
 def test_gemv_parity(cuda, name, rows, k, nb):
@@ -83,7 +83,7 @@ def test_gemv_parity(cuda, name, rows, k, nb):
     assert om.rel_l2(y, want) <= GEMV_REL_L2
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
 def test_gemv_awq_and_residual(cuda, name):
     import torch
 
@@ -101,7 +101,7 @@ def test_gemv_awq_and_residual(cuda, name):
     assert om.rel_l2(dst.cpu().numpy(), want) <= GEMV_REL_L2
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k"])
+@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("nb", [1, 4])
 def test_swiglu_parity(cuda, name, nb):
     type_id = TYPES[name]
@@ -154,3 +154,26 @@ def test_golden_fixtures(cuda):
         assert om.rel_l2(y, g[f"{name}_y"]) <= GEMV_REL_L2, name
     w = _upload(g["gf4_any_words"].view(np.uint8), om.TYPE_GF4, 8, 512)
     assert _bits_equal(_rt().dequantize(w).cpu().numpy(), g["gf4_any_deq"])
+
+
+@pytest.mark.parametrize("name", ["q4_k", "q5_k"])
+@pytest.mark.parametrize("nb", [1, 8])
+def test_gemv_large_ragged_kquant(cuda, name, nb):
+    """65549 x 4096 k-quant weights made on the GPU (the >= 4096-tile plans of
+    an LM-head-sized matrix, with a ragged last tile): the GEMV against the fp64
+    product of the library's dequantised weight, which the tests above pin
+    bit-for-bit to the oracle at smaller shapes."""
+    import torch
+
+    rt = _rt()
+    type_id = TYPES[name]
+    rows, k = 65549, 4096
+    g = torch.Generator(device=cuda)
+    g.manual_seed(5 + nb)
+    src = torch.randn((rows, k), generator=g, device=cuda) * 0.02
+    w = rt.quantize_weight(src, type_id)
+    del src
+    x = torch.randn((nb, k), generator=g, device=cuda)
+    y = rt.decode_matvec(w, x).double()
+    want = rt.dequantize(w).double() @ x.double().T
+    assert om.rel_l2(y.cpu().numpy(), want.T.cpu().numpy()) <= GEMV_REL_L2
