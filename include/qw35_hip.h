@@ -16,6 +16,9 @@
  *
  * Weight formats are the reference's raw GGUF tensor bytes (no repacking):
  *   type 100  GF4   8 elems / 4 B   (tools/gguf_custom_types.py:26-30)
+ *   type 101  GF2   256 elems / 80 B super-blocks: 16 code words, then their
+ *             16 e5m2 scale bytes (qw35-server/src/metal/qw35_gf2.metal:1-17;
+ *             qw35-server/src/loader/tensors.rs:124-135)
  *   type   8  q8_0 32 elems / 34 B  (qw35-server/src/loader/tensors.rs:142)
  *   type  12  Q4_K 256 elems / 144 B (qw35-server/src/loader/tensors.rs:146)
  *   type  13  Q5_K 256 elems / 176 B (qw35-server/src/loader/tensors.rs:147;
@@ -46,6 +49,7 @@ extern "C" {
 #define QW35_HIP_TYPE_Q5_K 13u
 #define QW35_HIP_TYPE_Q6_K 14u
 #define QW35_HIP_TYPE_GF4 100u
+#define QW35_HIP_TYPE_GF2 101u
 #define QW35_HIP_MAX_BATCH 8u
 
 /* GGUF tensor descriptor; field-for-field the reference's
@@ -98,7 +102,7 @@ int qw35_hip_decode_matvec(const qw35_hip_weight *w, const float *x, const float
  *   dst[b][r] = silu(gate[r] . (awq*x[b])) * (up[r] . (awq*x[b])),  silu(v) = v / (1 + exp(-v))
  * gate and up share type and shape.  Replaces encodeGf4FusedFfn
  * (Qw35MetalRuntime+FFN.m:13-35) / qw35_ffn_gate_up_swiglu_gf4_f32
- * (qw35-server/src/metal/qw35_gf4.metal:62-96), for GF4, q8_0, Q4_K and Q5_K
+ * (qw35-server/src/metal/qw35_gf4.metal:62-96), for GF4, GF2, q8_0, Q4_K and Q5_K
  * (Q6_K is rejected: the reference uses it for the LM head only). */
 int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weight *up, const float *x,
                                 const float *awq, float *dst, uint32_t n_batch, void *stream, char *err,
@@ -112,7 +116,7 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weig
  * encodeOutputHead (qw35-server/src/metal/bridge/Qw35MetalRuntime+Output.m:11-65):
  * qw35_output_q6_k_argmax_partials_16row_f32 + qw35_output_argmax_reduce_partials_f32
  * (qw35-server/src/metal/qw35_output.metal:2-182).  Any supported type (the
- * reference's head is Q6_K or GF4).  For the k-quants the logits are
+ * reference's head is Q6_K or GF4).  For the k-quants and GF2 the logits are
  * bit-identical to qw35_hip_decode_matvec's.  Two launches on `stream`;
  * workspace: device memory of qw35_hip_output_argmax_workspace_size(w, n_batch)
  * bytes (256-byte aligned, caller-owned, not shared by concurrent calls). */
@@ -134,7 +138,7 @@ int qw35_hip_dequantize(const qw35_hip_weight *w, const uint32_t *row_ids, uint3
  * the rounding the reference's tiled matmul applies when it dequantises a
  * k-quant weight tile to half (qw35_kernel_mul_mm, qw35-server/src/metal/
  * qw35_tiled_mm.metal:199-255).  Viewed as a type-1 (F16) weight it is the
- * operand of qw35_hip_matmul_prefill for q8_0 / Q4_K / Q5_K / Q6_K projections; made
+ * operand of qw35_hip_matmul_prefill for GF2 / q8_0 / Q4_K / Q5_K / Q6_K projections; made
  * once and kept resident (2 bytes per weight: about 4.2 GB for the 9B's q8_0
  * projections). */
 int qw35_hip_dequantize_f16(const qw35_hip_weight *w, void *dst, void *stream, char *err, uintptr_t err_len);
@@ -179,8 +183,8 @@ void qw35_hip_plan_destroy(void *plan);
  * encodeTiledKMatmul for type 100 (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366,
  * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255) and, through
  * an F16 weight (the prefill image of qw35_hip_dequantize_f16), for the
- * q8_0 / Q4_K / Q5_K / Q6_K projections (qw35_mul_mm_{q4_k,q5_k,q6_k,q8_0}_f32,
- * :209-214,236-255).
+ * GF2 / q8_0 / Q4_K / Q5_K / Q6_K projections
+ * (qw35_mul_mm_{gf2,q4_k,q5_k,q6_k,q8_0}_f32, qw35_tiled_mm.metal:208-254).
  * 1 <= n_tokens <= 65536, rows <= 2^24. */
 #define QW35_HIP_DTYPE_F32 0u
 #define QW35_HIP_DTYPE_BF16 1u
@@ -209,7 +213,7 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_
  * column c before encoding: the AWQ column scale of pack_ffn_gf4
  * (tools/qw35_cook_common.py:182-199).  GF4 is bit-identical to the reference
  * packer pack_gf4_prepared(rows, scale_search=False) (:83-119).  q8_0 (k % 32),
- * Q4_K, Q5_K and Q6_K (k % 256) are this library's min/max encoders; the reference
+ * Q4_K, Q5_K, Q6_K and GF2 (k % 256) are this library's min/max encoders; the reference
  * has none (it reads those types through gguf-py).  src must be finite. */
 int qw35_hip_quantize(uint32_t type_id, const float *src, uint64_t rows, uint64_t k, const float *col_scale,
                       void *dst, void *stream, char *err, uintptr_t err_len);

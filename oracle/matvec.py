@@ -19,9 +19,10 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import gf4, q4_k, q5_k, q6_k, q8_0
+from . import gf2, gf4, q4_k, q5_k, q6_k, q8_0
 
 TYPE_GF4 = gf4.GF4_TYPE_ID
+TYPE_GF2 = gf2.GF2_TYPE_ID
 TYPE_Q8_0 = q8_0.Q8_0_TYPE_ID
 TYPE_Q4_K = q4_k.Q4_K_TYPE_ID
 TYPE_Q5_K = q5_k.Q5_K_TYPE_ID
@@ -33,6 +34,8 @@ def tensor_nbytes(type_id: int, rows: int, k: int) -> int:
     """Byte size of a rows x k tensor (``qw35-server/src/loader/tensors.rs:123-172``)."""
     if type_id == TYPE_GF4:
         return gf4.gf4_nbytes(rows, k)
+    if type_id == TYPE_GF2:
+        return gf2.gf2_nbytes(rows, k)
     if type_id == TYPE_Q8_0:
         return q8_0.q8_0_nbytes(rows, k)
     if type_id == TYPE_Q4_K:
@@ -51,6 +54,8 @@ def quantize(type_id: int, w: np.ndarray) -> np.ndarray:
     """fp32 [R, K] -> raw tensor bytes as uint8 [R, row_bytes]."""
     if type_id == TYPE_GF4:
         return gf4.gf4_pack(w).view(np.uint8).reshape(w.shape[0], -1)
+    if type_id == TYPE_GF2:
+        return gf2.gf2_quantize(w)
     if type_id == TYPE_Q8_0:
         return q8_0.q8_0_quantize(w)
     if type_id == TYPE_Q4_K:
@@ -69,6 +74,8 @@ def dequant(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
     raw = np.ascontiguousarray(raw).view(np.uint8).reshape(rows, -1)
     if type_id == TYPE_GF4:
         return gf4.gf4_dequant(raw.view("<u4"))
+    if type_id == TYPE_GF2:
+        return gf2.gf2_dequant(raw, rows, raw.size // rows // gf2.GF2_BLOCK_BYTES * gf2.GF2_BLOCK_ELEMS)
     if type_id == TYPE_Q8_0:
         return q8_0.q8_0_dequant(raw)
     if type_id == TYPE_Q4_K:

@@ -16,6 +16,7 @@ TYPE_F16 = 1
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
 TYPE_Q5_K = 13
+TYPE_GF2 = 101
 TYPE_Q6_K = 14
 TYPE_GF4 = 100
 MAX_BATCH = 8

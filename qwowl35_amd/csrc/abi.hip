@@ -21,7 +21,8 @@ void set_err(char* err, uintptr_t err_len, const char* fmt, ...) {
 }
 
 bool type_supported(uint32_t t) {
-    return t == qw35::kTypeGF4 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K || t == qw35::kTypeQ5_K ||
+    return t == qw35::kTypeGF4 || t == qw35::kTypeGF2 || t == qw35::kTypeQ8_0 || t == qw35::kTypeQ4_K ||
+           t == qw35::kTypeQ5_K ||
            t == qw35::kTypeQ6_K ||
            t == qw35::kTypeF16;
 }
@@ -29,6 +30,7 @@ bool type_supported(uint32_t t) {
 uint64_t row_bytes(uint32_t t, uint64_t k) {
     switch (t) {
         case qw35::kTypeGF4: return (k + 7) / 8 * 4;
+        case qw35::kTypeGF2: return (k + 15) / 16 * 5;
         case qw35::kTypeQ8_0: return (k + 31) / 32 * 34;
         case qw35::kTypeQ4_K: return (k + 255) / 256 * 144;
         case qw35::kTypeQ5_K: return (k + 255) / 256 * 176;
@@ -41,6 +43,7 @@ uint64_t row_bytes(uint32_t t, uint64_t k) {
 const char* type_name(uint32_t t) {
     switch (t) {
         case qw35::kTypeGF4: return "gf4";
+        case qw35::kTypeGF2: return "gf2";
         case qw35::kTypeQ8_0: return "q8_0";
         case qw35::kTypeQ4_K: return "q4_k";
         case qw35::kTypeQ5_K: return "q5_k";
@@ -105,6 +108,7 @@ hipError_t dispatch_gemv(uint32_t type_id, const qw35::GemvArgs& a, hipStream_t 
         case qw35::kTypeGF4: return qw35::launch_gf4_gemv(a, s);
         case qw35::kTypeQ8_0: return qw35::launch_q8_0_gemv(a, s);
         case qw35::kTypeQ5_K: return qw35::launch_q5_k_gemv(a, s);
+        case qw35::kTypeGF2: return qw35::launch_gf2_gemv(a, s);
         case qw35::kTypeQ6_K: return qw35::launch_q6_k_gemv(a, s);
         default: return qw35::launch_q4_k_gemv(a, s);
     }

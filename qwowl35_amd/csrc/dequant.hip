@@ -1,4 +1,4 @@
-// fp32 (or fp16) dequantisation of GF4 / q8_0 / Q4_K / Q5_K / Q6_K / F16 tensors,
+// fp32 (or fp16) dequantisation of GF4 / GF2 / q8_0 / Q4_K / Q5_K / Q6_K / F16 tensors,
 // optionally gathering rows.
 //
 // This is the library's bit-exact statement of each format (every weight of
@@ -7,6 +7,7 @@
 // qw35_get_row(s)_{q8_0,q4_k}_f32 (qw35-server/src/metal/qw35_matvec.metal:100-169).
 //
 //   GF4  (tools/qw35_cook_common.py:79):  w = (4 - (c ^ 4)) * 0.25 * s, s = fp16(b << 8)
+//   GF2  (qw35_gf2.metal:19-50):          w = (q * fl(2/3) - 1) * s in fp32 steps, s = fp16(b << 8)
 //   q8_0 (qw35_types.metal:24-36):        w = fp32(d) * qs[i]
 //   Q4_K (qw35_matvec.metal:2-12):        w = d * sc_j * q - dmin * m_j
 //   Q5_K (qw35_matvec.metal:40-62):       the same with q = nibble | (bit j of qh[e % 32]) << 4
@@ -47,6 +48,18 @@ __global__ __launch_bounds__(256) void dequant_kernel(uint32_t type_id, const ui
         for (int i = 0; i < 8; ++i) {
             const uint32_t q = ((word >> (8 + 3 * i)) & 7u) ^ 4u;
             v[i] = (4.0f - (float)q) * 0.25f * s;
+        }
+    } else if (type_id == kTypeGF2) {
+        // 80-byte super-blocks of 256 columns: 16 code words, then their 16 scale bytes
+        const int col = 8 * g;
+        const uint8_t* blk = w + src_row * (size_t)(k >> 8) * 80 + (size_t)(col >> 8) * 80;
+        const int wi = (col & 255) >> 4;
+        const uint32_t word = reinterpret_cast<const uint32_t*>(blk)[wi] >> (2 * (col & 15));
+        const float s = f16_to_f32((uint32_t)blk[64 + wi] << 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float lev = __fsub_rn(__fmul_rn((float)((word >> (2 * i)) & 3u), 2.0f / 3.0f), 1.0f);
+            v[i] = __fmul_rn(lev, s);
         }
     } else if (type_id == kTypeQ8_0) {
         const uint8_t* row = w + src_row * (size_t)(k >> 5) * 34;

@@ -1,4 +1,4 @@
-// Weight producers: fp32 matrix -> GF4 / q8_0 / Q4_K / Q5_K / Q6_K / F16 tensor bytes, on the GPU.
+// Weight producers: fp32 matrix -> GF4 / GF2 / q8_0 / Q4_K / Q5_K / Q6_K / F16 tensor bytes, on the GPU.
 //
 // GF4 is the reference packer pack_gf4_prepared(rows, scale_search=False)
 // (tools/qw35_cook_common.py:83-119), including the optional AWQ column
@@ -80,6 +80,47 @@ __global__ __launch_bounds__(kEncodeThreads) void gf4_pack_kernel(const float* _
 }
 
 // One thread per q8_0 block: d = max|x| / 127, q = round_half_away(x * (1/d)).
+// One thread per GF2 super-block (256 columns = 16 groups of 16; this library's
+// encoder, the statement of oracle gf2_quantize):
+//   b = e5m2(max |x|) (fp16 RNE, low byte rounded half-up), s = fp16(b << 8)
+//   t = x / s (0 where s == 0), q = clip(rint(t * 1.5 + 1.5), 0, 3)
+// written as the reference's super-block: 16 code words (code i of word w in
+// bits 2i, 2i+1 for column 16w + i) then the 16 scale bytes
+// (qw35-server/src/metal/qw35_gf2.metal:1-17).
+__global__ __launch_bounds__(kEncodeThreads) void gf2_pack_kernel(const float* __restrict__ src,
+                                                                  const float* __restrict__ col_scale,
+                                                                  uint8_t* __restrict__ dst, uint64_t n_blocks,
+                                                                  uint32_t blocks_per_row) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kEncodeThreads + threadIdx.x; i < n_blocks;
+         i += (uint64_t)gridDim.x * kEncodeThreads) {
+        const float* x = src + 256 * i;
+        const float* cs = col_scale ? col_scale + 256u * (uint32_t)(i % blocks_per_row) : nullptr;
+        uint32_t words[16];
+        uint32_t sb[4] = {0, 0, 0, 0};
+        for (int w = 0; w < 16; ++w) {
+            float v[16];
+            float amax = 0.0f;
+            for (int l = 0; l < 16; ++l) {
+                v[l] = cs ? __fmul_rn(x[16 * w + l], cs[16 * w + l]) : x[16 * w + l];
+                amax = fmaxf(amax, fabsf(v[l]));
+            }
+            const uint32_t b = ((f32_to_f16_bits(amax) + 0x80u) >> 8) & 0xFFu;
+            const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)(b << 8));
+            uint32_t word = 0;
+            for (int l = 0; l < 16; ++l) {
+                const float t = s != 0.0f ? __fdiv_rn(v[l], s) : 0.0f;
+                const float q = fminf(fmaxf(rintf(__fadd_rn(__fmul_rn(t, 1.5f), 1.5f)), 0.0f), 3.0f);
+                word |= (uint32_t)q << (2 * l);
+            }
+            words[w] = word;
+            sb[w >> 2] |= b << (8 * (w & 3));
+        }
+        uint4_t* o = reinterpret_cast<uint4_t*>(dst + 80 * i);  // 80-byte blocks: 16-byte aligned
+        for (int q = 0; q < 4; ++q) o[q] = uint4_t{words[4 * q], words[4 * q + 1], words[4 * q + 2], words[4 * q + 3]};
+        o[4] = uint4_t{sb[0], sb[1], sb[2], sb[3]};
+    }
+}
+
 __global__ __launch_bounds__(kEncodeThreads) void q8_0_quantize_kernel(const float* __restrict__ src,
                                                                        const float* __restrict__ col_scale,
                                                                        uint8_t* __restrict__ dst, uint64_t n_blocks,
@@ -337,6 +378,12 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
             const uint64_t n = r * (uint64_t)(k / 256);
             hipLaunchKernelGGL(q6_k_quantize_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src,
                                col_scale, static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
+            break;
+        }
+        case kTypeGF2: {
+            const uint64_t n = r * (uint64_t)(k / 256);
+            hipLaunchKernelGGL(gf2_pack_kernel, dim3(grid_for(n)), dim3(kEncodeThreads), 0, stream, src, col_scale,
+                               static_cast<uint8_t*>(dst), n, (uint32_t)(k / 256));
             break;
         }
         case kTypeQ5_K: {

@@ -63,6 +63,7 @@ constexpr int kFmtQ4K = 1;
 constexpr int kFmtGF4 = 2;
 constexpr int kFmtQ6K = 3;
 constexpr int kFmtQ5K = 4;
+constexpr int kFmtGF2 = 5;
 
 template <int FMT>
 struct Fmt;
@@ -94,6 +95,13 @@ struct Fmt<kFmtQ5K> {
     static constexpr int kSegs = 11;
     static constexpr int kStride = 192;
     static constexpr int kTypeId = 13;
+};
+template <>
+struct Fmt<kFmtGF2> {
+    static constexpr int kChunkBytes = 80;  // 16 code words + 16 scale bytes = 256 columns
+    static constexpr int kSegs = 5;
+    static constexpr int kStride = 96;
+    static constexpr int kTypeId = 101;
 };
 template <>
 struct Fmt<kFmtQ6K> {
@@ -317,14 +325,31 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                     } else {
                         e[0] = v[0]; e[1] = u[0]; e[2] = v[1]; e[3] = u[1];
                     }
+                } else if constexpr (FMT == kFmtGF2) {
+                    // Columns 16w..16w+15 stored as x0 x8 x1 x9 .. x3 x11 | x4 x12 .. x7 x15
+                    // (MFMA k-slots of lane groups 2(w&1), 2(w&1)+1): the lanes holding
+                    // columns 0..3 / 4..7 write (x_c, x_c+8) pairs of their first two
+                    // columns, the lanes holding 8..11 / 12..15 those of the last two.
+                    float u[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor2>(v[q]);
+                    if (lane & 2) {
+                        e[0] = u[2]; e[1] = v[2]; e[2] = u[3]; e[3] = v[3];
+                    } else {
+                        e[0] = v[0]; e[1] = u[0]; e[2] = v[1]; e[3] = u[1];
+                    }
                 }
+                // GF2 k-slot of the lane's four values (natural order otherwise)
+                const int apos = FMT == kFmtGF2 ? 32 * (lane >> 3) + 16 * ((lane >> 2) & 1) + 8 * (lane & 1) +
+                                                      4 * ((lane >> 1) & 1)
+                                                : 4 * lane;
                 const half2_t hi0 = h2(e[0], e[1]);
                 const half2_t hi1 = h2(e[2], e[3]);
                 const half2_t lo0 = h2(e[0] - (float)hi0.x, e[1] - (float)hi0.y);
                 const half2_t lo1 = h2(e[2] - (float)hi1.x, e[3] - (float)hi1.y);
-                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + 4 * lane) =
+                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + apos) =
                     uint2_t_{as_u32(hi0), as_u32(hi1)};
-                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + 4 * lane) =
+                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + apos) =
                     uint2_t_{as_u32(lo0), as_u32(lo1)};
                 if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K) {
                     // sum of the scaled activations of each 32-column sub-block (8 lanes)
@@ -406,6 +431,42 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                             acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
                             acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
                         }
+                    } else if constexpr (FMT == kFmtGF2) {
+                        // Step j (32 columns): lane group kq decodes word 2j + (kq >> 1),
+                        // codes m and m + 8 for m = 4(kq & 1) .. +3, as pairs in the order
+                        // the activations were staged.  Mantissa 2q over 1024:
+                        // (1024 + 2q) / 4 - 256.75 = (2q - 3) / 4, exact; times s exact
+                        // (5 significant bits); y = 4/3 sum B x.
+                        const int hw = kq >> 1;
+                        const uint4_t scv = *reinterpret_cast<const uint4_t*>(wrow + 64);
+                        const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+                        // (byte << 8) in both halves: byte hw (even j) or 2 + hw (odd j) of dword j/2
+                        const uint32_t sel_even = 0x000C000Cu | (uint32_t)hw * 0x01000100u;
+                        const uint32_t sel_odd = 0x020C020Cu | (uint32_t)hw * 0x01000100u;
+                        const uint32_t* words = reinterpret_cast<const uint32_t*>(wrow) + hw;
+                        const int csh = 8 * (kq & 1);
+                        float4_t dd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t cw = words[2 * j] >> csh;
+                            const half2_t s2 = as_half2(__builtin_amdgcn_perm(scw[j >> 1], scw[j >> 1],
+                                                                              (j & 1) ? sel_odd : sel_even));
+                            const uint32_t pr[4] = {cw << 1, cw >> 1, cw >> 3, cw >> 5};
+                            uint32_t b4[4];
+#pragma unroll
+                            for (int p = 0; p < 4; ++p) {
+                                const half2_t pq = as_half2(and_xor(pr[p], 0x00060006u, 0x64006400u));
+                                b4[p] = as_u32(__builtin_elementwise_fma(pq, h2(0.25f, 0.25f), h2(-256.75f, -256.75f)) *
+                                               s2);
+                            }
+                            const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
+                            const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
+                            dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, dd, 0, 0, 0);
+                        }
+                        constexpr float kFourThirds = 4.0f / 3.0f;
+                        acc[t][m][0] = __builtin_fmaf(inv_sc[0] * kFourThirds, dd[0] + dd[1], acc[t][m][0]);
+                        if constexpr (NB > 1)
+                            acc[t][m][1] = __builtin_fmaf(inv_sc[1] * kFourThirds, dd[2] + dd[3], acc[t][m][1]);
                     } else if constexpr (FMT == kFmtQ6K) {
                         // The super-block starts `off` bytes into the row buffer
                         // (even); words are read 4-aligned and realigned by sh.
@@ -718,7 +779,7 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
             QW35_KQ_PLAN(1, 16, 1, 1)
         }
     }
-    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtQ6K) {
+    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtQ6K || FMT == kFmtGF2) {
         if constexpr (NB >= 4) {
             QW35_KQ_PLAN(2, 4, 4, 2)
             QW35_KQ_PLAN(1, 12, 4, 2)
@@ -755,6 +816,10 @@ hipError_t launch_q5_k_gemv(const GemvArgs& a, hipStream_t stream) {
     return a.w_up ? kq_launch_any<kFmtQ5K, true>(a, stream) : kq_launch_any<kFmtQ5K, false>(a, stream);
 }
 
+hipError_t launch_gf2_gemv(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? kq_launch_any<kFmtGF2, true>(a, stream) : kq_launch_any<kFmtGF2, false>(a, stream);
+}
+
 hipError_t launch_gf4_gemv_chunked(const GemvArgs& a, hipStream_t stream) {
     return a.w_up ? kq_launch_any<kFmtGF4, true>(a, stream) : kq_launch_any<kFmtGF4, false>(a, stream);
 }
@@ -771,6 +836,7 @@ int fmt_of(uint32_t type_id) {
         case kTypeQ8_0: return kFmtQ8;
         case kTypeQ4_K: return kFmtQ4K;
         case kTypeQ5_K: return kFmtQ5K;
+        case kTypeGF2: return kFmtGF2;
         case kTypeQ6_K: return kFmtQ6K;
         default: return kFmtGF4;
     }
@@ -791,6 +857,7 @@ hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* tok
         case kTypeQ8_0: e = kq_launch_any<kFmtQ8, false>(a, stream); break;
         case kTypeQ4_K: e = kq_launch_any<kFmtQ4K, false>(a, stream); break;
         case kTypeQ5_K: e = kq_launch_any<kFmtQ5K, false>(a, stream); break;
+        case kTypeGF2: e = kq_launch_any<kFmtGF2, false>(a, stream); break;
         case kTypeQ6_K: e = kq_launch_any<kFmtQ6K, false>(a, stream); break;
         default: e = kq_launch_any<kFmtGF4, false>(a, stream); break;
     }

@@ -14,6 +14,7 @@ constexpr uint32_t kTypeQ4_K = 12;
 constexpr uint32_t kTypeQ5_K = 13;
 constexpr uint32_t kTypeQ6_K = 14;
 constexpr uint32_t kTypeGF4 = 100;
+constexpr uint32_t kTypeGF2 = 101;
 
 // Largest decode batch of the GEMV kernels.
 constexpr int kMaxDecodeBatch = 8;
@@ -49,6 +50,7 @@ hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q5_k_gemv(const GemvArgs& a, hipStream_t stream);
+hipError_t launch_gf2_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q6_k_gemv(const GemvArgs& a, hipStream_t stream);
 
 // Greedy head: workgroups of the GEMV launch that launch_argmax_gemv makes for

@@ -26,13 +26,14 @@ from dataclasses import dataclass
 import torch
 
 from . import _ffi
-from ._ffi import Qw35Error, TYPE_F16, TYPE_GF4, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
+from ._ffi import Qw35Error, TYPE_F16, TYPE_GF2, TYPE_GF4, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0  # noqa: F401
 
 _ROW_BYTES = {
     TYPE_GF4: lambda k: (k + 7) // 8 * 4,
     TYPE_Q8_0: lambda k: (k + 31) // 32 * 34,
     TYPE_Q4_K: lambda k: (k + 255) // 256 * 144,
     TYPE_Q5_K: lambda k: (k + 255) // 256 * 176,
+    TYPE_GF2: lambda k: (k + 15) // 16 * 5,
     TYPE_Q6_K: lambda k: (k + 255) // 256 * 210,
     TYPE_F16: lambda k: 2 * k,
 }

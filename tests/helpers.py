@@ -5,7 +5,7 @@ import numpy as np
 
 from oracle import matvec as om
 
-TYPES = {"gf4": om.TYPE_GF4, "q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "q5_k": om.TYPE_Q5_K,
+TYPES = {"gf4": om.TYPE_GF4, "gf2": om.TYPE_GF2, "q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "q5_k": om.TYPE_Q5_K,
          "q6_k": om.TYPE_Q6_K}
 
 # rel-L2 bound of a GEMV against the fp64 matvec of the dequantised weights.

@@ -81,7 +81,7 @@ def test_gf4_pack_with_awq_columns(cuda):
     assert np.array_equal(got.reshape(rows, k // 8), want)
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf2", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("rows,k", [(1, 256), (33, 4096), (7, 12288)])
 def test_kquant_encoders_bit_exact(cuda, name, rows, k):
     type_id = TYPES[name]
@@ -92,7 +92,7 @@ def test_kquant_encoders_bit_exact(cuda, name, rows, k):
     assert np.array_equal(got, om.quantize(type_id, w))
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf2", "q8_0", "q4_k", "q5_k"])
 def test_kquant_encoders_wide_range_and_awq(cuda, name):
     type_id = TYPES[name]
     rng = np.random.default_rng(9)

@@ -40,7 +40,7 @@ def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     return bool(np.all(same | both_nan))
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf4", "gf2", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("rows,k", [(3, 256), (64, 4096), (37, 12288)])
 def test_dequant_bit_exact(cuda, name, rows, k):
     type_id = TYPES[name]
@@ -69,7 +69,7 @@ def test_dequant_row_gather(cuda):
     assert _bits_equal(got, want)
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf4", "gf2", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("rows,k", [(1, 256), (37, 4096), (130, 12288), (5, 8192), (64, 1024)])
 @pytest.mark.parametrize("nb", [1, 2, 3, 8])
 def test_gemv_parity(cuda, name, rows, k, nb):
@@ -83,7 +83,7 @@ def test_gemv_parity(cuda, name, rows, k, nb):
     assert om.rel_l2(y, want) <= GEMV_REL_L2
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf4", "gf2", "q8_0", "q4_k", "q5_k"])
 def test_gemv_awq_and_residual(cuda, name):
     import torch
 
@@ -101,7 +101,7 @@ def test_gemv_awq_and_residual(cuda, name):
     assert om.rel_l2(dst.cpu().numpy(), want) <= GEMV_REL_L2
 
 
-@pytest.mark.parametrize("name", ["gf4", "q8_0", "q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf4", "gf2", "q8_0", "q4_k", "q5_k"])
 @pytest.mark.parametrize("nb", [1, 4])
 def test_swiglu_parity(cuda, name, nb):
     type_id = TYPES[name]
@@ -156,7 +156,7 @@ def test_golden_fixtures(cuda):
     assert _bits_equal(_rt().dequantize(w).cpu().numpy(), g["gf4_any_deq"])
 
 
-@pytest.mark.parametrize("name", ["q4_k", "q5_k"])
+@pytest.mark.parametrize("name", ["gf2", "q4_k", "q5_k"])
 @pytest.mark.parametrize("nb", [1, 8])
 def test_gemv_large_ragged_kquant(cuda, name, nb):
     """65549 x 4096 k-quant weights made on the GPU (the >= 4096-tile plans of

@@ -122,7 +122,7 @@ def test_plan_reads_inputs_updated_in_place(cuda):
     plan.close()
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("name", ["gf2", "q8_0", "q4_k", "q5_k", "q6_k"])
 @pytest.mark.parametrize("nb", [1, 5])
 def test_plan_merges_projections_sharing_inputs(cuda, name, nb):
     """Consecutive k-quant matvecs over one input (a mixer's q/k/v or

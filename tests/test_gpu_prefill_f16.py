@@ -20,7 +20,7 @@ from tests.helpers import activations, awq_scales, bf16_normal, make_weight
 
 pytestmark = pytest.mark.gpu
 
-NAMES = {"gf4": om.TYPE_GF4, "q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "q5_k": om.TYPE_Q5_K,
+NAMES = {"gf4": om.TYPE_GF4, "gf2": om.TYPE_GF2, "q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "q5_k": om.TYPE_Q5_K,
          "q6_k": om.TYPE_Q6_K}
 
 
@@ -108,7 +108,7 @@ def test_f16_prefill_fp32_input(cuda):
     assert om.rel_l2(out, want) <= 1e-3
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("name", ["gf2", "q8_0", "q4_k", "q5_k", "q6_k"])
 def test_matvec_batch_long_kquant_chunk(cuda, name):
     rows, k, m = 700, 4096, 64
     raw, deq = _weight(name, rows, k, seed=9)
