@@ -231,6 +231,27 @@ def bench_q6k_head(b: Bench, rt, torch) -> dict:
     return out
 
 
+def bench_codecs(b: Bench, rt, torch, steps: int, warmup: int) -> dict:
+    """Every decode-GEMV codec on one 12288x4096 projection at batch 1 and 8,
+    rotating enough copies (>= 640 MB) that the 256 MB last-level cache holds none."""
+    out = {}
+    rows, k = 12288, 4096
+    names = {"gf4": rt.TYPE_GF4, "gf2": rt.TYPE_GF2, "q8_0": rt.TYPE_Q8_0, "q4_k": rt.TYPE_Q4_K,
+             "q5_k": rt.TYPE_Q5_K, "q6_k": rt.TYPE_Q6_K}
+    for name, t in names.items():
+        nbytes = rows * rt.row_bytes(t, k)
+        copies = max(2, -(-(640 << 20) // nbytes))
+        ws = [b.weight(t, rows, k) for _ in range(copies)]
+        for nb in (1, 8):
+            x = b.normal((nb, k))
+            y = torch.zeros((nb, rows), dtype=torch.float32, device=b.dev)
+            m, _, _ = b.time_calls(gemv_calls(rt, ws, x, y), steps, warmup)
+            out[f"codec_{name}_b{nb}_12288x4096"] = {"us": round(m * 1e3, 3),
+                                                     "GB/s": round(gemv_bytes(t, rows, k, nb, rt) / m / 1e6, 1)}
+        del ws
+    return out
+
+
 def bench_decode_stack(b: Bench, rt, torch) -> dict:
     """Config 5: the 32-layer Qwen3.5-9B decode-step projection stack as one
     recorded plan (hipGraph): per layer the q8_0 mixer projections (full
@@ -336,7 +357,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--headline-only", action="store_true", help="skip the extra configs (= --extras none)")
     ap.add_argument("--extras", default="all",
-                    help="comma list of extra configs: gf4,q8,q4k,q6k,prefill,stack (or all / none)")
+                    help="comma list of extra configs: gf4,q8,q4k,q6k,codecs,prefill,stack (or all / none)")
     ap.add_argument("--cpu-reps", type=int, default=40)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -374,7 +395,8 @@ def main() -> int:
     best_us = ceil["launch_floor_us"] + algo / (ceil["GB/s_1GiB"] * 1e3)
     extra["single_launch_frac_bound"] = round(algo / (best_us * 1e3) / HBM_PEAK_GBS, 4)
     want = set() if args.headline_only or args.extras == "none" else (
-        {"gf4", "q8", "q4k", "q6k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
+        {"gf4", "q8", "q4k", "q6k", "codecs", "prefill", "stack"} if args.extras == "all"
+        else set(args.extras.split(",")))
     if "gf4" in want:
         for nb in (2, 4, 8):
             xb = b.normal((nb, k))
@@ -423,6 +445,8 @@ def main() -> int:
         del down, head
     if "q6k" in want:
         extra.update(bench_q6k_head(b, rt, torch))
+    if "codecs" in want:
+        extra.update(bench_codecs(b, rt, torch, args.steps // 4, args.warmup // 2))
     if "prefill" in want:
         extra.update(bench_prefill(b, rt, torch))
     if "stack" in want:
