@@ -76,6 +76,37 @@ typedef struct {
     uint32_t reserved;
 } qw35_hip_weight;
 
+/* GGUF v3 reader over a host image of a model file (e.g. an mmap): the
+ * reference loader's parse_mapping (qw35-server/src/loader/tensors.rs:23-121):
+ * GGUF magic, version 3 only, metadata walked and skipped
+ * (loader/metadata.rs:206-288) except general.alignment (u32; 0 keeps 32),
+ * 1..8 dimensions, byte sizes by tensor_nbytes (tensors.rs:123-172) for
+ * every GGUF type the reference knows, data section at the aligned end of the
+ * tensor infos, every tensor inside the image.  *n_tensors = tensor count;
+ * out[0 .. min(cap, count)) are filled as bridge.rs:279-290 fills
+ * qw35_metal_tensor_desc (dims padded with 1, n_dims the true count, name
+ * pointing into model_map, abs_offset from the image start); out may be NULL
+ * with cap 0 to query the count.  *data_offset (nullable) = data section. */
+int qw35_hip_gguf_parse(const void *model_map, uint64_t model_size, qw35_hip_tensor_desc *out, uint32_t cap,
+                        uint32_t *n_tensors, uint64_t *data_offset, char *err, uintptr_t err_len);
+
+/* Device tensor store: replaces Qw35TensorStore (Qw35TensorStore.m:58-153),
+ * which wraps the host mmap in Metal buffers.  HBM is not host memory, so the
+ * image's bytes 0 .. end of the last tensor are copied once (synchronously)
+ * into one device allocation, the only device memory the library itself
+ * allocates; descs (e.g. from qw35_hip_gguf_parse) are checked to lie inside
+ * model_size and copied with their names, so the host image may be unmapped
+ * afterwards.  qw35_hip_store_weight gives the weight view (as
+ * qw35_hip_weight_view) of the tensor named name[0 .. name_len).  Destroy
+ * after the last kernel that reads the store has completed. */
+void *qw35_hip_store_create(const void *model_map, uint64_t model_size, const qw35_hip_tensor_desc *descs,
+                            uint32_t count, char *err, uintptr_t err_len);
+const void *qw35_hip_store_device_base(const void *store);
+uint64_t qw35_hip_store_bytes(const void *store);
+int qw35_hip_store_weight(const void *store, const char *name, uintptr_t name_len, qw35_hip_weight *out, char *err,
+                          uintptr_t err_len);
+void qw35_hip_store_destroy(void *store);
+
 /* 1 if a HIP device is present.  Replaces qw35_metal_has_device (Qw35FFI.h:18-19). */
 int qw35_hip_has_device(void);
 

@@ -74,6 +74,18 @@ class PlanOp(C.Structure):
 
 # name -> (restype, argtypes); every symbol declared in include/qw35_hip.h.
 PROTOTYPES: dict[str, tuple] = {
+    "qw35_hip_gguf_parse": (
+        C.c_int,
+        [C.c_void_p, C.c_uint64, C.POINTER(TensorDesc), C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+         C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_store_create": (
+        C.c_void_p, [C.c_void_p, C.c_uint64, C.POINTER(TensorDesc), C.c_uint32, C.c_char_p, C.c_size_t]),
+    "qw35_hip_store_device_base": (C.c_void_p, [C.c_void_p]),
+    "qw35_hip_store_bytes": (C.c_uint64, [C.c_void_p]),
+    "qw35_hip_store_weight": (
+        C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t, C.POINTER(Weight), C.c_char_p, C.c_size_t]),
+    "qw35_hip_store_destroy": (None, [C.c_void_p]),
     "qw35_hip_has_device": (C.c_int, []),
     "qw35_hip_weight_view": (C.c_int, [C.POINTER(TensorDesc), C.c_void_p, C.POINTER(Weight), C.c_char_p, C.c_size_t]),
     "qw35_hip_decode_matvec": (

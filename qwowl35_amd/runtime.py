@@ -50,8 +50,9 @@ def row_bytes(type_id: int, k: int) -> int:
 class HipWeight:
     """A weight tensor in HBM plus its C-ABI view (``qw35_hip_weight``)."""
 
-    storage: torch.Tensor  # uint8 device tensor holding the raw GGUF bytes
+    storage: torch.Tensor | None  # uint8 device tensor holding the raw GGUF bytes (None: owned by `owner`)
     view: _ffi.Weight
+    owner: object = None  # keeps a TensorStore alive while its weights are in use
 
     @property
     def type_id(self) -> int:
@@ -105,6 +106,92 @@ class HipWeight:
         w = _ffi.Weight()
         _ffi.call("qw35_hip_weight_view", C.byref(desc), C.c_void_p(storage.data_ptr()), C.byref(w))
         return cls(storage, w)
+
+
+def _device_of(w: HipWeight) -> torch.device:
+    if w.storage is not None:
+        return w.storage.device
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+@dataclass
+class GgufTensor:
+    """One tensor info of a GGUF image (``qw35_hip_gguf_parse``)."""
+
+    name: str
+    dims: tuple
+    type_id: int
+    abs_offset: int
+    bytes: int
+    elements: int
+
+
+def _image_ptr(image) -> tuple[C.c_void_p, int, object]:
+    """(pointer, size, keep-alive) of a host byte image (bytes, bytearray, mmap, numpy uint8)."""
+    import numpy as np
+
+    arr = np.frombuffer(image, dtype=np.uint8) if not isinstance(image, np.ndarray) else image.reshape(-1)
+    if arr.dtype != np.uint8 or not arr.flags.c_contiguous:
+        raise Qw35Error("GGUF image must be contiguous bytes")
+    return C.c_void_p(arr.ctypes.data), int(arr.size), arr
+
+
+def gguf_parse(image) -> tuple[list[GgufTensor], int, list]:
+    """Parse a GGUF v3 image (host bytes).  Returns (tensors, data section
+    offset, the raw ``TensorDesc`` array whose names point into ``image``)."""
+    ptr, size, keep = _image_ptr(image)
+    n = C.c_uint32(0)
+    off = C.c_uint64(0)
+    _ffi.call("qw35_hip_gguf_parse", ptr, size, None, 0, C.byref(n), C.byref(off))
+    descs = (_ffi.TensorDesc * max(1, n.value))()
+    _ffi.call("qw35_hip_gguf_parse", ptr, size, descs, n.value, C.byref(n), C.byref(off))
+    out = []
+    for i in range(n.value):
+        d = descs[i]
+        name = C.string_at(d.name, d.name_len).decode("utf-8", errors="replace") if d.name_len else ""
+        out.append(GgufTensor(name, tuple(int(d.dims[j]) for j in range(min(4, d.n_dims))), int(d.type_id),
+                              int(d.abs_offset), int(d.bytes), int(d.elements)))
+    return out, int(off.value), (descs, n.value, keep)
+
+
+class TensorStore:
+    """GGUF tensors resident in HBM (``qw35_hip_store_*``, the counterpart of
+    the reference's Qw35TensorStore): the image is parsed, copied to the device
+    once, and ``weight(name)`` returns a ``HipWeight`` view."""
+
+    def __init__(self, image):
+        self.tensors, self.data_offset, (descs, n, keep) = gguf_parse(image)
+        ptr, size, _ = _image_ptr(keep)
+        self._h = _ffi.call("qw35_hip_store_create", ptr, size, descs, n)
+        self.by_name = {t.name: t for t in self.tensors}
+
+    @classmethod
+    def from_file(cls, path) -> "TensorStore":
+        import numpy as np
+
+        return cls(np.memmap(path, dtype=np.uint8, mode="r"))
+
+    def weight(self, name: str) -> HipWeight:
+        w = _ffi.Weight()
+        raw = name.encode()
+        _ffi.call("qw35_hip_store_weight", C.c_void_p(self._h), raw, len(raw), C.byref(w))
+        return HipWeight(None, w, owner=self)
+
+    @property
+    def device_bytes(self) -> int:
+        return int(_ffi.load().qw35_hip_store_bytes(C.c_void_p(self._h)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            torch.cuda.synchronize()
+            _ffi.load().qw35_hip_store_destroy(C.c_void_p(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def _ptr(t: torch.Tensor | None) -> C.c_void_p:
@@ -238,7 +325,7 @@ def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None,
 def prefill_image(w: HipWeight, stream=None) -> HipWeight:
     """fp16_rne of the dequantised weight as a new F16 ``HipWeight``
     (``qw35_hip_dequantize_f16``), the operand of ``matmul_prefill``."""
-    dst = torch.empty(w.rows * w.k * 2, dtype=torch.uint8, device=w.storage.device)
+    dst = torch.empty(w.rows * w.k * 2, dtype=torch.uint8, device=_device_of(w))
     _ffi.call("qw35_hip_dequantize_f16", C.byref(w.view), _ptr(dst), _stream(stream))
     return HipWeight.from_device(dst, TYPE_F16, w.rows, w.k)
 
@@ -251,7 +338,7 @@ def dequantize(w: HipWeight, row_ids: torch.Tensor | None = None, stream=None) -
         n = int(row_ids.numel())
     else:
         n = w.rows
-    dst = torch.empty((n, w.k), dtype=torch.float32, device=w.storage.device)
+    dst = torch.empty((n, w.k), dtype=torch.float32, device=_device_of(w))
     _ffi.call("qw35_hip_dequantize", C.byref(w.view), _ptr(row_ids), n, _ptr(dst), _stream(stream))
     return dst
 
