@@ -11,8 +11,8 @@
  * Pointers marked "device" are HBM addresses (hipMalloc'd or offsets into an
  * uploaded model image).  `stream` is a hipStream_t (NULL = default stream).
  * Calls on one stream are ordered; the library keeps no global mutable state
- * except its plans, which are single-threaded objects (like MetalRuntime,
- * `Send` but not `Sync`, qw35-server/src/metal/bridge.rs:257).
+ * except its plans and tensor stores, which are single-threaded objects (like
+ * MetalRuntime, `Send` but not `Sync`, qw35-server/src/metal/bridge.rs:257).
  *
  * Weight formats are the reference's raw GGUF tensor bytes (no repacking):
  *   type 100  GF4   8 elems / 4 B   (tools/gguf_custom_types.py:26-30)
