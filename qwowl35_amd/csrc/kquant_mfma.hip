@@ -42,7 +42,8 @@
 // (v_alignbyte).  Its 16 sub-blocks of 16 weights each have an int8 scale, so
 // the contraction runs on v_mfma_f32_16x16x16_f16, one MFMA per sub-block:
 //   B: the 6-bit code (ql nibble | qh 2 bits << 4) -> exact fp16 q - 32;
-//   y += d * sc_s * sum (q - 32) x.
+//   y += d * sum_s sc_s * sum (q - 32) x  (sc_s applied in fp32 per sub-block,
+//   four independent MFMAs before their epilogues, d once per chunk).
 //
 // Greedy head (qw35_output_q6_k_argmax_partials_16row_f32 +
 // qw35_output_argmax_reduce_partials_f32, qw35_output.metal:2-182): with
@@ -107,7 +108,10 @@ template <>
 struct Fmt<kFmtQ6K> {
     static constexpr int kChunkBytes = 210;  // one super-block = 256 columns
     static constexpr int kSegs = 14;         // aligned segments covering bytes [210c, 210c + 210)
-    static constexpr int kStride = 240;
+    // No pad (2-way bank conflicts on the transposed reads) so that two 16-wave
+    // workgroups fit a CU's LDS; the 2-byte realignment of d may read 4 bytes
+    // past a row, still inside the wave's block (the activation buffer follows).
+    static constexpr int kStride = 224;
     static constexpr int kTypeId = 14;
 };
 
@@ -469,36 +473,58 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                             acc[t][m][1] = __builtin_fmaf(inv_sc[1] * kFourThirds, dd[2] + dd[3], acc[t][m][1]);
                     } else if constexpr (FMT == kFmtQ6K) {
                         // The super-block starts `off` bytes into the row buffer
-                        // (even); words are read 4-aligned and realigned by sh.
+                        // (even, wave-uniform); words are read 4-aligned and, for the
+                        // chunks at 2 mod 4, realigned by two bytes.
                         const int off = ((wave * CPW + c) * 210) & 15;
-                        const int sh = off & 3;
                         const uint8_t* sb = wrow + (off & ~3);
-                        auto ld = [&](int o) {
-                            const uint32_t* p = reinterpret_cast<const uint32_t*>(sb + o);
-                            return __builtin_amdgcn_alignbyte(p[1], p[0], sh);
+                        const _Float16* abase = a_live ? arow + 4 * kq : arow;  // arow: the zero row when !a_live
+                        const int astep = a_live ? 16 : 0;
+                        auto q6k_chunk = [&](auto ALIGNED) {
+                            auto ld = [&](int o) {
+                                const uint32_t* p = reinterpret_cast<const uint32_t*>(sb + o);
+                                if constexpr (decltype(ALIGNED)::value) return p[0];
+                                else return __builtin_amdgcn_alignbyte(p[1], p[0], 2);
+                            };
+                            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(ld(208) & 0xFFFFu));
+                            uint32_t scw[4];
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) scw[q] = ld(192 + 4 * q);
+                            // sum_s sc_s * sum (q - 32) x in fp32; d and the inverse
+                            // activation scale once per chunk.
+                            float cs0 = 0.0f, cs1 = 0.0f;
+#pragma unroll
+                            for (int s4 = 0; s4 < 16; s4 += 4) {
+                                float4_t dd[4];
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const int sbk = s4 + u;
+                                    const int h = sbk >> 3, g = (sbk & 7) >> 1, p = sbk & 1;
+                                    const uint32_t qlw = ld(64 * h + 32 * (g & 1) + 16 * p + 4 * kq);
+                                    const uint32_t qhw = ld(128 + 32 * h + 16 * p + 4 * kq);
+                                    const uint32_t nib = ((g >> 1) ? (qlw >> 4) : qlw) & 0x0F0F0F0Fu;
+                                    const uint32_t qv = nib | (((qhw >> (2 * g)) & 0x03030303u) << 4);
+                                    uint32_t b0, b1;
+                                    u4x4_to_h(qv, bias, b0, b1);
+                                    const half4_t bop = __builtin_bit_cast(half4_t, uint2_t_{b0, b1});
+                                    const half4_t aop = *reinterpret_cast<const half4_t*>(abase + astep * sbk);
+                                    dd[u] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, bop, float4_t{0.f, 0.f, 0.f, 0.f},
+                                                                                0, 0, 0);
+                                }
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const int sbk = s4 + u;
+                                    const float scf = (float)(int)(int8_t)((scw[sbk >> 2] >> (8 * (sbk & 3))) & 0xFFu);
+                                    cs0 = __builtin_fmaf(scf, dd[u][0] + dd[u][1], cs0);
+                                    if constexpr (NB > 1) cs1 = __builtin_fmaf(scf, dd[u][2] + dd[u][3], cs1);
+                                }
+                            }
+                            acc[t][m][0] = __builtin_fmaf(d * inv_sc[0], cs0, acc[t][m][0]);
+                            if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(d * inv_sc[1], cs1, acc[t][m][1]);
                         };
-                        const float d =
-                            (float)__builtin_bit_cast(_Float16, (uint16_t)(ld(208) & 0xFFFFu));
-                        uint32_t scw[4];
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) scw[q] = ld(192 + 4 * q);
-#pragma unroll
-                        for (int sbk = 0; sbk < 16; ++sbk) {
-                            const int h = sbk >> 3, g = (sbk & 7) >> 1, p = sbk & 1;
-                            const uint32_t qlw = ld(64 * h + 32 * (g & 1) + 16 * p + 4 * kq);
-                            const uint32_t qhw = ld(128 + 32 * h + 16 * p + 4 * kq);
-                            const uint32_t nib = ((g >> 1) ? (qlw >> 4) : qlw) & 0x0F0F0F0Fu;
-                            const uint32_t qv = nib | (((qhw >> (2 * g)) & 0x03030303u) << 4);
-                            uint32_t b0, b1;
-                            u4x4_to_h(qv, bias, b0, b1);
-                            const half4_t bop = __builtin_bit_cast(half4_t, uint2_t_{b0, b1});
-                            const half4_t aop = *reinterpret_cast<const half4_t*>(arow + (a_live ? 16 * sbk + 4 * kq : 0));
-                            const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                                aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                            const float dsc = d * (float)(int)(int8_t)((scw[sbk >> 2] >> (8 * (sbk & 3))) & 0xFFu);
-                            acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
-                            acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
-                        }
+                        if ((off & 3) == 0)
+                            q6k_chunk(std::true_type{});
+                        else
+                            q6k_chunk(std::false_type{});
                     } else {  // Q4_K, Q5_K
                         const uint4_t hd = *reinterpret_cast<const uint4_t*>(wrow);
                         const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)hd.x);
