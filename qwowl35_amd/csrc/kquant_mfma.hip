@@ -786,8 +786,10 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
         for (int s = 0; s < a.n_seg; ++s) total_rows += a.seg_rows[s];
     }
     KqPlan p = plan_kq(FMT, total_rows, a.k, NB);
+    // Fused gate/up holds two matrices' loads per tile: more than two row tiles
+    // per workgroup spill registers, so those take the one-tile shape below.
 #define QW35_KQ_PLAN(RT, KS, CPW, P)                                                             \
-    if constexpr (kq_fits<FMT, NB, RT, P, SWIGLU>()) {                                             \
+    if constexpr (kq_fits<FMT, NB, RT, P, SWIGLU>() && (!SWIGLU || RT <= 2)) {                     \
         if (p.rt == RT && p.ks == KS && p.cpw == CPW && p.p == P)                                  \
             return kq_launch_cfg<FMT, NB, RT, KS, CPW, P, SWIGLU>(a, stream);                      \
     }
@@ -814,7 +816,7 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
             QW35_KQ_PLAN(1, 16, 3, 2)
         }
     }
-    // over the load budget (fused gate/up at batch 8): one tile per workgroup
+    // over the load budget or the register budget (fused gate/up): one tile per workgroup
     if (p.rt > 1) return kq_launch_cfg<FMT, NB, 1, 8, 2, (kq_fits<FMT, NB, 1, 2, SWIGLU>() ? 2 : 1), SWIGLU>(a, stream);
 #undef QW35_KQ_PLAN
     return hipErrorInvalidValue;

@@ -177,3 +177,25 @@ def test_gemv_large_ragged_kquant(cuda, name, nb):
     y = rt.decode_matvec(w, x).double()
     want = rt.dequantize(w).double() @ x.double().T
     assert om.rel_l2(y.cpu().numpy(), want.T.cpu().numpy()) <= GEMV_REL_L2
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "gf2"])
+def test_swiglu_tall_batch8(cuda, name):
+    """Fused gate/up at batch 8 on 8208 rows (the tall-matrix launch shapes,
+    ragged last tile), weights made on the GPU, against fp64 on the library's
+    dequantised weights."""
+    import torch
+
+    rt = _rt()
+    type_id = TYPES[name]
+    rows, k = 8208, 4096
+    g = torch.Generator(device=cuda)
+    g.manual_seed(3)
+    wg = rt.quantize_weight(torch.randn((rows, k), generator=g, device=cuda) * 0.02, type_id)
+    wu = rt.quantize_weight(torch.randn((rows, k), generator=g, device=cuda) * 0.02, type_id)
+    x = torch.randn((8, k), generator=g, device=cuda)
+    y = rt.ffn_gate_up_swiglu(wg, wu, x).double()
+    gate = rt.dequantize(wg).double() @ x.double().T
+    up = rt.dequantize(wu).double() @ x.double().T
+    want = (gate / (1 + torch.exp(-gate)) * up).T
+    assert om.rel_l2(y.cpu().numpy(), want.cpu().numpy()) <= GEMV_REL_L2

@@ -132,13 +132,14 @@ def test_q6k_rejects_unaligned_rows_and_swiglu(cuda):
 def _weight(name, rows, k, seed):
     if name == "q6_k":
         return _q6k(rows, k, seed)
-    return make_weight({"q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "gf4": om.TYPE_GF4}[name], rows, k, seed=seed)
+    return make_weight(_TYPE[name], rows, k, seed=seed)
 
 
-_TYPE = {"q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "q6_k": om.TYPE_Q6_K, "gf4": om.TYPE_GF4}
+_TYPE = {"q8_0": om.TYPE_Q8_0, "q4_k": om.TYPE_Q4_K, "q5_k": om.TYPE_Q5_K, "q6_k": om.TYPE_Q6_K,
+         "gf4": om.TYPE_GF4, "gf2": om.TYPE_GF2}
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "q6_k", "gf2"])
 @pytest.mark.parametrize("nb", [1, 2, 5, 8])
 @pytest.mark.parametrize("rows", [1000, 4133])
 def test_argmax_equals_rule_on_matvec_logits(cuda, name, nb, rows):
