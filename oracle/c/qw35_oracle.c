@@ -11,6 +11,10 @@
  *   Q6_K w = d * sc[e/16] * (q - 32), q = ql nibble | qh bits << 4
  *                                                              qw35_matvec.metal:458-542 (bit extraction),
  *                                                              qw35_types.metal:17-22 (block)
+ *   Q5_K w = d * sc_j * q - dmin * m_j, q = nibble | bit j of qh[e % 32] << 4
+ *                                                              qw35_matvec.metal:40-62, qw35_types.metal:9-15
+ *   GF2  w = (q * fl(2/3) - 1) * s, 2-bit q, 80-byte super-blocks of 16 words + 16 scale bytes
+ *                                                              qw35_gf2.metal:1-50
  */
 #include <math.h>
 #include <stddef.h>
@@ -103,6 +107,48 @@ void qw35o_q6_k_dequant(const uint8_t *raw, size_t n_blocks, float *out) {
                     const int e = 128 * ip + 32 * j + l;
                     out[256 * b + e] = (d * (float)sc[e / 16]) * (float)(q[j] - 32);
                 }
+            }
+        }
+    }
+}
+
+/* Q5_K: the Q4_K block with 32 bytes of fifth code bits between the scales
+ * and the nibbles (d, dmin, scales[12], qh[32], qs[128] = 176 bytes). */
+void qw35o_q5_k_dequant(const uint8_t *raw, size_t n_blocks, float *out) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t *blk = raw + 176 * b;
+        const float d = half_bits_to_float(rd16(blk));
+        const float dmin = half_bits_to_float(rd16(blk + 2));
+        const uint8_t *scales = blk + 4;
+        const uint8_t *qh = blk + 16;
+        const uint8_t *qs = blk + 48;
+        for (int e = 0; e < 256; ++e) {
+            const int j = e / 32;
+            int sc, m;
+            scale_min_k4(j, scales, &sc, &m);
+            const uint8_t byte = qs[(j / 2) * 32 + (e % 32)];
+            const int q = ((j & 1) ? (byte >> 4) : (byte & 0x0F)) | (((qh[e % 32] >> j) & 1) << 4);
+            const float dsc = d * (float)sc;
+            const float mm = dmin * (float)m;
+            out[256 * b + e] = dsc * (float)q - mm;
+        }
+    }
+}
+
+/* GF2: per 256 columns, 16 little-endian code words (code i of word w is
+ * column 16w + i, bits 2i..2i+1) then their 16 e5m2 scale bytes. */
+void qw35o_gf2_dequant(const uint8_t *raw, size_t n_blocks, float *out) {
+    const float two_thirds = 2.0f / 3.0f;
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t *blk = raw + 80 * b;
+        for (int w = 0; w < 16; ++w) {
+            const uint32_t word = (uint32_t)blk[4 * w] | ((uint32_t)blk[4 * w + 1] << 8) |
+                                  ((uint32_t)blk[4 * w + 2] << 16) | ((uint32_t)blk[4 * w + 3] << 24);
+            const float s = half_bits_to_float((uint16_t)(blk[64 + w] << 8));
+            for (int i = 0; i < 16; ++i) {
+                const float q = (float)((word >> (2 * i)) & 3u);
+                const float level = q * two_thirds - 1.0f;
+                out[256 * b + 16 * w + i] = level * s;
             }
         }
     }

@@ -19,7 +19,8 @@ def lib() -> C.CDLL:
         if not LIB.exists():
             raise FileNotFoundError(f"{LIB} missing; run `make -C oracle`")
         _lib = C.CDLL(str(LIB))
-        for name in ("qw35o_gf4_dequant", "qw35o_q8_0_dequant", "qw35o_q4_k_dequant", "qw35o_q6_k_dequant"):
+        for name in ("qw35o_gf4_dequant", "qw35o_q8_0_dequant", "qw35o_q4_k_dequant", "qw35o_q6_k_dequant",
+                     "qw35o_q5_k_dequant", "qw35o_gf2_dequant"):
             getattr(_lib, name).argtypes = [C.c_void_p, C.c_size_t, C.c_void_p]
             getattr(_lib, name).restype = None
         _lib.qw35o_matvec_f64.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p]
@@ -38,6 +39,10 @@ def dequant(type_id: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
         lib().qw35o_q4_k_dequant(raw.ctypes.data, rows * k // 256, out.ctypes.data)
     elif type_id == 14:
         lib().qw35o_q6_k_dequant(raw.ctypes.data, rows * k // 256, out.ctypes.data)
+    elif type_id == 13:
+        lib().qw35o_q5_k_dequant(raw.ctypes.data, rows * k // 256, out.ctypes.data)
+    elif type_id == 101:
+        lib().qw35o_gf2_dequant(raw.ctypes.data, rows * k // 256, out.ctypes.data)
     else:
         raise ValueError(type_id)
     return out

@@ -23,7 +23,7 @@ def _same_bits(a, b):
     return bool(np.all((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))))
 
 
-@pytest.mark.parametrize("type_id", [om.TYPE_GF4, om.TYPE_Q8_0, om.TYPE_Q4_K])
+@pytest.mark.parametrize("type_id", [om.TYPE_GF4, om.TYPE_GF2, om.TYPE_Q8_0, om.TYPE_Q4_K, om.TYPE_Q5_K])
 def test_c_twin_dequant(type_id):
     raw, deq = make_weight(type_id, 24, 1024, seed=type_id)
     assert _same_bits(c_oracle.dequant(type_id, raw, 24, 1024), deq)
@@ -40,6 +40,16 @@ def test_c_twin_q4_k_random_bytes():
     raw.reshape(8, 4, 144)[..., 1] &= np.uint8(0xFB)
     raw.reshape(8, 4, 144)[..., 3] &= np.uint8(0xFB)
     assert _same_bits(c_oracle.dequant(om.TYPE_Q4_K, raw, 8, 1024), om.dequant(om.TYPE_Q4_K, raw, 8, 1024))
+
+
+def test_c_twin_q5_k_and_gf2_random_bytes():
+    rng = np.random.default_rng(5)
+    raw = rng.integers(0, 256, (8, 176 * 4), dtype=np.uint8)
+    raw.reshape(8, 4, 176)[..., 1] &= np.uint8(0xFB)  # finite d and dmin
+    raw.reshape(8, 4, 176)[..., 3] &= np.uint8(0xFB)
+    assert _same_bits(c_oracle.dequant(om.TYPE_Q5_K, raw, 8, 1024), om.dequant(om.TYPE_Q5_K, raw, 8, 1024))
+    g = rng.integers(0, 256, (8, 80 * 4), dtype=np.uint8)  # every scale byte, finite or not
+    assert _same_bits(c_oracle.dequant(om.TYPE_GF2, g, 8, 1024), om.dequant(om.TYPE_GF2, g, 8, 1024))
 
 
 def test_c_twin_matvec():
