@@ -816,6 +816,12 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
             QW35_KQ_PLAN(1, 16, 3, 2)
         }
     }
+    // Fused gate/up planned with more than two tiles: three tiles with one
+    // chunk in flight (half the load registers of the planned shape, so no
+    // spills); 12288 rows are then exactly 256 workgroups, one per CU.
+    if constexpr (SWIGLU && NB >= 4 && kq_fits<FMT, NB, 3, 1, SWIGLU>()) {
+        if (p.rt > 2) return kq_launch_cfg<FMT, NB, 3, 8, 2, 1, SWIGLU>(a, stream);
+    }
     // over the load budget or the register budget (fused gate/up): one tile per workgroup
     if (p.rt > 1) return kq_launch_cfg<FMT, NB, 1, 8, 2, (kq_fits<FMT, NB, 1, 2, SWIGLU>() ? 2 : 1), SWIGLU>(a, stream);
 #undef QW35_KQ_PLAN
