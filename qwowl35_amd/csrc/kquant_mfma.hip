@@ -723,7 +723,8 @@ struct KqPlan {
 // e.g. q8_0 12352 x 4096 b8 {4, 8, 2, 1} 21.5 us ({3, 8, 2, 2} 35.9 us);
 // q8_0 4096 x 4096 b1 {1, 16, 1, 1} 6.2 us ({1, 8, 2, 2} 7.2 us); Q4_K
 // 248320 x 4096 b1 {2, 16, 1, 1} 128 us ({1, 8, 2, 2} 156 us), b8
-// {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us).
+// {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us); batch-1 heads: Q4_K {3, 8, 2, 2}
+// 134-136 us ({2, 16, 1, 1} 142 us), Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us).
 KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
@@ -738,7 +739,10 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
             }
             return fmt == kFmtQ8 ? KqPlan{1, 8, 2, 1} : KqPlan{1, 8, 2, 2};
         }
-        if (fmt != kFmtQ8 && fmt != kFmtGF4 && tiles >= 4096) return {2, 16, 1, 1};
+        if (tiles >= 4096) {  // LM-head sized
+            if (fmt == kFmtQ4K) return {3, 8, 2, 2};
+            if (fmt == kFmtQ5K || fmt == kFmtGF2) return {2, 16, 1, 1};
+        }
         if (fmt == kFmtQ8 && tiles < 512) return {1, 16, 1, 1};
         return {1, 8, 2, 2};
     }
