@@ -348,6 +348,18 @@ def cpu_baseline_gf4(rows: int, k: int, seed: int, reps: int):
     return float(np.median(t_dq)), float(np.median(t_mv)), blas
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (the first 'model name' of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -426,6 +438,35 @@ def main() -> int:
         set_bytes = sum(gemv_bytes(rt.TYPE_Q8_0, r, kk, 1, rt) for r, kk in shapes)
         extra["q8_0_layer_set_b1"] = {"us_per_set": round(per_set_ms * 1e3, 3), "bytes": set_bytes,
                                       "GB/s": round(set_bytes / per_set_ms / 1e6, 1)}
+        # The same sets as one recorded decode plan, each projection reading
+        # the input it has in a layer: q/k/v share the attention input and
+        # gate/up the FFN input, so each group is one launch (4 per set).
+        xin = {name: b.normal((1, kk)) for name, kk in
+               (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 12288))}
+        role = ["attn", "attn", "attn", "o", "ffn", "ffn", "down"]
+        ys = [torch.zeros((1, r), dtype=torch.float32, device=b.dev) for r, _ in shapes]
+        plan = rt.DecodePlan()
+        for st in sets:
+            for w, r, y in zip(st, role, ys):
+                plan.matvec(w, xin[r], y)
+        plan.record()
+        with torch.cuda.stream(b.stream):
+            for _ in range(3):
+                plan.launch(stream=b.stream)
+        torch.cuda.synchronize()
+        reps = max(20, args.steps // 40)
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(b.stream):
+            ev0.record(b.stream)
+            for _ in range(reps):
+                plan.launch(stream=b.stream)
+            ev1.record(b.stream)
+        torch.cuda.synchronize()
+        plan_set_ms = ev0.elapsed_time(ev1) / reps / len(sets)
+        extra["q8_0_layer_set_b1_plan"] = {"us_per_set": round(plan_set_ms * 1e3, 3), "merged": "q/k/v, o, gate/up, down",
+                                           "GB/s": round(set_bytes / plan_set_ms / 1e6, 1)}
+        plan.close()
         del sets
     if "q4k" in want:
         # config 3: Q4_K down 4096x12288 (24 copies) and LM head 248320x4096, batch 1 and 8
@@ -464,7 +505,7 @@ def main() -> int:
             "kind": "port",
             "sample": f"numpy oracle on the host: GF4 dequant of the 12288x4096 b1 weight (1 thread, "
                       f"{t_dq * 1e3:.1f} ms) + fp32 W@x ({blas} BLAS threads, {t_mv * 1e3:.2f} ms), "
-                      f"median of {args.cpu_reps}",
+                      f"median of {args.cpu_reps}; {cpu_model()}, {os.cpu_count()} logical CPUs visible",
         }
     out = {
         "metric": "GF4 b1 matvec HBM GB/s (12288x4096)",
