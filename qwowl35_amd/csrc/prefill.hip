@@ -752,6 +752,12 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w) {
             if (blocks >= cus) break;  // more splits only add partial sums
         }
     }
+    // One block per CU or fewer: the 8-wave form of the same tile hides more
+    // latency.  Same-box A/B, GF4: 12288x4096 M=128 {64,2,2} 37.7 -> 35.8 us,
+    // M=512 {128,2,1} 76.4 -> 71.2 us; 4096x12288 M=512 {128,2,4} 75.7 ->
+    // 72.9 us.  At three blocks per CU (M=2048) it was slower, 216 -> 233 us.
+    const long blocks = (long)((m + best.bm - 1) / best.bm) * ((rows + 255) / 256) * best.splits;
+    if (!f16w && best.fn == 2 && best.bm >= 64 && blocks <= cus) best.waves = 8;
     return best;
 }
 
@@ -823,9 +829,15 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
                 default: return hipErrorInvalidValue;
             }
         } else switch (cfg.bm * 10 + cfg.fn) {
-            case 1282: e = launch_f16_tile<128, 4, 2, 2>(p, kf32, stream); break;
+            case 1282:
+                e = cfg.waves == 8 ? launch_f16_tile<128, 8, 1, 2>(p, kf32, stream)
+                                   : launch_f16_tile<128, 4, 2, 2>(p, kf32, stream);
+                break;
             case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
-            case 642: e = launch_f16_tile<64, 4, 2, 2>(p, kf32, stream); break;
+            case 642:
+                e = cfg.waves == 8 ? launch_f16_tile<64, 8, 1, 2>(p, kf32, stream)
+                                   : launch_f16_tile<64, 4, 2, 2>(p, kf32, stream);
+                break;
             case 644: e = launch_f16_tile<64, 4, 4, 2>(p, kf32, stream); break;
             case 322: e = launch_f16_tile<32, 4, 2, 2>(p, kf32, stream); break;
             default: return hipErrorInvalidValue;

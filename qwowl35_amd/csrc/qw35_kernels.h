@@ -95,6 +95,9 @@ struct PrefillCfg {
     int bm;      // tokens per block: 128, 64 or 32
     int fn;      // 32-row weight tiles per wave (4 waves per block): 2 or 4 (4 needs bm >= 64)
     int splits;  // K splits; k / splits must be a multiple of 256
+    // 8: the same bm x 256 tile on 8 waves of one 32-row weight tile each
+    // (GF4, fn 2 only), two waves per SIMD where a CU gets only one block.
+    int waves = 4;
 };
 PrefillCfg plan_gf4_prefill(int m, int rows, int k);
 size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg);
