@@ -726,7 +726,12 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // F16 weights (2 bytes per weight against GF4's half byte) use FN = 2 only:
 // their four-slot register ring of 16-byte loads is four times GF4's.
 PrefillCfg plan_prefill(int m, int rows, int k, bool f16w) {
-    constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9, kUsPerPartialMB = 0.5;
+    constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9;
+    // K-split partial sums cost less relative to fp16 weight tiles than to GF4
+    // ones: with 0.5 the F16 plan for 8192x4096 M=128 was {64,2,4} 57.1 us,
+    // with 0.35 it is {128,2,8} 47.0 us; the other F16 shapes of the sweep
+    // (4096 / 8192 / 12288 rows, M = 128..2048) keep their plans.
+    const double kUsPerPartialMB = f16w ? 0.35 : 0.5;
     const int cus = num_cus();
     const int chunks = k / 256;
     const double w_bytes = f16w ? 2.0 : 0.5;
