@@ -179,11 +179,12 @@ def test_gemv_large_ragged_kquant(cuda, name, nb):
     assert om.rel_l2(y.cpu().numpy(), want.T.cpu().numpy()) <= GEMV_REL_L2
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "gf2"])
-def test_swiglu_tall_batch8(cuda, name):
-    """Fused gate/up at batch 8 on 8208 rows (the tall-matrix launch shapes,
-    ragged last tile), weights made on the GPU, against fp64 on the library's
-    dequantised weights."""
+@pytest.mark.parametrize("nb", [8, 4])
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "gf2", "gf4"])
+def test_swiglu_tall_batch8(cuda, name, nb):
+    """Fused gate/up at batch 4 and 8 on 8208 rows (the tall-matrix launch
+    shapes: three row tiles per workgroup, ragged last tile), weights made on
+    the GPU, against fp64 on the library's dequantised weights."""
     import torch
 
     rt = _rt()
@@ -193,7 +194,7 @@ def test_swiglu_tall_batch8(cuda, name):
     g.manual_seed(3)
     wg = rt.quantize_weight(torch.randn((rows, k), generator=g, device=cuda) * 0.02, type_id)
     wu = rt.quantize_weight(torch.randn((rows, k), generator=g, device=cuda) * 0.02, type_id)
-    x = torch.randn((8, k), generator=g, device=cuda)
+    x = torch.randn((nb, k), generator=g, device=cuda)
     y = rt.ffn_gate_up_swiglu(wg, wu, x).double()
     gate = rt.dequantize(wg).double() @ x.double().T
     up = rt.dequantize(wu).double() @ x.double().T
