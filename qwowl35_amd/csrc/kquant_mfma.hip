@@ -722,9 +722,9 @@ struct KqPlan {
 // Settings from launch-shape sweeps on MI355X (graph replays, rotated weights),
 // e.g. q8_0 12352 x 4096 b8 {4, 8, 2, 1} 21.5 us ({3, 8, 2, 2} 35.9 us);
 // q8_0 4096 x 4096 b1 {1, 16, 1, 1} 6.2 us ({1, 8, 2, 2} 7.2 us); Q4_K
-// 248320 x 4096 b1 {2, 16, 1, 1} 128 us ({1, 8, 2, 2} 156 us), b8
-// {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us); batch-1 heads: Q4_K {3, 8, 2, 2}
-// 134-136 us ({2, 16, 1, 1} 142 us), Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us).
+// 248320 x 4096 b8 {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us).  Batch-1 heads,
+// one sweep on one box: Q4_K {3, 8, 2, 2} 134-136 us ({2, 16, 1, 1} 142 us),
+// Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us).
 KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
