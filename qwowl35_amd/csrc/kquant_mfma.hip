@@ -733,7 +733,13 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     if (chunks <= 16) {
         if (nb >= 4) {
             if (tiles >= 512) {
-                if (fmt != kFmtQ8 && fmt != kFmtGF4) return tiles >= 4096 ? KqPlan{2, 4, 4, 2} : KqPlan{4, 8, 2, 1};
+                if (fmt != kFmtQ8 && fmt != kFmtGF4) {
+                    // LM-head sized: at batch 8 four tiles per 4-wave workgroup
+                    // (Q4_K head b8 199 us, Q6_K 278 us; {2, 4, 4, 2} 234 / 322 us)
+                    if (tiles >= 4096)
+                        return nb >= 8 && (fmt == kFmtQ4K || fmt == kFmtQ6K) ? KqPlan{4, 4, 4, 1} : KqPlan{2, 4, 4, 2};
+                    return {4, 8, 2, 1};
+                }
                 if (fmt == kFmtQ8) return {4, 8, 2, 1};
                 return {3, 8, 2, 2};
             }
@@ -810,6 +816,9 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
         } else {
             QW35_KQ_PLAN(1, 16, 1, 1)
         }
+    }
+    if constexpr (NB == 8 && (FMT == kFmtQ4K || FMT == kFmtQ6K)) {
+        QW35_KQ_PLAN(4, 4, 4, 1)
     }
     if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtQ6K || FMT == kFmtGF2) {
         if constexpr (NB >= 4) {
