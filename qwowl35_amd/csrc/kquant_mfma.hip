@@ -754,6 +754,8 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     }
     if (chunks <= 32) return {1, 8, 4, 2};
     if (fmt != kFmtQ8 && fmt != kFmtGF4) return nb >= 4 ? KqPlan{1, 12, 4, 2} : KqPlan{1, 16, 3, 2};
+    // GF4 4096 x 12288 b8: {1, 12, 4, 2} 17.1 us ({1, 8, 6, 2} 17.9 us, two sweeps)
+    if (fmt == kFmtGF4 && nb >= 8) return {1, 12, 4, 2};
     return {1, 8, 6, 2};
 }
 
@@ -819,6 +821,9 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
     }
     if constexpr (NB == 8 && (FMT == kFmtQ4K || FMT == kFmtQ6K)) {
         QW35_KQ_PLAN(4, 4, 4, 1)
+    }
+    if constexpr (NB == 8 && FMT == kFmtGF4) {
+        QW35_KQ_PLAN(1, 12, 4, 2)
     }
     if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtQ6K || FMT == kFmtGF2) {
         if constexpr (NB >= 4) {
