@@ -724,7 +724,8 @@ struct KqPlan {
 // q8_0 4096 x 4096 b1 {1, 16, 1, 1} 6.2 us ({1, 8, 2, 2} 7.2 us); Q4_K
 // 248320 x 4096 b8 {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us).  Batch-1 heads,
 // one sweep on one box: Q4_K {3, 8, 2, 2} 134-136 us ({2, 16, 1, 1} 142 us),
-// Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us).
+// Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us), GF2 {3, 8, 2, 2} 113 us
+// ({2, 16, 1, 1} 119 us); Q5_K keeps {2, 16, 1, 1} 157 us ({3, 8, 2, 2} 160 us).
 KqPlan plan_kq(int fmt, int rows, int k, int nb) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
@@ -735,9 +736,9 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
             if (tiles >= 512) {
                 if (fmt != kFmtQ8 && fmt != kFmtGF4) {
                     // LM-head sized: at batch 8 four tiles per 4-wave workgroup
-                    // (Q4_K head b8 199 us, Q6_K 278 us; {2, 4, 4, 2} 234 / 322 us)
-                    if (tiles >= 4096)
-                        return nb >= 8 && (fmt == kFmtQ4K || fmt == kFmtQ6K) ? KqPlan{4, 4, 4, 1} : KqPlan{2, 4, 4, 2};
+                    // (head b8 Q4_K 199 us, Q6_K 278, Q5_K 249, GF2 176; with
+                    // {2, 4, 4, 2} 234 / 322 / 261 / 210 us)
+                    if (tiles >= 4096) return nb >= 8 ? KqPlan{4, 4, 4, 1} : KqPlan{2, 4, 4, 2};
                     return {4, 8, 2, 1};
                 }
                 if (fmt == kFmtQ8) return {4, 8, 2, 1};
@@ -746,8 +747,8 @@ KqPlan plan_kq(int fmt, int rows, int k, int nb) {
             return fmt == kFmtQ8 ? KqPlan{1, 8, 2, 1} : KqPlan{1, 8, 2, 2};
         }
         if (tiles >= 4096) {  // LM-head sized
-            if (fmt == kFmtQ4K) return {3, 8, 2, 2};
-            if (fmt == kFmtQ5K || fmt == kFmtGF2) return {2, 16, 1, 1};
+            if (fmt == kFmtQ4K || fmt == kFmtGF2) return {3, 8, 2, 2};
+            if (fmt == kFmtQ5K) return {2, 16, 1, 1};
         }
         if (fmt == kFmtQ8 && tiles < 512) return {1, 16, 1, 1};
         return {1, 8, 2, 2};
@@ -819,7 +820,7 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
             QW35_KQ_PLAN(1, 16, 1, 1)
         }
     }
-    if constexpr (NB == 8 && (FMT == kFmtQ4K || FMT == kFmtQ6K)) {
+    if constexpr (NB == 8 && (FMT == kFmtQ4K || FMT == kFmtQ6K || FMT == kFmtQ5K || FMT == kFmtGF2)) {
         QW35_KQ_PLAN(4, 4, 4, 1)
     }
     if constexpr (NB == 8 && FMT == kFmtGF4) {
