@@ -88,20 +88,25 @@ __device__ __forceinline__ uint4_t load_stream16(const void* p) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
-// Power-of-two factor 2^e that brings max_abs to at most 2^14, so that every
-// scaled activation fits fp16 (max 65504) with headroom; 1 for zero input.
+// Power-of-two factor 2^e that brings max_abs into [2^13, 2^14), so that every
+// scaled activation fits fp16 (max 65504) with headroom and the small ones stay
+// clear of fp16 subnormals; 1 for zero, inf or NaN input.  |e| <= 125 covers
+// every finite fp32 maximum down to 2^-111 exactly (smaller maxima land below
+// 2^13, still normal in fp16 down to 2^-139), and keeps 2^(e+1) -- the prefill
+// staging doubles the factor -- and its inverse normal fp32 numbers.
 __device__ __forceinline__ float fp16_range_scale(float max_abs) {
-    if (!(max_abs > 0.0f) || !(max_abs < 3.0e38f)) return 1.0f;
+    if (!(max_abs > 0.0f) || !(max_abs <= 3.4028234663852886e38f)) return 1.0f;
     int e;
     (void)frexpf(max_abs, &e);  // max_abs in [2^(e-1), 2^e)
     int shift = 14 - e;         // max_abs * 2^shift < 2^14
-    if (shift > 24) shift = 24;
-    if (shift < -24) shift = -24;
+    if (shift > 125) shift = 125;
+    if (shift < -125) shift = -125;
     return ldexpf(1.0f, shift);
 }
 
-// 1 / s for s = 2^e, |e| <= 24 (what fp16_range_scale returns): the exponent
-// field is mirrored about 127, so the result is exact.
+// 1 / s for s = 2^e, |e| <= 126 (fp16_range_scale returns |e| <= 125, the
+// prefill staging at most 2^126): the exponent field is mirrored about 127,
+// so the result is exact.
 __device__ __forceinline__ float pow2_inverse(float s) {
     return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, s));
 }

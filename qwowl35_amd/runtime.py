@@ -82,6 +82,8 @@ class HipWeight:
     def upload(cls, raw, type_id: int, rows: int, k: int, device="cuda") -> "HipWeight":
         """Copy raw tensor bytes (numpy / torch, any shape) into HBM and validate."""
         t = torch.as_tensor(raw).reshape(-1).view(torch.uint8)
+        if t.numel() != rows * row_bytes(type_id, k):
+            raise Qw35Error(f"{rows}x{k} type {type_id} takes {rows * row_bytes(type_id, k)} bytes, got {t.numel()}")
         dev = torch.empty(t.numel(), dtype=torch.uint8, device=device)
         dev.copy_(t)
         return cls.from_device(dev, type_id, rows, k)
@@ -103,6 +105,11 @@ class HipWeight:
         desc.abs_offset = offset
         desc.bytes = nbytes if nbytes is not None else rows * row_bytes(type_id, k)
         desc.elements = rows * k
+        have = storage.numel() * storage.element_size()
+        if not storage.is_cuda or not storage.is_contiguous():
+            raise Qw35Error("weight storage must be a contiguous device tensor")
+        if offset < 0 or offset + desc.bytes > have:
+            raise Qw35Error(f"weight bytes [{offset}, {offset + desc.bytes}) exceed the {have}-byte storage")
         w = _ffi.Weight()
         _ffi.call("qw35_hip_weight_view", C.byref(desc), C.c_void_p(storage.data_ptr()), C.byref(w))
         return cls(storage, w)
@@ -207,17 +214,37 @@ def _stream(stream) -> C.c_void_p:
 def _check_act(x: torch.Tensor, k: int, name: str) -> int:
     if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous():
         raise Qw35Error(f"{name} must be a contiguous fp32 device tensor")
-    if x.shape[-1] != k:
-        raise Qw35Error(f"{name} last dim {x.shape[-1]} != k={k}")
-    return 1 if x.dim() == 1 else int(x.shape[0])
+    if x.dim() not in (1, 2) or x.shape[-1] != k:
+        raise Qw35Error(f"{name} must be [k] or [n_batch, k] with k={k}, got {tuple(x.shape)}")
+    nb = 1 if x.dim() == 1 else int(x.shape[0])
+    if not 1 <= nb <= _ffi.MAX_BATCH:
+        raise Qw35Error(f"{name}: n_batch={nb} must be in 1..{_ffi.MAX_BATCH}")
+    return nb
+
+
+def _check_out(dst: torch.Tensor, nb: int, rows: int, x: torch.Tensor, name: str) -> None:
+    """dst must be a contiguous fp32 tensor on x's device holding n_batch * rows values."""
+    if dst.dtype != torch.float32 or not dst.is_cuda or not dst.is_contiguous() or dst.device != x.device:
+        raise Qw35Error(f"{name} must be a contiguous fp32 tensor on {x.device}")
+    if dst.numel() != nb * rows:
+        raise Qw35Error(f"{name} holds {dst.numel()} values, expected n_batch*rows = {nb}*{rows}")
+
+
+def _check_awq(awq: torch.Tensor | None, k: int, x: torch.Tensor, name: str = "awq") -> None:
+    if awq is None:
+        return
+    if awq.dtype != torch.float32 or not awq.is_contiguous() or awq.device != x.device or awq.numel() != k:
+        raise Qw35Error(f"{name} must be a contiguous fp32 tensor of k={k} values on {x.device}")
 
 
 def decode_matvec(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, residual: bool = False,
                   awq: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """``dst (+)= W @ (awq * x)`` for x [k] or [n_batch, k] (n_batch <= 8)."""
     nb = _check_act(x, w.k, "x")
+    _check_awq(awq, w.k, x)
     if dst is None:
         dst = torch.zeros((nb, w.rows) if x.dim() == 2 else (w.rows,), dtype=torch.float32, device=x.device)
+    _check_out(dst, nb, w.rows, x, "dst")
     _ffi.call("qw35_hip_decode_matvec", C.byref(w.view), _ptr(x), _ptr(awq), _ptr(dst), nb, int(bool(residual)),
               _stream(stream))
     return dst
@@ -227,8 +254,10 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
                        awq: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """``dst = silu(gate @ (awq*x)) * (up @ (awq*x))``."""
     nb = _check_act(x, gate.k, "x")
+    _check_awq(awq, gate.k, x)
     if dst is None:
         dst = torch.empty((nb, gate.rows) if x.dim() == 2 else (gate.rows,), dtype=torch.float32, device=x.device)
+    _check_out(dst, nb, gate.rows, x, "dst")
     _ffi.call("qw35_hip_ffn_gate_up_swiglu", C.byref(gate.view), C.byref(up.view), _ptr(x), _ptr(awq), _ptr(dst),
               nb, _stream(stream))
     return dst
@@ -249,6 +278,7 @@ def output_argmax(w: HipWeight, x: torch.Tensor, awq: torch.Tensor | None = None
     the logits.  Returns (tokens [n_batch] int32 holding the uint32 row ids --
     0xFFFFFFFF reads as -1 -- and fp32 logits [n_batch]), written on ``stream``."""
     nb = _check_act(x, w.k, "x")
+    _check_awq(awq, w.k, x)
     need = int(_ffi.load().qw35_hip_output_argmax_workspace_size(C.byref(w.view), nb))
     if need == 0:
         raise Qw35Error("output_argmax: invalid weight or batch")
@@ -386,12 +416,16 @@ class DecodePlan:
     def matvec(self, w: HipWeight, x: torch.Tensor, dst: torch.Tensor, residual: bool = False,
                awq: torch.Tensor | None = None) -> "DecodePlan":
         nb = _check_act(x, w.k, "x")
+        _check_awq(awq, w.k, x)
+        _check_out(dst, nb, w.rows, x, "dst")
         self._add(_ffi.OP_MATVEC, nb, residual, w, None, x, awq, dst)
         return self
 
     def swiglu(self, gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: torch.Tensor,
                awq: torch.Tensor | None = None) -> "DecodePlan":
         nb = _check_act(x, gate.k, "x")
+        _check_awq(awq, gate.k, x)
+        _check_out(dst, nb, gate.rows, x, "dst")
         self._add(_ffi.OP_SWIGLU, nb, False, gate, up, x, awq, dst)
         return self
 

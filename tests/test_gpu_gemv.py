@@ -200,3 +200,37 @@ def test_swiglu_tall_batch8(cuda, name, nb):
     up = rt.dequantize(wu).double() @ x.double().T
     want = (gate / (1 + torch.exp(-gate)) * up).T
     assert om.rel_l2(y.cpu().numpy(), want.cpu().numpy()) <= GEMV_REL_L2
+
+
+def test_entry_points_validate_buffers(cuda):
+    """The Python entry points reject, before any launch, an output that does
+    not hold n_batch x rows fp32 values, an AWQ vector that is not k fp32
+    values, and weight bytes outside their storage (the C ABI sees only raw
+    pointers, so these would otherwise be out-of-bounds device accesses)."""
+    import torch
+
+    rt = _rt()
+    raw, _ = make_weight(om.TYPE_Q8_0, 64, 512, seed=1)
+    w = _upload(raw, om.TYPE_Q8_0, 64, 512)
+    x = torch.zeros((2, 512), dtype=torch.float32, device=cuda)
+    bad_dst = [torch.zeros((2, 63), dtype=torch.float32, device=cuda),
+               torch.zeros((2, 64), dtype=torch.float16, device=cuda),
+               torch.zeros((2, 128), dtype=torch.float32, device=cuda)[:, ::2]]
+    for d in bad_dst:
+        with pytest.raises(rt.Qw35Error, match="dst"):
+            rt.decode_matvec(w, x, dst=d)
+        with pytest.raises(rt.Qw35Error, match="dst"):
+            rt.DecodePlan().matvec(w, x, d)
+        with pytest.raises(rt.Qw35Error, match="dst"):
+            rt.ffn_gate_up_swiglu(w, w, x, dst=d)
+    for a in (torch.ones(511, device=cuda), torch.ones(512, dtype=torch.float16, device=cuda)):
+        with pytest.raises(rt.Qw35Error, match="awq"):
+            rt.decode_matvec(w, x, awq=a)
+        with pytest.raises(rt.Qw35Error, match="awq"):
+            rt.output_argmax(w, x, awq=a)
+    with pytest.raises(rt.Qw35Error, match="n_batch"):
+        rt.decode_matvec(w, torch.zeros((9, 512), dtype=torch.float32, device=cuda))
+    with pytest.raises(rt.Qw35Error, match="exceed"):
+        rt.HipWeight.from_device(w.storage, om.TYPE_Q8_0, 64, 512, offset=16)
+    with pytest.raises(rt.Qw35Error, match="bytes"):
+        rt.HipWeight.upload(raw[:-1], om.TYPE_Q8_0, 64, 512)

@@ -1,0 +1,133 @@
+"""Config 5 at its real shapes: the 32-layer Qwen3.5-9B decode-step projection
+stack (q8_0 mixers, GF4 FFN, Q4_K head; 217 GEMVs recorded as one plan) at
+batch 1 and 8.  Every layer has its own weights (distinct seeds) and its own
+output buffers, so every output of every projection is checked against the
+fp64 product of the library's dequantised weights (which the dequantisation
+tests pin bit for bit to the oracle), within GEMV_REL_L2; the residual
+stream, which every output and down projection adds into, against the fp64
+sum of all 64 contributions; and every replay of the plan against the first,
+bit for bit.
+"""
+from __future__ import annotations
+
+import pytest
+
+from oracle import matvec as om
+from tests.helpers import GEMV_REL_L2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def stack9b(cuda):
+    from qwowl35_amd import qwen35
+
+    st = qwen35.ProjectionStack.synthetic(qwen35.QWEN35_9B, seed=11, distinct=True, device=cuda)
+    assert st.weight_bytes == qwen35.projection_bytes(st.hp, st.types) == 5_205_131_264
+    return st
+
+
+def _deq64(w, rows_per_block=32768):
+    """The library's dequantised weight in fp64, [rows, k] (row blocks keep the head's fp32 copy small)."""
+    import torch
+
+    from qwowl35_amd import runtime as rt
+
+    if w.rows <= rows_per_block:
+        return rt.dequantize(w).double()
+    out = torch.empty((w.rows, w.k), dtype=torch.float64, device=w.storage.device)
+    for r0 in range(0, w.rows, rows_per_block):
+        n = min(rows_per_block, w.rows - r0)
+        ids = torch.arange(r0, r0 + n, dtype=torch.int32, device=w.storage.device)
+        out[r0:r0 + n] = rt.dequantize(w, ids).double()
+    return out
+
+
+def _rel(got, want):
+    return om.rel_l2(got.cpu().numpy(), want.cpu().numpy())
+
+
+@pytest.mark.parametrize("nb", [1, 8])
+def test_stack9b_every_output(cuda, stack9b, nb):
+    import torch
+
+    from qwowl35_amd import qwen35
+
+    hp = stack9b.hp
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(100 + nb)
+    bufs = qwen35.StepBuffers.make(hp, nb, gen, awq=True, shared_outputs=False)
+    act0 = bufs.act.clone()
+    plan = qwen35.build_plan(stack9b, bufs)
+    assert len(plan) == qwen35.gemv_count(hp) == 217
+    print(f"stack9b nb={nb}: launching the recorded plan", flush=True)
+    plan.launch()
+    torch.cuda.synchronize()
+    first = {"act": bufs.act.clone(), "logits": bufs.logits.clone(),
+             "ffn_act": [a.clone() for a in bufs.ffn_act]}
+
+    x = bufs.norm.double().T
+    fx = (bufs.ffn_norm.double() * bufs.awq.double()).T
+    want_act = act0.double().clone()
+    worst = 0.0
+    for il, ws in enumerate(stack9b.layers):
+        mix = qwen35.mixer_projections(hp, il)
+        for p in mix[:-1]:
+            want = (_deq64(ws[p.name]) @ x).T
+            e = _rel(bufs.mixer_out[il][p.name], want)
+            worst = max(worst, e)
+            assert e <= GEMV_REL_L2, (il, p.name, e)
+        out = mix[-1]
+        want_act += (_deq64(ws[out.name]) @ bufs.core[out.k].double().T).T
+        gate = _deq64(ws["ffn_gate"]) @ fx
+        up = _deq64(ws["ffn_up"]) @ fx
+        want_g = (gate / (1.0 + torch.exp(-gate)) * up).T
+        e = _rel(bufs.ffn_act[il], want_g)
+        worst = max(worst, e)
+        assert e <= GEMV_REL_L2, (il, "ffn_gate_up_swiglu", e)
+        # the down projection reads the SwiGLU output the plan produced
+        want_act += (_deq64(ws["ffn_down"]) @ bufs.ffn_act[il].double().T).T
+    e = _rel(bufs.act, want_act)
+    assert e <= GEMV_REL_L2, ("residual stream", e)
+    want_logits = (_deq64(stack9b.head) @ x).T
+    e_head = _rel(bufs.logits, want_logits)
+    assert e_head <= GEMV_REL_L2, ("output.weight", e_head)
+    print(f"stack9b nb={nb}: worst projection rel-L2 {worst:.2e}, head {e_head:.2e}", flush=True)
+
+    # replays: the residual stream restored, outputs poisoned in between
+    for rep in range(2):
+        bufs.act.copy_(act0)
+        bufs.logits.fill_(float("nan"))
+        for a in bufs.ffn_act:
+            a.fill_(float("nan"))
+        plan.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(bufs.act, first["act"]), rep
+        assert torch.equal(bufs.logits, first["logits"]), rep
+        for il, a in enumerate(bufs.ffn_act):
+            assert torch.equal(a, first["ffn_act"][il]), (rep, il)
+    plan.close()
+
+
+def test_stack9b_shared_buffers_match_distinct(cuda, stack9b):
+    """The benchmark's form (one set of mixer / FFN output buffers reused by
+    every layer, as the reference runtime does) gives the same residual stream
+    and logits as the checked form above, bit for bit."""
+    import torch
+
+    from qwowl35_amd import qwen35
+
+    hp = stack9b.hp
+    res = []
+    for shared in (False, True):
+        gen = torch.Generator(device=cuda)
+        gen.manual_seed(7)
+        bufs = qwen35.StepBuffers.make(hp, 2, gen, awq=True, shared_outputs=shared)
+        plan = qwen35.build_plan(stack9b, bufs)
+        plan.launch()
+        torch.cuda.synchronize()
+        res.append((bufs.act.clone(), bufs.logits.clone(), bufs.ffn_act[-1].clone()))
+        plan.close()
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
