@@ -1,0 +1,10 @@
+// Chunked decode GEMV, gf4, fused gate/up/SwiGLU instantiations (kernel in kquant_mfma.h).
+#include "kquant_mfma.h"
+
+namespace qw35 {
+
+hipError_t kq_gf4_swiglu(const GemvArgs& a, hipStream_t stream) {
+    return kq_launch_any<kFmtGF4, true>(a, stream);
+}
+
+}  // namespace qw35

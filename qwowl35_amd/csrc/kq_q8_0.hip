@@ -1,0 +1,14 @@
+// Chunked decode GEMV, q8_0, plain (and greedy-head) instantiations (kernel in kquant_mfma.h).
+#include "kquant_mfma.h"
+
+namespace qw35 {
+
+hipError_t kq_q8_0_plain(const GemvArgs& a, hipStream_t stream) {
+    return kq_launch_any<kFmtQ8, false>(a, stream);
+}
+
+hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream) {
+    return a.w_up ? kq_q8_0_swiglu(a, stream) : kq_q8_0_plain(a, stream);
+}
+
+}  // namespace qw35
