@@ -156,6 +156,24 @@ int qw35_hip_output_argmax(const qw35_hip_weight *w, const float *x, const float
                            uint32_t *token, float *logit, void *workspace, uint64_t workspace_bytes, void *stream,
                            char *err, uintptr_t err_len);
 
+/* Greedy head that allocates nothing and takes no workspace: the same
+ * validation, kernels and results (bit for bit) as qw35_hip_output_argmax,
+ * with the per-workgroup partials in a device array the library owns,
+ * QW35_HIP_ARGMAX_SCRATCH_BYTES on each GPU it runs on, held until the
+ * process ends.  No counterpart in the reference: it is for callers that
+ * cannot allocate or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  A head whose partials
+ * exceed the array (2 x 4 x n_batch x the GEMV's workgroup count, each half
+ * rounded up to 256 bytes; e.g. every plan of a 248320 x 4096 head at batch
+ * 1..8 fits) is refused with an error.  All calls on one GPU share its
+ * array, which keeps the last call's partials: calls that overlap on one GPU
+ * (concurrent streams, or threads) race and must be serialised by the
+ * caller.  The first call on each device looks the array up
+ * (hipGetSymbolAddress); make it outside graph capture. */
+#define QW35_HIP_ARGMAX_SCRATCH_BYTES (2u << 20)
+int qw35_hip_output_argmax_noalloc(const qw35_hip_weight *w, const float *x, const float *awq, uint32_t n_batch,
+                                   uint32_t *token, float *logit, void *stream, char *err, uintptr_t err_len);
+
 /* fp32 dequantisation (bit-exact statement of each format).  row_ids == NULL:
  * all rows, dst fp32 [rows][k]; otherwise dst[i] = row row_ids[i] (device
  * uint32 [n_rows]; an id >= rows gives a row of zeros), which is the

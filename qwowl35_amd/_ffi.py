@@ -104,6 +104,11 @@ PROTOTYPES: dict[str, tuple] = {
         [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
          C.c_void_p, C.c_char_p, C.c_size_t],
     ),
+    "qw35_hip_output_argmax_noalloc": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_char_p,
+         C.c_size_t],
+    ),
     "qw35_hip_dequantize": (
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],

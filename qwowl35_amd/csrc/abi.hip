@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/qw35_hip.h"
 #include "qw35_kernels.h"
 
@@ -549,6 +551,73 @@ int qw35_hip_output_argmax(const qw35_hip_weight* w, const float* x, const float
                      "output_argmax", err, err_len)
                ? 1
                : 0;
+}
+
+}  // extern "C"
+
+// Scratch of qw35_hip_output_argmax_noalloc: the greedy head's per-workgroup
+// (row, logit) partials, in a device array the library owns instead of a
+// caller workspace.  Each GPU holds its own copy for the life of the process;
+// host code addresses it only through the pointer hipGetSymbolAddress
+// returns for the current device (the array's name is a host-side stand-in).
+static __device__ __align__(256) uint8_t scratch[QW35_HIP_ARGMAX_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device.
+void* scratch_of_current_device(char* err, uintptr_t err_len) {
+    int dev = -1;
+    if (!check_hip(hipGetDevice(&dev), "output_argmax_noalloc: device", err, err_len)) return nullptr;
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_err(err, err_len, "output_argmax_noalloc: device %d out of range", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (!check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "output_argmax_noalloc: scratch address", err,
+                       err_len))
+            return nullptr;
+        if (!p) {
+            set_err(err, err_len, "output_argmax_noalloc: null scratch address");
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int qw35_hip_output_argmax_noalloc(const qw35_hip_weight* w, const float* x, const float* awq, uint32_t n_batch,
+                                   uint32_t* token, float* logit, void* stream, char* err, uintptr_t err_len) {
+    if (!check_weight(w, "output_argmax_noalloc", err, err_len) ||
+        !check_gemv_type(w, "output_argmax_noalloc", err, err_len))
+        return 0;
+    if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
+        set_err(err, err_len, "output_argmax_noalloc: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);
+        return 0;
+    }
+    const uint64_t need = 2 * argmax_ws_part(w, n_batch);
+    if (need > QW35_HIP_ARGMAX_SCRATCH_BYTES) {
+        set_err(err, err_len,
+                "output_argmax_noalloc: the partials of a %llu-row head at batch %u take %llu bytes and exceed the "
+                "library's %llu-byte array; use qw35_hip_output_argmax with a workspace",
+                (unsigned long long)w->rows, n_batch, (unsigned long long)need,
+                (unsigned long long)QW35_HIP_ARGMAX_SCRATCH_BYTES);
+        return 0;
+    }
+    void* ptr = scratch_of_current_device(err, err_len);
+    if (!ptr) return 0;
+    // Same validation and kernels as the workspace entry point, over the array.
+    return qw35_hip_output_argmax(w, x, awq, n_batch, token, logit, ptr, QW35_HIP_ARGMAX_SCRATCH_BYTES, stream, err,
+                                  err_len);
 }
 
 uint32_t qw35_hip_stream_read_sink_len(uint64_t bytes) { return qw35::stream_read_blocks(bytes); }
