@@ -10,9 +10,11 @@
  *     Qw35FFI.h:87-88).
  * Pointers marked "device" are HBM addresses (hipMalloc'd or offsets into an
  * uploaded model image).  `stream` is a hipStream_t (NULL = default stream).
- * Calls on one stream are ordered; the library keeps no global mutable state
- * except its plans and tensor stores, which are single-threaded objects (like
- * MetalRuntime, `Send` but not `Sync`, qw35-server/src/metal/bridge.rs:257).
+ * Calls on one stream are ordered.  The library's objects are its plans and
+ * runtimes, single-threaded objects (like MetalRuntime, `Send` but not `Sync`,
+ * qw35-server/src/metal/bridge.rs:257), and its tensor stores, immutable
+ * and shared per model image under a lock; its only other global state is
+ * the per-device array of qw35_hip_output_argmax_noalloc.
  *
  * Weight formats are the reference's raw GGUF tensor bytes (no repacking):
  *   type 100  GF4   8 elems / 4 B   (tools/gguf_custom_types.py:26-30)
@@ -93,12 +95,20 @@ int qw35_hip_gguf_parse(const void *model_map, uint64_t model_size, qw35_hip_ten
 /* Device tensor store: replaces Qw35TensorStore (Qw35TensorStore.m:58-153),
  * which wraps the host mmap in Metal buffers.  HBM is not host memory, so the
  * image's bytes 0 .. end of the last tensor are copied once (synchronously)
- * into one device allocation, the only device memory the library itself
- * allocates; descs (e.g. from qw35_hip_gguf_parse) are checked to lie inside
- * model_size and copied with their names, so the host image may be unmapped
- * afterwards.  qw35_hip_store_weight gives the weight view (as
- * qw35_hip_weight_view) of the tensor named name[0 .. name_len).  Destroy
- * after the last kernel that reads the store has completed. */
+ * into one device allocation; descs (e.g. from qw35_hip_gguf_parse) are
+ * checked to lie inside model_size and copied with their names, so the host
+ * image may be unmapped afterwards.  One store per model image and device is
+ * shared, as the reference shares one store per mapped file between its
+ * runtimes (Qw35MetalRuntime.m:42-80): a create over the same (model_map,
+ * model_size, descriptor count) on the same device returns the existing
+ * store with one more reference, and qw35_hip_store_destroy drops one; the
+ * device copy is freed with the last.  The store is immutable after creation,
+ * so its users may be on different threads.  Sharing is keyed by the image's
+ * address: an image must not be changed, or freed and replaced at the same
+ * address, while a store over it is alive.  qw35_hip_store_weight gives the
+ * weight view (as qw35_hip_weight_view) of the tensor named
+ * name[0 .. name_len).  Drop the last reference after the last kernel that
+ * reads the store has completed. */
 void *qw35_hip_store_create(const void *model_map, uint64_t model_size, const qw35_hip_tensor_desc *descs,
                             uint32_t count, char *err, uintptr_t err_len);
 const void *qw35_hip_store_device_base(const void *store);
@@ -202,16 +212,23 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight *w, void *dst, void *stream, c
  * plan; the device memory they describe must outlive it. */
 #define QW35_HIP_OP_MATVEC 0u /* dst (+)= W (awq * x), see qw35_hip_decode_matvec */
 #define QW35_HIP_OP_SWIGLU 1u /* dst = silu(gate (awq*x)) * (up (awq*x)) */
+#define QW35_HIP_OP_ARGMAX 2u /* greedy head, see qw35_hip_output_argmax: token[b], dst[b] = logit */
 typedef struct {
     uint32_t kind;               /* QW35_HIP_OP_* */
     uint32_t n_batch;            /* 1..8 */
     int32_t residual;            /* MATVEC only: nonzero adds into dst */
     uint32_t reserved;
-    const qw35_hip_weight *w;    /* MATVEC weight or SWIGLU gate */
+    const qw35_hip_weight *w;    /* MATVEC / ARGMAX weight or SWIGLU gate */
     const qw35_hip_weight *w_up; /* SWIGLU up, else NULL */
     const float *x;              /* device [n_batch][k] */
     const float *awq;            /* device [k] or NULL */
-    float *dst;                  /* device [n_batch][rows] */
+    float *dst;                  /* device [n_batch][rows]; ARGMAX: the chosen logits [n_batch] */
+    /* ARGMAX only (NULL / 0 otherwise): the chosen rows [n_batch], and a workspace
+     * of qw35_hip_output_argmax_workspace_size(w, n_batch) bytes, 256-byte
+     * aligned, used by this op alone. */
+    uint32_t *token;
+    void *workspace;
+    uint64_t workspace_bytes;
 } qw35_hip_plan_op;
 
 /* Validate the ops (same rules as the single calls) and record them; NULL on
@@ -222,6 +239,115 @@ int qw35_hip_plan_launch(void *plan, void *stream, char *err, uintptr_t err_len)
 /* Number of ops recorded in the plan (0 for NULL). */
 uint32_t qw35_hip_plan_size(const void *plan);
 void qw35_hip_plan_destroy(void *plan);
+
+/* ---- Projection runtime: the in-scope part of the runtime-level ABI ----
+ *
+ * The reference's Rust host drives a whole-model runtime through
+ * qw35_metal_runtime_create / eval_token / argmax / copy_logits / sync /
+ * destroy (qw35-server/src/metal/bridge/Qw35FFI.h:19-118).  This library
+ * builds the part of that runtime that is this path: the model's projection
+ * weights resolved by their GGUF names and validated against the
+ * hyper-parameters (Qw35MetalRuntime.m:287-372), held in a device tensor store
+ * shared by every runtime over the same model image (Qw35MetalRuntime.m:42-80),
+ * and one decode step's projections in the reference's dispatch order
+ * (encodeDecodeLayers, Qw35MetalRuntime.m:1170-1221) recorded as a hipGraph.
+ * The attention, DeltaNet recurrence, norms, embedding and KV cache between
+ * the projections are not part of this library: each step reads its inputs
+ * from runtime-owned device buffers (qw35_hip_runtime_buffer) that the
+ * caller's own kernels fill, as the reference's _norm / _core / _act_a buffers
+ * are filled by its non-projection kernels. */
+
+/* Hyper-parameters: field for field the reference's qw35_metal_hparams
+ * (Qw35MetalTypes.h:30-59; append-only).  The runtime reads the projection
+ * shapes from transformer_layers, embedding_length, feed_forward_length,
+ * attention_heads / kv_heads / key_length / value_length, ssm_state_size,
+ * ssm_group_count, ssm_time_step_rank, ssm_inner_size,
+ * full_attention_interval (0 = 4) and attn_gate; the rest is carried for the
+ * caller's kernels.  n_cls_out must be 0 (classification heads are not part
+ * of this path). */
+typedef struct {
+    uint32_t transformer_layers;
+    uint32_t embedding_length;
+    uint32_t feed_forward_length;
+    uint32_t attention_heads;
+    uint32_t attention_kv_heads;
+    uint32_t attention_key_length;
+    uint32_t attention_value_length;
+    uint32_t rope_dimension_count;
+    int32_t rope_sections[4];
+    float rope_freq_base;
+    float rms_epsilon;
+    uint32_t ssm_conv_kernel;
+    uint32_t ssm_state_size;
+    uint32_t ssm_group_count;
+    uint32_t ssm_time_step_rank;
+    uint32_t ssm_inner_size;
+    uint32_t full_attention_interval;
+    int32_t attn_window;
+    int32_t attn_sink;
+    uint32_t attn_gate;
+    uint32_t n_cls_out;
+} qw35_hip_hparams;
+
+/* Output-head mode of an eval call: the reference's qw35_logits_mode
+ * (Qw35MetalTypes.h:61-66). */
+typedef enum {
+    QW35_HIP_LOGITS_NONE = 0,   /* no head */
+    QW35_HIP_LOGITS_ARGMAX = 1, /* fused greedy head only; logits never materialised */
+    QW35_HIP_LOGITS_FULL = 2,   /* the full logits vector */
+} qw35_hip_logits_mode;
+
+/* Runtime-owned fp32 device buffers, [n_batch][width] with row stride width
+ * (the reference runtime's buffers, Qw35MetalRuntime.m:374-460). */
+#define QW35_HIP_RT_NORM 0u   /* [emb] input of the mixer input projections, the FFN and the head (_norm) */
+#define QW35_HIP_RT_CORE 1u   /* [max(heads*value_length, ssm_inner)] input of attn_output / ssm_out (_core) */
+#define QW35_HIP_RT_ACT 2u    /* [emb] residual stream; attn_output, ssm_out and ffn_down add into it (_act_a) */
+#define QW35_HIP_RT_QKV 3u    /* attn_q (heads*key_length*(attn_gate?2:1)) or attn_qkv output (_qkv) */
+#define QW35_HIP_RT_K 4u      /* [kv_heads*key_length] attn_k output */
+#define QW35_HIP_RT_V 5u      /* [kv_heads*value_length] attn_v output */
+#define QW35_HIP_RT_Z 6u      /* [ssm_inner] attn_gate output (_z_gate) */
+#define QW35_HIP_RT_BETA 7u   /* [ssm_time_step_rank] ssm_beta output (_beta) */
+#define QW35_HIP_RT_ALPHA 8u  /* [ssm_time_step_rank] ssm_alpha output (_alpha) */
+#define QW35_HIP_RT_FFN 9u    /* [ffn] SwiGLU output, input of ffn_down (_ffn_gate) */
+#define QW35_HIP_RT_LOGITS 10u /* [vocab] output head (_logits) */
+#define QW35_HIP_RT_NBUF 11u
+
+/* Create a runtime on the current device: parse nothing (descs come from
+ * qw35_hip_gguf_parse or the caller's loader), share or create the device
+ * store of model_map (qw35_hip_store_create), resolve and validate every
+ * projection (blk.N.attn_q/k/v/output or blk.N.attn_qkv/attn_gate/ssm_beta/
+ * ssm_alpha/ssm_out by layer kind, blk.N.ffn_gate/up/down, output.weight with
+ * vocab_size rows), and allocate the buffers above for max_batch (1..8) batch
+ * rows.  NULL on error (missing tensor, shape that does not match hparams,
+ * type the GEMVs do not take, gate/up of different types). */
+void *qw35_hip_runtime_create(const void *model_map, uint64_t model_size, const qw35_hip_tensor_desc *tensors,
+                              uintptr_t tensor_count, const qw35_hip_hparams *hparams, uint32_t vocab_size,
+                              uint32_t max_batch, char *err, uintptr_t err_len);
+/* Waits for the runtime's work, then frees it (the store when its last user goes). */
+void qw35_hip_runtime_destroy(void *runtime);
+/* One decode step's projections for n_batch rows of the buffers, replayed from
+ * a hipGraph recorded on first use of (n_batch, logits_mode).  Asynchronous on
+ * the runtime's stream: device errors surface at the next sync / argmax /
+ * copy_logits, as in the reference (Qw35FFI.h:87-88).  Replaces the projection
+ * part of qw35_metal_runtime_eval_token (Qw35FFI.h:92-97). */
+int qw35_hip_runtime_eval_step(void *runtime, uint32_t n_batch, int logits_mode, char *err, uintptr_t err_len);
+/* Wait for the last eval; then the greedy head's rows and logits of its n_batch
+ * batch rows (that eval must have used QW35_HIP_LOGITS_ARGMAX).  Replaces
+ * qw35_metal_runtime_argmax (Qw35FFI.h:106-111). */
+int qw35_hip_runtime_argmax(void *runtime, uint32_t *token, float *logit, char *err, uintptr_t err_len);
+/* Wait for the last eval (QW35_HIP_LOGITS_FULL) and copy its n_batch x vocab
+ * logits into dst (len >= n_batch * vocab floats).  Replaces
+ * qw35_metal_runtime_copy_logits (Qw35FFI.h:113-118). */
+int qw35_hip_runtime_copy_logits(void *runtime, float *dst, uintptr_t len, char *err, uintptr_t err_len);
+/* Wait for all of the runtime's work.  Replaces qw35_metal_runtime_sync (Qw35FFI.h:71-72). */
+int qw35_hip_runtime_sync(void *runtime, char *err, uintptr_t err_len);
+/* Device address and row width (floats) of buffer `which` (QW35_HIP_RT_*). */
+int qw35_hip_runtime_buffer(void *runtime, uint32_t which, float **device_ptr, uint64_t *width, char *err,
+                            uintptr_t err_len);
+/* The runtime's stream (hipStream_t), for ordering the caller's kernels and copies with its steps. */
+void *qw35_hip_runtime_stream(void *runtime);
+/* The device tensor store the runtime reads its weights from. */
+const void *qw35_hip_runtime_store(void *runtime);
 
 /* Multi-token (prefill) matmul of a GF4 or F16 weight on MFMA:
  *   c[t][r] = sum_k bf16_rne(awq[k] * a[t][k]) * W[r][k]    (awq == NULL: a[t][k] as bf16)

@@ -69,6 +69,48 @@ class PlanOp(C.Structure):
         ("x", C.c_void_p),
         ("awq", C.c_void_p),
         ("dst", C.c_void_p),
+        ("token", C.c_void_p),
+        ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_uint64),
+    ]
+
+
+OP_ARGMAX = 2
+
+LOGITS_NONE = 0
+LOGITS_ARGMAX = 1
+LOGITS_FULL = 2
+
+# Runtime buffers (QW35_HIP_RT_*).
+RT_NORM, RT_CORE, RT_ACT, RT_QKV, RT_K, RT_V, RT_Z, RT_BETA, RT_ALPHA, RT_FFN, RT_LOGITS = range(11)
+RT_NBUF = 11
+
+
+class Hparams(C.Structure):
+    """``qw35_hip_hparams`` == ``qw35_metal_hparams`` (Qw35MetalTypes.h:30-59)."""
+
+    _fields_ = [
+        ("transformer_layers", C.c_uint32),
+        ("embedding_length", C.c_uint32),
+        ("feed_forward_length", C.c_uint32),
+        ("attention_heads", C.c_uint32),
+        ("attention_kv_heads", C.c_uint32),
+        ("attention_key_length", C.c_uint32),
+        ("attention_value_length", C.c_uint32),
+        ("rope_dimension_count", C.c_uint32),
+        ("rope_sections", C.c_int32 * 4),
+        ("rope_freq_base", C.c_float),
+        ("rms_epsilon", C.c_float),
+        ("ssm_conv_kernel", C.c_uint32),
+        ("ssm_state_size", C.c_uint32),
+        ("ssm_group_count", C.c_uint32),
+        ("ssm_time_step_rank", C.c_uint32),
+        ("ssm_inner_size", C.c_uint32),
+        ("full_attention_interval", C.c_uint32),
+        ("attn_window", C.c_int32),
+        ("attn_sink", C.c_int32),
+        ("attn_gate", C.c_uint32),
+        ("n_cls_out", C.c_uint32),
     ]
 
 
@@ -114,6 +156,20 @@ PROTOTYPES: dict[str, tuple] = {
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
     ),
     "qw35_hip_dequantize_f16": (C.c_int, [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_create": (
+        C.c_void_p,
+        [C.c_void_p, C.c_uint64, C.POINTER(TensorDesc), C.c_size_t, C.POINTER(Hparams), C.c_uint32, C.c_uint32,
+         C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_runtime_destroy": (None, [C.c_void_p]),
+    "qw35_hip_runtime_eval_step": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_copy_logits": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_sync": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_buffer": (
+        C.c_int, [C.c_void_p, C.c_uint32, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64), C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_stream": (C.c_void_p, [C.c_void_p]),
+    "qw35_hip_runtime_store": (C.c_void_p, [C.c_void_p]),
     "qw35_hip_plan_create": (C.c_void_p, [C.POINTER(PlanOp), C.c_uint32, C.c_char_p, C.c_size_t]),
     "qw35_hip_plan_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
     "qw35_hip_plan_size": (C.c_uint32, [C.c_void_p]),

@@ -192,6 +192,13 @@ bool mergeable(const qw35_hip_plan_op& a, const qw35_hip_plan_op& b) {
     return !overlaps(a.dst, da, b.dst, db) && !overlaps(a.x, xa, a.dst, da) && !overlaps(a.x, xa, b.dst, db);
 }
 
+// Greedy head workspace: per batch row, one (token, logit) partial per
+// workgroup of the GEMV launch; tokens first, logits at a 256-byte boundary.
+uint64_t argmax_ws_part(const qw35_hip_weight* w, uint32_t n_batch) {
+    const uint64_t n = (uint64_t)qw35::argmax_groups(w->type_id, (int)w->rows, (int)w->k, (int)n_batch) * n_batch;
+    return (n * 4 + 255) / 256 * 256;
+}
+
 // A recorded decode-step plan: the launches (their weight pointers, shapes and
 // buffers baked into the kernel arguments) held as an instantiated hipGraph.
 struct Plan {
@@ -298,6 +305,22 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                 return nullptr;
             }
             if (!check_swiglu(o.w, o.w_up, o.x, o.awq, o.dst, o.n_batch, what, err, err_len)) return nullptr;
+        } else if (o.kind == QW35_HIP_OP_ARGMAX) {
+            if (o.w_up || o.residual) {
+                set_err(err, err_len, "%s: an ARGMAX op takes no w_up or residual", what);
+                return nullptr;
+            }
+            if (!check_matvec(o.w, o.x, o.awq, o.dst, o.n_batch, what, err, err_len)) return nullptr;
+            if (!o.token || ((uintptr_t)o.token & 3u)) {
+                set_err(err, err_len, "%s: an ARGMAX op needs a 4-byte aligned token output", what);
+                return nullptr;
+            }
+            const uint64_t part = argmax_ws_part(o.w, o.n_batch);
+            if (!o.workspace || ((uintptr_t)o.workspace & 255u) || o.workspace_bytes < 2 * part) {
+                set_err(err, err_len, "%s: an ARGMAX op needs a 256-byte aligned workspace of >= %llu bytes", what,
+                        (unsigned long long)(2 * part));
+                return nullptr;
+            }
         } else {
             set_err(err, err_len, "%s: unknown kind %u", what, o.kind);
             return nullptr;
@@ -315,6 +338,15 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
     if (e == hipSuccess) {
         for (uint32_t i = 0; i < n_ops && launch == hipSuccess;) {
             const qw35_hip_plan_op& o = ops[i];
+            if (o.kind == QW35_HIP_OP_ARGMAX) {
+                qw35::GemvArgs a = gemv_args(o.w, nullptr, o.x, o.awq, nullptr, o.n_batch, 0);
+                a.am_token = static_cast<uint32_t*>(o.workspace);
+                a.am_logit = reinterpret_cast<float*>(static_cast<uint8_t*>(o.workspace) +
+                                                      argmax_ws_part(o.w, o.n_batch));
+                launch = qw35::launch_argmax_gemv(o.w->type_id, a, o.token, o.dst, s);
+                ++i;
+                continue;
+            }
             const bool sw = o.kind == QW35_HIP_OP_SWIGLU;
             qw35::GemvArgs a = gemv_args(o.w, sw ? o.w_up : nullptr, o.x, o.awq, o.dst, o.n_batch,
                                          sw ? 0 : o.residual);
@@ -506,12 +538,6 @@ int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_
                : 0;
 }
 
-// Greedy head workspace: per batch row, one (token, logit) partial per
-// workgroup of the GEMV launch; tokens first, logits at a 256-byte boundary.
-static uint64_t argmax_ws_part(const qw35_hip_weight* w, uint32_t n_batch) {
-    const uint64_t n = (uint64_t)qw35::argmax_groups(w->type_id, (int)w->rows, (int)w->k, (int)n_batch) * n_batch;
-    return (n * 4 + 255) / 256 * 256;
-}
 
 uint64_t qw35_hip_output_argmax_workspace_size(const qw35_hip_weight* w, uint32_t n_batch) {
     char msg[8];

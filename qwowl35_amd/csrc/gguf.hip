@@ -21,8 +21,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/qw35_hip.h"
@@ -165,7 +167,23 @@ struct Store {
     uint64_t bytes = 0;
     std::vector<std::string> names;
     std::vector<qw35_hip_tensor_desc> descs;
+    std::unordered_map<std::string, size_t> index;  // name -> descs position
+    // Sharing key and reference count (under g_stores_mu).
+    const void* map = nullptr;
+    uint64_t map_size = 0;
+    uint32_t count = 0;
+    int device = -1;
+    int refs = 0;
 };
+
+// Every live store, so that creates over the same image and device share one.
+std::mutex g_stores_mu;
+std::vector<Store*> g_stores;
+
+void store_free(Store* s) {
+    if (s->dev) (void)hipFree(s->dev);
+    delete s;
+}
 
 }  // namespace
 
@@ -288,19 +306,36 @@ void* qw35_hip_store_create(const void* model_map, uint64_t model_size, const qw
         }
         if (d.abs_offset + d.bytes > end) end = d.abs_offset + d.bytes;
     }
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess) {
+        (void)hipGetLastError();
+        gg_err(err, err_len, "store_create: no current HIP device");
+        return nullptr;
+    }
+    // Creation runs under the lock, so two first users of one image copy it once.
+    std::lock_guard<std::mutex> lock(g_stores_mu);
+    for (Store* o : g_stores) {
+        if (o->map == model_map && o->map_size == model_size && o->count == count && o->device == device) {
+            ++o->refs;
+            return o;
+        }
+    }
     Store* s = new (std::nothrow) Store();
     if (!s) {
         gg_err(err, err_len, "store_create: out of host memory");
         return nullptr;
     }
+    s->map = model_map;
+    s->map_size = model_size;
+    s->count = count;
+    s->device = device;
     s->bytes = end;
     if (end) {
         hipError_t e = hipMalloc(&s->dev, end);
         if (e == hipSuccess) e = hipMemcpy(s->dev, model_map, end, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             gg_err(err, err_len, "store_create: %llu device bytes: %s", (unsigned long long)end, hipGetErrorString(e));
-            if (s->dev) (void)hipFree(s->dev);
-            delete s;
+            store_free(s);
             return nullptr;
         }
     }
@@ -311,12 +346,15 @@ void* qw35_hip_store_create(const void* model_map, uint64_t model_size, const qw
             s->names.emplace_back(reinterpret_cast<const char*>(descs[i].name),
                                   descs[i].name ? descs[i].name_len : 0);
             s->descs[i].name = reinterpret_cast<const uint8_t*>(s->names.back().data());
+            s->index.emplace(s->names.back(), i);  // the first of duplicate names wins
         }
+        g_stores.push_back(s);
     } catch (...) {
         gg_err(err, err_len, "store_create: out of host memory");
-        qw35_hip_store_destroy(s);
+        store_free(s);
         return nullptr;
     }
+    s->refs = 1;
     return s;
 }
 
@@ -331,10 +369,8 @@ int qw35_hip_store_weight(const void* store, const char* name, uintptr_t name_le
         return 0;
     }
     const Store* s = static_cast<const Store*>(store);
-    for (size_t i = 0; i < s->names.size(); ++i) {
-        if (s->names[i].size() == name_len && memcmp(s->names[i].data(), name, name_len) == 0)
-            return qw35_hip_weight_view(&s->descs[i], s->dev, out, err, err_len);
-    }
+    const auto it = s->index.find(std::string(name, name_len));
+    if (it != s->index.end()) return qw35_hip_weight_view(&s->descs[it->second], s->dev, out, err, err_len);
     gg_err(err, err_len, "store_weight: no tensor named %.*s", (int)(name_len < 96 ? name_len : 96), name);
     return 0;
 }
@@ -342,8 +378,14 @@ int qw35_hip_store_weight(const void* store, const char* name, uintptr_t name_le
 void qw35_hip_store_destroy(void* store) {
     Store* s = static_cast<Store*>(store);
     if (!s) return;
-    if (s->dev) (void)hipFree(s->dev);
-    delete s;
+    std::lock_guard<std::mutex> lock(g_stores_mu);
+    if (--s->refs > 0) return;
+    for (size_t i = 0; i < g_stores.size(); ++i)
+        if (g_stores[i] == s) {
+            g_stores.erase(g_stores.begin() + (ptrdiff_t)i);
+            break;
+        }
+    store_free(s);
 }
 
 }  // extern "C"

@@ -276,3 +276,19 @@ def gemv_count(hp: Hparams, head: bool = True) -> int:
     """GEMVs of one step as the reference dispatches them (fused gate/up counts once)."""
     n = sum(len(mixer_projections(hp, il)) + 2 for il in range(hp.transformer_layers))
     return n + (1 if head else 0)
+
+
+def gguf_name(il: int | None, proj: str) -> str:
+    """GGUF tensor name of a projection: ``blk.{il}.{proj}.weight``, or ``output.weight`` (il None)."""
+    return "output.weight" if il is None else f"blk.{il}.{proj}.weight"
+
+
+def stack_tensors(stack: ProjectionStack) -> list[tuple[str, tuple[int, int], int, torch.Tensor]]:
+    """(GGUF name, dims (k, rows), type id, device bytes) of every projection of a stack, in layer order."""
+    out = []
+    for il, ws in enumerate(stack.layers):
+        for name, w in ws.items():
+            out.append((gguf_name(il, name), (w.k, w.rows), w.type_id, w.storage))
+    h = stack.head
+    out.append((gguf_name(None, "output"), (h.k, h.rows), h.type_id, h.storage))
+    return out

@@ -429,6 +429,27 @@ class DecodePlan:
         self._add(_ffi.OP_SWIGLU, nb, False, gate, up, x, awq, dst)
         return self
 
+    def argmax(self, w: HipWeight, x: torch.Tensor, token: torch.Tensor, logit: torch.Tensor,
+               awq: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> "DecodePlan":
+        """The greedy head as a plan op: ``token[b]`` / ``logit[b]`` (int32 / fp32
+        device, n_batch each) of the largest ``W @ (awq * x[b])`` entry."""
+        nb = _check_act(x, w.k, "x")
+        _check_awq(awq, w.k, x)
+        _check_out(logit, nb, 1, x, "logit")
+        if token.dtype != torch.int32 or not token.is_contiguous() or token.numel() != nb or token.device != x.device:
+            raise Qw35Error(f"token must be a contiguous int32 tensor of n_batch={nb} values on {x.device}")
+        if workspace is None:
+            workspace = output_argmax_workspace(w, nb, device=x.device)
+        base = workspace.data_ptr()
+        pad = (-base) % 256
+        self._add(_ffi.OP_ARGMAX, nb, False, w, None, x, awq, logit)
+        op = self._ops[-1]
+        op.token = token.data_ptr()
+        op.workspace = base + pad
+        op.workspace_bytes = workspace.numel() - pad
+        self._keep.extend([token, workspace])
+        return self
+
     def _add(self, kind, nb, residual, w, up, x, awq, dst):
         if self._handle is not None:
             raise Qw35Error("plan already recorded")
@@ -461,6 +482,118 @@ class DecodePlan:
         if self._handle is not None:
             _ffi.load().qw35_hip_plan_destroy(self._handle)
             self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _hip_runtime() -> C.CDLL:
+    """The process's HIP runtime (the one torch and libqw35_hip.so share, soname
+    libamdhip64.so.7): plumbing for copies into library-owned device buffers."""
+    _ffi.load()
+    lib = C.CDLL("libamdhip64.so.7")
+    lib.hipMemcpy.restype = C.c_int
+    lib.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    return lib
+
+
+_HIP_MEMCPY_DEFAULT = 4  # hipMemcpyDefault: direction from the (unified) addresses
+
+
+def hparams_struct(hp) -> _ffi.Hparams:
+    """``qw35_hip_hparams`` from an object with the projection fields (e.g. ``qwen35.Hparams``)."""
+    h = _ffi.Hparams()
+    for name, _ in _ffi.Hparams._fields_:
+        if name == "rope_sections" or not hasattr(hp, name):
+            continue
+        setattr(h, name, getattr(hp, name))
+    return h
+
+
+class ProjectionRuntime:
+    """The projection runtime (``qw35_hip_runtime_*``): the in-scope part of the
+    reference's ``qw35_metal_runtime_*`` ABI (Qw35FFI.h:19-118).
+
+    Built from a GGUF image (host bytes or an mmap) and the hyper-parameters;
+    ``write(which, x)`` fills an input buffer (``_ffi.RT_NORM`` / ``RT_CORE`` /
+    ``RT_ACT``), ``eval_step(n_batch, mode)`` replays one decode step's
+    projections, and ``argmax()`` / ``copy_logits()`` / ``read(which, n_batch)``
+    wait and read back, as ``qw35_metal_runtime_argmax`` / ``copy_logits`` do.
+    """
+
+    def __init__(self, image, hparams, vocab: int, max_batch: int = 1):
+        self._h = None
+        tensors, _, (descs, n, keep) = gguf_parse(image)
+        ptr, size, _ = _image_ptr(keep)
+        self._keep = keep
+        self.tensors = tensors
+        self.hparams = hparams_struct(hparams)
+        self.vocab = int(vocab)
+        self.max_batch = int(max_batch)
+        self._h = C.c_void_p(_ffi.call("qw35_hip_runtime_create", ptr, size, descs, n, C.byref(self.hparams),
+                                       self.vocab, self.max_batch))
+        self._hip = _hip_runtime()
+        self.last_batch = 0
+
+    def buffer(self, which: int) -> tuple[int, int]:
+        """(device address, width in floats) of runtime buffer ``which``."""
+        p, w = C.c_void_p(), C.c_uint64()
+        _ffi.call("qw35_hip_runtime_buffer", self._h, which, C.byref(p), C.byref(w))
+        return int(p.value or 0), int(w.value)
+
+    @property
+    def store_base(self) -> int:
+        return int(_ffi.load().qw35_hip_store_device_base(_ffi.load().qw35_hip_runtime_store(self._h)) or 0)
+
+    def _copy(self, dst: int, src: int, nbytes: int) -> None:
+        rc = self._hip.hipMemcpy(C.c_void_p(dst), C.c_void_p(src), nbytes, _HIP_MEMCPY_DEFAULT)
+        if rc != 0:
+            raise Qw35Error(f"hipMemcpy failed ({rc})")
+
+    def write(self, which: int, x: torch.Tensor) -> None:
+        """Copy fp32 [n_batch, width'] (contiguous, any device) into buffer ``which``."""
+        torch.cuda.synchronize()
+        self.sync()
+        ptr, width = self.buffer(which)
+        if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() > width * self.max_batch or not ptr:
+            raise Qw35Error(f"write: fp32 contiguous data of at most {self.max_batch} x {width} floats")
+        self._copy(ptr, x.data_ptr(), x.numel() * 4)
+
+    def read(self, which: int, n_floats: int) -> torch.Tensor:
+        """The first ``n_floats`` of buffer ``which`` (after waiting), as a CPU tensor."""
+        self.sync()
+        ptr, width = self.buffer(which)
+        if n_floats > width * self.max_batch:
+            raise Qw35Error("read: more floats than the buffer holds")
+        out = torch.empty(n_floats, dtype=torch.float32)
+        self._copy(out.data_ptr(), ptr, n_floats * 4)
+        return out
+
+    def eval_step(self, n_batch: int = 1, mode: int = _ffi.LOGITS_FULL) -> None:
+        _ffi.call("qw35_hip_runtime_eval_step", self._h, n_batch, mode)
+        self.last_batch = n_batch
+
+    def argmax(self) -> tuple[list[int], list[float]]:
+        tok = (C.c_uint32 * self.last_batch)()
+        lg = (C.c_float * self.last_batch)()
+        _ffi.call("qw35_hip_runtime_argmax", self._h, tok, lg)
+        return list(tok), list(lg)
+
+    def copy_logits(self) -> torch.Tensor:
+        out = torch.empty((self.last_batch, self.vocab), dtype=torch.float32)
+        _ffi.call("qw35_hip_runtime_copy_logits", self._h, C.c_void_p(out.data_ptr()), out.numel())
+        return out
+
+    def sync(self) -> None:
+        _ffi.call("qw35_hip_runtime_sync", self._h)
+
+    def close(self) -> None:
+        if self._h:
+            _ffi.load().qw35_hip_runtime_destroy(self._h)
+            self._h = None
 
     def __del__(self):
         try:

@@ -58,6 +58,55 @@ def test_struct_layout_matches_header(tmp_path):
     assert [int(v) for v in b.split()] == [C.sizeof(w), w.rows.offset, w.bytes.offset, w.type_id.offset]
 
 
+def test_runtime_struct_layouts_match_header(tmp_path):
+    """qw35_hip_hparams (the reference's qw35_metal_hparams, Qw35MetalTypes.h:30-59:
+    96 bytes, n_cls_out last) and qw35_hip_plan_op against their ctypes mirrors."""
+    src = tmp_path / "layout2.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "qw35_hip.h"\n'
+        "int main(void){\n"
+        'printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(qw35_hip_hparams), offsetof(qw35_hip_hparams, rope_sections),'
+        " offsetof(qw35_hip_hparams, rope_freq_base), offsetof(qw35_hip_hparams, ssm_inner_size),"
+        " offsetof(qw35_hip_hparams, full_attention_interval), offsetof(qw35_hip_hparams, attn_gate),"
+        " offsetof(qw35_hip_hparams, n_cls_out));\n"
+        'printf("%zu %zu %zu %zu\\n", sizeof(qw35_hip_plan_op), offsetof(qw35_hip_plan_op, dst),'
+        " offsetof(qw35_hip_plan_op, token), offsetof(qw35_hip_plan_op, workspace_bytes));\n"
+        'printf("%d %d %d %d\\n", (int)QW35_HIP_LOGITS_NONE, (int)QW35_HIP_LOGITS_ARGMAX, (int)QW35_HIP_LOGITS_FULL,'
+        " (int)QW35_HIP_RT_NBUF);\n"
+        "return 0;}\n"
+    )
+    exe = tmp_path / "layout2"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    a, b, c = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")[:3]
+    h = _ffi.Hparams
+    assert [int(v) for v in a.split()] == [96, 32, 48, 72, 76, 88, 92]
+    assert [int(v) for v in a.split()] == [C.sizeof(h), h.rope_sections.offset, h.rope_freq_base.offset,
+                                           h.ssm_inner_size.offset, h.full_attention_interval.offset,
+                                           h.attn_gate.offset, h.n_cls_out.offset]
+    op = _ffi.PlanOp
+    assert [int(v) for v in b.split()] == [C.sizeof(op), op.dst.offset, op.token.offset, op.workspace_bytes.offset]
+    assert [int(v) for v in c.split()] == [_ffi.LOGITS_NONE, _ffi.LOGITS_ARGMAX, _ffi.LOGITS_FULL, _ffi.RT_NBUF]
+
+
+def test_runtime_create_rejects_bad_inputs_without_a_device(lib):
+    """Argument checks that come before any device work."""
+    hp = _ffi.Hparams()
+    d = _ffi.TensorDesc()
+    img = (C.c_uint8 * 64)()
+    with pytest.raises(_ffi.Qw35Error, match="invalid runtime creation inputs"):
+        _ffi.call("qw35_hip_runtime_create", None, 64, C.byref(d), 1, C.byref(hp), 10, 1)
+    with pytest.raises(_ffi.Qw35Error, match="must be positive"):
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1)
+    hp.transformer_layers, hp.embedding_length, hp.feed_forward_length, hp.n_cls_out = 1, 256, 256, 2
+    with pytest.raises(_ffi.Qw35Error, match="classification heads"):
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1)
+    hp.n_cls_out = 0
+    with pytest.raises(_ffi.Qw35Error, match="max_batch=0"):
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 0)
+    with pytest.raises(_ffi.Qw35Error, match="invalid runtime"):
+        _ffi.call("qw35_hip_runtime_eval_step", None, 1, 2)
+
+
 def _weight(type_id=100, k=4096, rows=16, data=4096, nbytes=None):
     w = _ffi.Weight()
     w.data = data
