@@ -1,26 +1,34 @@
 #!/usr/bin/env python3
-"""Benchmark of the quantized GEMV path on one MI355X.
+"""Benchmark of the quantized GEMV / prefill path on one MI355X.
 
-Headline (BASELINE.json metric, config 1): GF4 decode GEMV, batch 1, W 12288x4096
-= GF4 pack of bf16(0.02 N(0,1)), x fp32 N(0,1).  One "step" is one GEMV launch
-over one weight copy; the launches rotate over 32 distinct weight copies
-(805 MB > the 256 MB Infinity Cache) so every step streams its weights from HBM.
-Weights and activations are made on the GPU (torch's seeded generator, the
-library's own GF4 / q8_0 / Q4_K encoders) and are resident before timing.
+Headline (BASELINE.json metric, config 1): the GF4 decode GEMV, batch 1, W
+12288x4096 = GF4 pack of bf16(0.02 N(0,1)), x fp32 N(0,1).  One "step" is one
+GEMV launch over one weight copy; the launches rotate over 32 distinct weight
+copies (805 MB > the 256 MB Infinity Cache) so every step streams its weights
+from HBM.  Exactly ``--steps`` launches are timed.  Weights and activations are
+made on the GPU (torch's seeded generator, the library's own encoders) and are
+resident before timing; nothing crosses PCIe inside the timed region.
 
-Launches are captured into a hipGraph and replayed; HIP events on the replay
-stream bracket the timed replays.  Printed: one JSON line with the driver's
-contract fields plus ``roofline`` (dominant kernel) and ``cpu_baseline`` (the
-numpy oracle GF4 dequant + matvec on this host's cores), and under ``extra``
-the other configs: GF4 batches 2..8 and the transposed shape, the q8_0 layer
-set (config 2), the Q4_K down / LM-head GEMVs at batch 1 and 8 (config 3), the
-GF4 prefill matmul with its MFMA utilisation (config 4) and the 32-layer 9B
-decode-step projection stack replayed as one recorded plan (config 5).
-``--gpus`` above 1 is refused: this build measures one GPU.
+Launches are captured into hipGraphs and replayed; HIP events recorded on the
+replay stream bracket the timed replays.  Printed: one JSON line with the
+driver's contract fields plus ``roofline`` (the headline kernel) and
+``cpu_baseline`` (the numpy oracle's dequantisation + BLAS matvec on this
+host's cores), and under ``extra`` the other configs, each with its own
+``roofline`` and ``cpu_baseline``: GF4 batches 2..8 and the down-projection
+shape, the q8_0 layer set (config 2), the Q4_K down / LM-head GEMVs at batch 1
+and 8 (config 3), the Q6_K head and greedy head, the GF4 prefill matmul with
+its MFMA utilisation (config 4), and the 32-layer 9B decode-step projection
+stack replayed as one recorded plan (config 5).  ``roofline.traffic`` is the
+PMC-measured HBM bytes per launch from the committed ``profiles/*_traffic.md``
+summary whose kernel line names exactly the instantiation this run launches
+(``qw35_hip_gemv_kernel``), else null.  ``--gpus`` above 1 is refused: this
+build measures one GPU.
 """
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
+import glob
 import json
 import os
 import re
@@ -33,21 +41,52 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gf4_gemv_b1_12288x4096_traffic.md")
+BF16_DENSE_PEAK_TFLOPS = 2500.0
+DTYPE = "gf4/q8_0/q4_k weights as exact f16, f32 activations as f16 hi+lo, f32 accumulate"
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# ---------------------------------------------------------------- rooflines
+
+
+def traffic_for(kernel: str | None) -> int | None:
+    """HBM bytes per launch from the committed PMC summary that names exactly this kernel."""
+    if not kernel:
+        return None
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.md"))):
+        text = open(path).read()
+        for m in re.finditer(r"kernel:\s*`([^`]+)`\s*\ntraffic_bytes_per_launch:\s*(\d+)", text):
+            if re.search(re.escape(kernel) + r"\(", m.group(1)):
+                return int(m.group(2))
+    return None
+
+
+def hbm_roofline(nbytes: float, us: float, kernel: str | None = None) -> dict:
+    gbs = nbytes / (us * 1e3)
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_for(kernel), "kernel": kernel}
+
+
+def mfma_roofline(flops: float, us: float, kernel: str | None = None) -> dict:
+    tf = flops / (us * 1e6)
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_DENSE_PEAK_TFLOPS, 4), "traffic": None, "kernel": kernel}
+
+
+# ---------------------------------------------------------------- GPU timing
+
+
 class Bench:
-    def __init__(self, torch, runtime, seed: int = 1):
+    def __init__(self, torch, rt, seed: int = 1):
         self.torch = torch
-        self.rt = runtime
+        self.rt = rt
         self.dev = torch.device("cuda:0")
         self.gen = torch.Generator(device=self.dev)
         self.gen.manual_seed(seed)
-        self.stream = torch.cuda.Stream()
+        self.stream = torch.cuda.Stream()  # default priority
 
     def normal(self, shape, std=1.0, bf16=False):
         t = self.torch.randn(shape, generator=self.gen, device=self.dev, dtype=self.torch.float32)
@@ -57,116 +96,368 @@ class Bench:
             t = t.to(self.torch.bfloat16).to(self.torch.float32)
         return t
 
-    def weight(self, type_id, rows, k, std=0.02, tile_rows=None):
-        """Encoded N(0, std) weight.  tile_rows: encode that many distinct rows and
-        repeat them (the LM head, whose 1.0e9 fp32 source would not be worth making)."""
+    def weight(self, type_id, rows, k, tile_rows=None):
+        """Encoded N(0, 0.02) weight; tile_rows repeats that many distinct rows (the LM heads)."""
+        from qwowl35_amd import qwen35
+
         if tile_rows is None or tile_rows >= rows:
-            src = self.normal((rows, k), std, bf16=(type_id == self.rt.TYPE_GF4))
-            hw = self.rt.quantize_weight(src, type_id)
-            del src
-            return hw
-        src = self.normal((tile_rows, k), std)
-        part = self.rt.quantize(src, type_id)
+            return qwen35.synthetic_weight(self.gen, type_id, rows, k)
+        part = qwen35.synthetic_weight(self.gen, type_id, tile_rows, k)
         rb = self.rt.row_bytes(type_id, k)
         full = self.torch.empty(rows * rb, dtype=self.torch.uint8, device=self.dev)
         for r0 in range(0, rows, tile_rows):
             n = min(tile_rows, rows - r0)
-            full[r0 * rb:(r0 + n) * rb].copy_(part[:n * rb])
+            full[r0 * rb:(r0 + n) * rb].copy_(part.storage[:n * rb])
         return self.rt.HipWeight.from_device(full, type_id, rows, k)
 
-    def time_calls(self, calls, steps: int, warmup: int):
-        """Graph-capture ``calls`` (one launch each) and replay; returns
-        (ms per launch, ms per graph, launches timed)."""
+    def _graph(self, calls):
         torch = self.torch
-        n = len(calls)
-        with torch.cuda.stream(self.stream):
-            for c in calls:  # first-touch and code-object load outside the capture
-                c(self.stream)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=self.stream):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
             for c in calls:
                 c(self.stream)
-        reps_w = max(1, warmup // n)
-        reps = max(1, steps // n)
+        return g
+
+    def time_launches(self, calls, launches: int, warmup: int):
+        """Time exactly ``launches`` launches, rotating over ``calls`` (one launch
+        each), replayed from graphs; returns (ms per launch, launches)."""
+        torch = self.torch
+        n = len(calls)
+        launches = max(1, int(launches))
         with torch.cuda.stream(self.stream):
-            for _ in range(reps_w):
-                graph.replay()
+            for c in calls:  # first touch and code-object load outside the capture
+                c(self.stream)
+        torch.cuda.synchronize()
+        full = self._graph(calls)
+        reps, rem = divmod(launches, n)
+        part = self._graph(calls[:rem]) if rem else None
+        with torch.cuda.stream(self.stream):
+            for _ in range(max(1, -(-warmup // n))):
+                full.replay()
         torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(self.stream):  # replays and events on the same stream
             ev0.record(self.stream)
             for _ in range(reps):
-                graph.replay()
+                full.replay()
+            if part is not None:
+                part.replay()
             ev1.record(self.stream)
         torch.cuda.synchronize()
-        total = ev0.elapsed_time(ev1)
-        return total / (reps * n), total / reps, reps * n
+        return ev0.elapsed_time(ev1) / launches, launches
+
+    def time_plan(self, plan, reps: int, warmup: int = 3):
+        """ms per replay of a recorded DecodePlan."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                plan.launch(stream=self.stream)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.stream):
+            ev0.record(self.stream)
+            for _ in range(reps):
+                plan.launch(stream=self.stream)
+            ev1.record(self.stream)
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / reps
 
 
-def gemv_calls(rt, weights, x, y):
-    return [lambda s, w=w: rt.decode_matvec(w, x, y, stream=s) for w in weights]
+def gemv_calls(rt, weights, x, y, awq=None):
+    return [lambda s, w=w: rt.decode_matvec(w, x, y, awq=awq, stream=s) for w in weights]
 
 
-def gemv_bytes(type_id, rows, k, nb, rt):
+def gemv_bytes(rt, type_id, rows, k, nb):
     return rows * rt.row_bytes(type_id, k) + 4 * nb * (k + rows)
 
 
-def read_traffic(kernel_hint: str):
-    """HBM bytes per launch from the committed PMC summary, if it names this kernel."""
-    try:
-        text = open(TRAFFIC_PROFILE).read()
-    except OSError:
-        return None, None
-    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
-    k = re.search(r"kernel:\s*`([^`]+)`", text)
-    if not m or not k or kernel_hint not in k.group(1):
-        return None, None
-    return int(m.group(1)), k.group(1)
+def gemv_line(b: Bench, weights, nb, launches, warmup, awq=None) -> dict:
+    """One GEMV configuration: µs per launch, algorithmic GB/s and its roofline."""
+    rt, w0 = b.rt, weights[0]
+    x = b.normal((nb, w0.k))
+    y = b.torch.zeros((nb, w0.rows), dtype=b.torch.float32, device=b.dev)
+    ms, _ = b.time_launches(gemv_calls(rt, weights, x, y, awq), launches, warmup)
+    kern = rt.gemv_kernel(w0, nb, awq=awq is not None)["name"]
+    nbytes = gemv_bytes(rt, w0.type_id, w0.rows, w0.k, nb)
+    return {"us": round(ms * 1e3, 3), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms * 1e3, kern)}
 
 
-def stream_ceiling(b: Bench, rt, torch, bufs) -> dict:
+def stream_ceiling(b: Bench, bufs) -> dict:
     """Streaming-read ceiling on the same box: the library's read probe over the
-    same rotated 25 MB buffers (launch and ramp included, like the GEMV) and
-    over one 1 GiB buffer."""
+    same rotated 25 MB buffers (launch and ramp included, like the GEMV), over
+    one 1 GiB buffer, and over 16 bytes (one workgroup: the per-launch floor)."""
+    rt, torch = b.rt, b.torch
     sinks = [torch.empty(rt.stream_read(bufs[0]).numel(), dtype=torch.int32, device=b.dev) for _ in bufs]
     calls = [lambda s, t=t, k=k: rt.stream_read(t, k, stream=s) for t, k in zip(bufs, sinks)]
-    ms, _, _ = b.time_calls(calls, 2000, 200)
+    ms, _ = b.time_launches(calls, 2000, 200)
     big = torch.zeros(1 << 30, dtype=torch.uint8, device=b.dev)
     sink_big = rt.stream_read(big)
-    ms_big, _, _ = b.time_calls([lambda s: rt.stream_read(big, sink_big, stream=s)], 40, 5)
+    ms_big, _ = b.time_launches([lambda s: rt.stream_read(big, sink_big, stream=s)], 40, 5)
     n = bufs[0].numel()
     tiny = torch.zeros(16, dtype=torch.uint8, device=b.dev)
     sink_tiny = rt.stream_read(tiny)
-    ms_tiny, _, _ = b.time_calls([lambda s: rt.stream_read(tiny, sink_tiny, stream=s)] * 32, 2000, 200)
+    ms_tiny, _ = b.time_launches([lambda s: rt.stream_read(tiny, sink_tiny, stream=s)] * 32, 2000, 200)
     return {"GB/s_25MB": round(n / (ms * 1e-3) / 1e9, 1), "us_25MB": round(ms * 1e3, 3),
-            "GB/s_1GiB": round((1 << 30) / (ms_big * 1e-3) / 1e9, 1),
-            "launch_floor_us": round(ms_tiny * 1e3, 3)}
+            "GB/s_1GiB": round((1 << 30) / (ms_big * 1e-3) / 1e9, 1), "launch_floor_us": round(ms_tiny * 1e3, 3)}
 
 
-BF16_DENSE_PEAK_TFLOPS = 2500.0
-
-
-def mfma_ceiling(b: Bench, rt, torch) -> float:
+def mfma_ceiling(b: Bench) -> float:
     """Sustained fp16 MFMA rate on the same box (TFLOP/s): the library's MFMA
     probe, 4 workgroups (16 waves) per CU, no memory traffic."""
+    rt, torch = b.rt, b.torch
     wg = 4 * torch.cuda.get_device_properties(b.dev).multi_processor_count
     iters = 2000
     sink = torch.empty(wg * 256, dtype=torch.float32, device=b.dev)
-    ms, _, _ = b.time_calls([lambda s: rt.mfma_probe(wg, iters, sink, stream=s)], 10, 2)
+    ms, _ = b.time_launches([lambda s: rt.mfma_probe(wg, iters, sink, stream=s)], 10, 2)
     return wg * iters * rt.MFMA_PROBE_FLOPS_PER_WG_ITER / (ms * 1e-3) / 1e12
 
 
-def bench_prefill(b: Bench, rt, torch) -> dict:
+# ---------------------------------------------------------------- CPU baseline (numpy oracle)
+
+
+def cpu_threads() -> int:
+    """Worker threads for the numpy baseline: the job's CPU share (OMP_NUM_THREADS), else the visible CPUs."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+class CpuBaseline:
+    """The repository's numpy CPU path: the oracle's vectorised dequantisation
+    (rows split over ``threads`` workers; numpy releases the GIL) into an fp32
+    matrix, then BLAS ``W @ x`` (float32).  Dequantisation and product are timed
+    separately with perf_counter, median of ``reps`` after one warm-up."""
+
+    def __init__(self, threads: int, reps: int):
+        self.threads = threads
+        self.reps = reps
+        self.pool = cf.ThreadPoolExecutor(max_workers=threads)
+        try:
+            from threadpoolctl import threadpool_info
+
+            self.blas = max([int(p.get("num_threads", 1)) for p in threadpool_info()] or [1])
+        except Exception:  # noqa: BLE001
+            self.blas = 1
+
+    def dequant(self, type_id, raw: np.ndarray, rows: int, k: int, out: np.ndarray) -> None:
+        from oracle import matvec as om
+
+        rb = raw.size // rows
+        raw2 = raw.reshape(rows, rb)
+        step = -(-rows // self.threads)
+
+        def job(r0):
+            r1 = min(rows, r0 + step)
+            out[r0:r1] = om.dequant(type_id, raw2[r0:r1], r1 - r0, k)
+
+        list(self.pool.map(job, range(0, rows, step)))
+
+    def gemv(self, type_id, raw: np.ndarray, rows: int, k: int, nb: int, seed: int = 0) -> tuple[float, float]:
+        """(seconds of dequantisation, seconds of W @ X) per call, medians."""
+        x = np.random.default_rng(seed).standard_normal((k, nb), dtype=np.float32)
+        w = np.empty((rows, k), dtype=np.float32)
+        self.dequant(type_id, raw, rows, k, w)
+        _ = w @ x
+        t_dq, t_mv = [], []
+        for _ in range(self.reps):
+            t0 = time.perf_counter()
+            self.dequant(type_id, raw, rows, k, w)
+            t1 = time.perf_counter()
+            _ = w @ x
+            t2 = time.perf_counter()
+            t_dq.append(t1 - t0)
+            t_mv.append(t2 - t1)
+        return float(np.median(t_dq)), float(np.median(t_mv))
+
+    def matmul(self, type_id, raw: np.ndarray, rows: int, k: int, m: int, seed: int = 0) -> tuple[float, float]:
+        """(dequantisation s, fp32 W @ A^T s) for an m-token chunk (the prefill baseline)."""
+        a = np.random.default_rng(seed).standard_normal((k, m), dtype=np.float32)
+        w = np.empty((rows, k), dtype=np.float32)
+        self.dequant(type_id, raw, rows, k, w)
+        _ = w @ a
+        t_dq, t_mm = [], []
+        for _ in range(self.reps):
+            t0 = time.perf_counter()
+            self.dequant(type_id, raw, rows, k, w)
+            t1 = time.perf_counter()
+            _ = w @ a
+            t2 = time.perf_counter()
+            t_dq.append(t1 - t0)
+            t_mm.append(t2 - t1)
+        return float(np.median(t_dq)), float(np.median(t_mm))
+
+    def record(self, value, unit, sample: str) -> dict:
+        return {"value": value, "unit": unit, "cores": self.threads, "kind": "port",
+                "sample": f"{sample}; numpy oracle dequantisation on {self.threads} threads + BLAS ({self.blas} "
+                          f"threads), median of {self.reps}; {cpu_model()}, {os.cpu_count()} logical CPUs visible"}
+
+
+def host_bytes(w) -> np.ndarray:
+    return w.storage.cpu().numpy()
+
+
+# ---------------------------------------------------------------- configs
+
+
+def bench_gf4_extra(b: Bench, weights, cpu: CpuBaseline | None, steps: int, warmup: int) -> dict:
+    """GF4 12288x4096 at batch 2, 4, 8 (same rotated copies as the headline) and
+    4096x12288 (the FFN down projection) at batch 1 and 8."""
+    rt, out = b.rt, {}
+    for nb in (2, 4, 8):
+        out[f"gf4_b{nb}_12288x4096"] = gemv_line(b, weights, nb, steps // 2, warmup)
+    down = [b.weight(rt.TYPE_GF4, 4096, 12288) for _ in range(32)]
+    for nb in (1, 8):
+        line = gemv_line(b, down, nb, steps // 2, warmup)
+        if cpu is not None:
+            t_dq, t_mv = cpu.gemv(rt.TYPE_GF4, host_bytes(down[0]), 4096, 12288, nb)
+            line["cpu_baseline"] = cpu.record(round(line["bytes"] / (t_dq + t_mv) / 1e9, 3), "GB/s",
+                                              f"GF4 4096x12288 b{nb}: dequant {t_dq * 1e3:.1f} ms + matvec "
+                                              f"{t_mv * 1e3:.2f} ms per call")
+        out[f"gf4_b{nb}_4096x12288"] = line
+    del down
+    return out
+
+
+Q8_LAYER = [(8192, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096), (4096, 12288)]
+
+
+def bench_q8_layer(b: Bench, cpu: CpuBaseline | None, steps: int, warmup: int) -> dict:
+    """Config 2: q8_0 projections of one decoder layer (q 8192, k / v 1024, o 4096,
+    gate / up 12288 rows x 4096; down 4096 x 12288), batch 1, 3 distinct sets (670 MB)."""
+    rt, torch = b.rt, b.torch
+    sets = [[b.weight(rt.TYPE_Q8_0, r, k) for r, k in Q8_LAYER] for _ in range(3)]
+    acts = {k: b.normal((1, k)) for k in (4096, 12288)}
+    outs = {r: torch.zeros((1, r), dtype=torch.float32, device=b.dev) for r, _ in Q8_LAYER}
+    calls = [lambda s, w=w: rt.decode_matvec(w, acts[w.k], outs[w.rows], stream=s) for st in sets for w in st]
+    ms, _ = b.time_launches(calls, max(len(calls), steps // 2), warmup)
+    set_bytes = sum(gemv_bytes(rt, rt.TYPE_Q8_0, r, k, 1) for r, k in Q8_LAYER)
+    set_us = ms * 1e3 * len(Q8_LAYER)
+    per_matrix = {f"{r}x{k}": rt.gemv_kernel(w, 1)["name"] for (r, k), w in zip(Q8_LAYER, sets[0])}
+    out = {"q8_0_layer_set_b1": {"us_per_set": round(set_us, 3), "bytes": set_bytes, "kernels": per_matrix,
+                                 "roofline": hbm_roofline(set_bytes, set_us)}}
+    # The same sets as one recorded plan, each projection reading the input it
+    # has in a layer: q/k/v share the attention input and gate/up the FFN input,
+    # so each group is one merged launch (4 per set).
+    xin = {name: b.normal((1, k)) for name, k in (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 12288))}
+    role = ["attn", "attn", "attn", "o", "ffn", "ffn", "down"]
+    ys = [torch.zeros((1, r), dtype=torch.float32, device=b.dev) for r, _ in Q8_LAYER]
+    plan = rt.DecodePlan()
+    for st in sets:
+        for w, r, y in zip(st, role, ys):
+            plan.matvec(w, xin[r], y)
+    plan.record()
+    plan_us = b.time_plan(plan, max(20, steps // 40)) * 1e3 / len(sets)
+    plan.close()
+    line = {"us_per_set": round(plan_us, 3), "merged": "q/k/v, o, gate/up, down", "bytes": set_bytes,
+            "roofline": hbm_roofline(set_bytes, plan_us)}
+    if cpu is not None:
+        t = 0.0
+        parts = []
+        for (r, k), w in zip(Q8_LAYER, sets[0]):
+            t_dq, t_mv = cpu.gemv(rt.TYPE_Q8_0, host_bytes(w), r, k, 1)
+            t += t_dq + t_mv
+            parts.append(f"{r}x{k} {1e3 * (t_dq + t_mv):.1f} ms")
+        line["cpu_baseline"] = cpu.record(round(set_bytes / t / 1e9, 3), "GB/s",
+                                          f"the 7 q8_0 matrices at full size, b1 ({', '.join(parts)})")
+        out["q8_0_layer_set_b1"]["cpu_baseline"] = line["cpu_baseline"]
+    out["q8_0_layer_set_b1_plan"] = line
+    del sets
+    return out
+
+
+def bench_q4k(b: Bench, cpu: CpuBaseline | None, steps: int, warmup: int) -> dict:
+    """Config 3: Q4_K down 4096x12288 (24 copies) and LM head 248320x4096, batch 1 and 8."""
+    rt = b.rt
+    out = {}
+    down = [b.weight(rt.TYPE_Q4_K, 4096, 12288) for _ in range(24)]
+    head = b.weight(rt.TYPE_Q4_K, 248320, 4096, tile_rows=16384)
+    for nb in (1, 8):
+        out[f"q4_k_down_b{nb}_4096x12288"] = gemv_line(b, down, nb, steps // 4, warmup // 2)
+        out[f"q4_k_head_b{nb}_248320x4096"] = gemv_line(b, [head], nb, 200, 20)
+        if cpu is not None:
+            t_dq, t_mv = cpu.gemv(rt.TYPE_Q4_K, host_bytes(down[0]), 4096, 12288, nb)
+            line = out[f"q4_k_down_b{nb}_4096x12288"]
+            line["cpu_baseline"] = cpu.record(round(line["bytes"] / (t_dq + t_mv) / 1e9, 3), "GB/s",
+                                              f"Q4_K 4096x12288 b{nb}: dequant {t_dq * 1e3:.1f} ms + matvec "
+                                              f"{t_mv * 1e3:.2f} ms per call")
+            # head: a sample of 1/8 of the rows (31040 x 4096), time scaled by 8
+            rows = 248320 // 8
+            raw = host_bytes(head)[: rows * rt.row_bytes(rt.TYPE_Q4_K, 4096)]
+            t_dq, t_mv = cpu.gemv(rt.TYPE_Q4_K, raw, rows, 4096, nb)
+            line = out[f"q4_k_head_b{nb}_248320x4096"]
+            line["cpu_baseline"] = cpu.record(round(line["bytes"] / (8 * (t_dq + t_mv)) / 1e9, 3), "GB/s",
+                                              f"Q4_K head b{nb}: 31040 of the 248320 rows (dequant "
+                                              f"{t_dq * 1e3:.1f} ms + matvec {t_mv * 1e3:.2f} ms), scaled by 8")
+    del down, head
+    return out
+
+
+def bench_q6k_head(b: Bench, steps: int) -> dict:
+    """The 9B LM head as the reference requires it (Q6_K, 248320 x 4096,
+    Qw35MetalRuntime.m:202-208): the full-logits GEMV and the fused greedy
+    head (GEMV + per-workgroup argmax + reduction, no logits written), b1 and b8."""
+    rt, torch = b.rt, b.torch
+    vocab, hidden = 248320, 4096
+    head = b.weight(rt.TYPE_Q6_K, vocab, hidden, tile_rows=16384)
+    wbytes = head.storage.numel()
+    out = {}
+    for nb in (1, 8):
+        out[f"q6_k_head_b{nb}_248320x4096"] = gemv_line(b, [head], nb, 200, 20)
+        x = b.normal((nb, hidden))
+        ws = rt.output_argmax_workspace(head, nb, device=b.dev)
+        ms, _ = b.time_launches([lambda s: rt.output_argmax(head, x, workspace=ws, stream=s)], 200, 20)
+        nbytes = wbytes + 4 * nb * hidden
+        out[f"q6_k_greedy_head_b{nb}"] = {"us_two_launches": round(ms * 1e3, 3), "bytes": nbytes,
+                                          "roofline": hbm_roofline(nbytes, ms * 1e3)}
+    return out
+
+
+def bench_codecs(b: Bench, steps: int, warmup: int) -> dict:
+    """Every decode-GEMV codec on one 12288x4096 projection at batch 1 and 8,
+    rotating enough copies (>= 640 MB) that the last-level cache holds none."""
+    rt, out = b.rt, {}
+    names = {"gf4": rt.TYPE_GF4, "gf2": rt.TYPE_GF2, "q8_0": rt.TYPE_Q8_0, "q4_k": rt.TYPE_Q4_K,
+             "q5_k": rt.TYPE_Q5_K, "q6_k": rt.TYPE_Q6_K}
+    for name, t in names.items():
+        copies = max(2, -(-(640 << 20) // (12288 * rt.row_bytes(t, 4096))))
+        ws = [b.weight(t, 12288, 4096) for _ in range(copies)]
+        for nb in (1, 8):
+            out[f"codec_{name}_b{nb}_12288x4096"] = gemv_line(b, ws, nb, steps, warmup)
+        del ws
+    return out
+
+
+def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
     """Config 4: GF4 prefill dequant-matmul, W 12288x4096 and 4096x12288 (12
     rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out; the staged
     path (workspace, fp16 MFMA; the time includes the staging pass) and the
     direct path (bf16 MFMA).  Then the q8_0 projections through their fp16
-    prefill image (6 rotated copies).  Utilisation is reported against the
-    nominal 2.5 PFLOP/s and against the MFMA probe's sustained rate on this box."""
-    ceiling = mfma_ceiling(b, rt, torch)
+    prefill image (6 rotated copies).  Utilisation is against the nominal
+    2.5 PFLOP/s and against the MFMA probe's sustained rate on this box."""
+    rt, torch = b.rt, b.torch
+    ceiling = mfma_ceiling(b)
     out = {"mfma_probe_TFLOP/s": round(ceiling, 1)}
+
+    def line(ms, m, rows, k, kern):
+        flops = 2.0 * m * rows * k
+        r = {"us": round(ms * 1e3, 2), "roofline": mfma_roofline(flops, ms * 1e3, kern)}
+        r["frac_of_probe"] = round(flops / (ms * 1e-3) / 1e12 / ceiling, 4)
+        return r
+
     for rows, k in ((12288, 4096), (4096, 12288)):
         ws = [b.weight(rt.TYPE_GF4, rows, k) for _ in range(12)]
         awq = torch.rand((k,), generator=b.gen, device=b.dev) * 1.5 + 0.5
@@ -174,18 +465,18 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
             a = b.normal((m, k)).to(torch.bfloat16)
             c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
             wsp = rt.prefill_workspace(ws[0], m, device=b.dev)
-            for path, work in (("", wsp), ("_direct", None)):
+            for path, work, kern in (("", wsp, "gf4_prefill_f16_kernel"), ("_direct", None, "gf4_prefill_kernel")):
                 calls = [lambda s, w=w, work=work: rt.matmul_prefill(w, a, awq=awq, dst=c, workspace=work, stream=s)
                          for w in ws]
-                ms, _, _ = b.time_calls(calls, max(24, 4800 // m), 12)
-                tflops = 2.0 * m * rows * k / (ms * 1e-3) / 1e12
-                out[f"prefill_gf4_m{m}_{rows}x{k}{path}"] = {
-                    "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
-                    "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
-                    "frac_of_probe": round(tflops / ceiling, 4)}
+                ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
+                r = line(ms, m, rows, k, kern)
+                if cpu is not None and path == "" and rows == 12288:
+                    t_dq, t_mm = cpu.matmul(rt.TYPE_GF4, host_bytes(ws[0]), rows, k, m)
+                    r["cpu_baseline"] = cpu.record(
+                        round(2.0 * m * rows * k / (t_dq + t_mm) / 1e12, 4), "TFLOP/s",
+                        f"GF4 {rows}x{k}, M={m}: dequant {t_dq * 1e3:.1f} ms + fp32 W@A^T {t_mm * 1e3:.1f} ms")
+                out[f"prefill_gf4_m{m}_{rows}x{k}{path}"] = r
         del ws
-    # k-quant projections (q8_0 attention/SSM q, out): the F16 prefill image,
-    # made once per weight at load time, contracted on fp16 MFMA.
     for rows, k in ((8192, 4096), (4096, 4096)):
         q8 = [b.weight(rt.TYPE_Q8_0, rows, k) for _ in range(6)]
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -199,165 +490,53 @@ def bench_prefill(b: Bench, rt, torch) -> dict:
             c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
             wsp = rt.prefill_workspace(imgs[0], m, device=b.dev)
             calls = [lambda s, w=w: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in imgs]
-            ms, _, _ = b.time_calls(calls, max(24, 4800 // m), 12)
-            tflops = 2.0 * m * rows * k / (ms * 1e-3) / 1e12
-            out[f"prefill_q8_0_f16img_m{m}_{rows}x{k}"] = {
-                "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
-                "mfma_util": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
-                "frac_of_probe": round(tflops / ceiling, 4)}
+            ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
+            out[f"prefill_q8_0_f16img_m{m}_{rows}x{k}"] = line(ms, m, rows, k, "gf4_prefill_f16_kernel")
         del q8, imgs
     return out
 
 
-def bench_q6k_head(b: Bench, rt, torch) -> dict:
-    """The 9B LM head as the reference requires it (Q6_K, 248320 x 4096,
-    qw35-server/src/metal/bridge/Qw35MetalRuntime.m:202-208): the full-logits
-    GEMV and the fused greedy head (qw35_hip_output_argmax: GEMV + per-workgroup
-    argmax + reduction, no logits written) at batch 1 and 8."""
-    vocab, hidden = 248320, 4096
-    head = b.weight(rt.TYPE_Q6_K, vocab, hidden, tile_rows=16384)
-    wbytes = head.storage.numel()
-    out = {}
-    for nb in (1, 8):
-        x = b.normal((nb, hidden))
-        y = torch.zeros((nb, vocab), dtype=torch.float32, device=b.dev)
-        m, _, _ = b.time_calls(gemv_calls(rt, [head], x, y), 200, 20)
-        out[f"q6_k_head_b{nb}_248320x4096"] = {"us": round(m * 1e3, 3),
-                                                "GB/s": round(gemv_bytes(rt.TYPE_Q6_K, vocab, hidden, nb, rt) / m / 1e6, 1)}
-        ws = rt.output_argmax_workspace(head, nb, device=b.dev)
-        m, _, _ = b.time_calls([lambda s: rt.output_argmax(head, x, workspace=ws, stream=s)], 200, 20)
-        out[f"q6_k_greedy_head_b{nb}"] = {"us_two_launches": round(m * 1e3, 3),
-                                          "GB/s": round((wbytes + 4 * nb * hidden) / m / 1e6, 1)}
-    return out
-
-
-def bench_codecs(b: Bench, rt, torch, steps: int, warmup: int) -> dict:
-    """Every decode-GEMV codec on one 12288x4096 projection at batch 1 and 8,
-    rotating enough copies (>= 640 MB) that the 256 MB last-level cache holds none."""
-    out = {}
-    rows, k = 12288, 4096
-    names = {"gf4": rt.TYPE_GF4, "gf2": rt.TYPE_GF2, "q8_0": rt.TYPE_Q8_0, "q4_k": rt.TYPE_Q4_K,
-             "q5_k": rt.TYPE_Q5_K, "q6_k": rt.TYPE_Q6_K}
-    for name, t in names.items():
-        nbytes = rows * rt.row_bytes(t, k)
-        copies = max(2, -(-(640 << 20) // nbytes))
-        ws = [b.weight(t, rows, k) for _ in range(copies)]
-        for nb in (1, 8):
-            x = b.normal((nb, k))
-            y = torch.zeros((nb, rows), dtype=torch.float32, device=b.dev)
-            m, _, _ = b.time_calls(gemv_calls(rt, ws, x, y), steps, warmup)
-            out[f"codec_{name}_b{nb}_12288x4096"] = {"us": round(m * 1e3, 3),
-                                                     "GB/s": round(gemv_bytes(t, rows, k, nb, rt) / m / 1e6, 1)}
-        del ws
-    return out
-
-
-def bench_decode_stack(b: Bench, rt, torch) -> dict:
+def bench_stack(b: Bench, cpu_rates: dict | None) -> dict:
     """Config 5: the 32-layer Qwen3.5-9B decode-step projection stack as one
-    recorded plan (hipGraph): per layer the q8_0 mixer projections (full
-    attention every 4th layer: q 8192, k 1024, v 1024, o 4096 rows; Gated
-    DeltaNet otherwise: qkv 8192, z 4096, beta 32, alpha 32, out 4096 rows; all
-    k = 4096), GF4 fused gate/up/SwiGLU (12288 x 4096) and GF4 down
-    (4096 x 12288, residual), then the Q4_K LM head (248320 x 4096).  Every
-    layer has its own weight buffers (5.2 GB per token)."""
-    hidden, ffn, vocab, layers = 4096, 12288, 248320, 32
-    src = {}
+    recorded plan (hipGraph), in the reference's dispatch order: per layer the
+    q8_0 mixer input projections (merged into one launch), the q8_0 output
+    projection (+= residual), the GF4 fused gate/up/SwiGLU and the GF4 down
+    projection (+= residual); then the Q4_K LM head.  The runtime's buffer
+    sharing (one output buffer per role, no AWQ: the reference folds it into
+    the norms) -- the same plan qw35_hip_runtime_eval_step records.  Every layer
+    has its own weight buffers (5.2 GB per step)."""
+    from qwowl35_amd import qwen35
 
-    def layer_weight(t, rows, k):
-        key = (t, rows, k)
-        if key not in src:
-            src[key] = b.normal((rows, k), 0.02, bf16=(t == rt.TYPE_GF4))
-        return rt.quantize_weight(src[key], t)
-
-    stack = []
-    for il in range(layers):
-        if (il + 1) % 4 == 0:
-            mixer = [layer_weight(rt.TYPE_Q8_0, r, hidden) for r in (8192, 1024, 1024)]
-        else:
-            mixer = [layer_weight(rt.TYPE_Q8_0, r, hidden) for r in (8192, 4096, 32, 32)]
-        out_proj = layer_weight(rt.TYPE_Q8_0, hidden, hidden)
-        ffn_w = [layer_weight(rt.TYPE_GF4, ffn, hidden), layer_weight(rt.TYPE_GF4, ffn, hidden),
-                 layer_weight(rt.TYPE_GF4, hidden, ffn)]
-        stack.append((mixer, out_proj, ffn_w))
-    src.clear()
-    head = b.weight(rt.TYPE_Q4_K, vocab, hidden, tile_rows=16384)
-    total = sum(w.storage.numel() for mixer, o, f in stack for w in (*mixer, o, *f)) + head.storage.numel()
+    hp = qwen35.QWEN35_9B
+    stack = qwen35.ProjectionStack.synthetic(hp, distinct=False, head_tile_rows=16384, device=b.dev)
+    total = stack.weight_bytes
     out = {}
     for nb in (1, 8):
-        x = b.normal((nb, hidden))
-        att = b.normal((nb, hidden))
-        awq = torch.rand((hidden,), generator=b.gen, device=b.dev) * 1.5 + 0.5
-        h = torch.zeros((nb, hidden), dtype=torch.float32, device=b.dev)
-        g = torch.zeros((nb, ffn), dtype=torch.float32, device=b.dev)
-        att_out = [torch.zeros((nb, r), dtype=torch.float32, device=b.dev) for r in (8192, 1024, 1024)]
-        delta_out = [torch.zeros((nb, r), dtype=torch.float32, device=b.dev) for r in (8192, 4096, 32, 32)]
-        logits = torch.zeros((nb, vocab), dtype=torch.float32, device=b.dev)
-        plan = rt.DecodePlan()
-        for mixer, out_proj, (gate, up, down) in stack:
-            outs = att_out if len(mixer) == 3 else delta_out  # q/k/v or qkv/z/beta/alpha
-            for w, o in zip(mixer, outs):
-                plan.matvec(w, x, o)
-            plan.matvec(out_proj, att, h, residual=True)
-            plan.swiglu(gate, up, x, g, awq=awq)
-            plan.matvec(down, g, h, residual=True)
-        plan.matvec(head, x, logits)
-        plan.record()
-        with torch.cuda.stream(b.stream):
-            for _ in range(3):
-                plan.launch(stream=b.stream)
-        torch.cuda.synchronize()
-        reps = 20
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(b.stream):
-            ev0.record(b.stream)
-            for _ in range(reps):
-                plan.launch(stream=b.stream)
-            ev1.record(b.stream)
-        torch.cuda.synchronize()
-        us = ev0.elapsed_time(ev1) * 1e3 / reps
-        out[f"decode_stack_9b_b{nb}"] = {
-            "gemvs": len(plan), "weight_bytes": int(total), "us_per_step": round(us, 1),
-            "us_per_token": round(us / nb, 1), "GB/s": round(total / us / 1e3, 1)}
+        bufs = qwen35.StepBuffers.make(hp, nb, b.gen, awq=False, shared_outputs=True)
+        bufs.ffn_norm = bufs.norm
+        plan = qwen35.build_plan(stack, bufs)
+        us = b.time_plan(plan, 20) * 1e3
+        line = {"gemvs": len(plan), "weight_bytes": int(total), "us_per_step": round(us, 1),
+                "us_per_token": round(us / nb, 1), "roofline": hbm_roofline(total, us)}
+        if cpu_rates is not None:
+            cpu_us = 0.0
+            for il in range(hp.transformer_layers):
+                for p in qwen35.mixer_projections(hp, il):
+                    cpu_us += p.rows * b.rt.row_bytes(stack.types.mixer, p.k) / cpu_rates["q8_0"]
+                for p in qwen35.ffn_projections(hp):
+                    cpu_us += p.rows * b.rt.row_bytes(stack.types.ffn, p.k) / cpu_rates["gf4"]
+            cpu_us += hp.vocab * b.rt.row_bytes(stack.types.head, hp.embedding_length) / cpu_rates["q4_k"]
+            cpu_us *= 1e6
+            line["cpu_baseline"] = {
+                "value": round(cpu_us / nb, 1), "unit": "us/token", "cores": cpu_rates["threads"], "kind": "port",
+                "sample": "the sum over the 217 projections of their weight bytes at the per-codec CPU rates "
+                          f"measured in this run at batch {cpu_rates['nb']} (GF4 {cpu_rates['gf4'] / 1e9:.3f}, q8_0 "
+                          f"{cpu_rates['q8_0'] / 1e9:.3f}, Q4_K {cpu_rates['q4_k'] / 1e9:.3f} GB/s), divided by the "
+                          f"batch; {cpu_model()}"}
+        out[f"decode_stack_9b_b{nb}"] = line
         plan.close()
+    del stack
     return out
-
-
-def cpu_baseline_gf4(rows: int, k: int, seed: int, reps: int):
-    """numpy oracle on the host: GF4 dequant (vectorised numpy) + fp32 W @ x (BLAS)."""
-    from threadpoolctl import threadpool_info
-
-    from oracle import gf4 as ogf4
-    from oracle import matvec as om
-
-    rng = np.random.default_rng(seed)
-    w = om.bf16_round(rng.standard_normal((rows, k), dtype=np.float32) * np.float32(0.02))
-    words = ogf4.gf4_pack(w)
-    x = rng.standard_normal(k, dtype=np.float32)
-    ogf4.gf4_dequant(words) @ x  # warm-up
-    t_dq, t_mv = [], []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        wd = ogf4.gf4_dequant(words)
-        t1 = time.perf_counter()
-        _ = wd @ x
-        t2 = time.perf_counter()
-        t_dq.append(t1 - t0)
-        t_mv.append(t2 - t1)
-    blas = max([int(p.get("num_threads", 1)) for p in threadpool_info()] or [1])
-    return float(np.median(t_dq)), float(np.median(t_mv)), blas
-
-
-def cpu_model() -> str:
-    """The host CPU's model name (the first 'model name' of /proc/cpuinfo)."""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown CPU"
 
 
 def main() -> int:
@@ -366,11 +545,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=4000)
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--copies", type=int, default=32, help="distinct GF4 weight copies rotated (>= 24)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--headline-only", action="store_true", help="skip the extra configs (= --extras none)")
     ap.add_argument("--extras", default="all",
-                    help="comma list of extra configs: gf4,q8,q4k,q6k,codecs,prefill,stack (or all / none)")
-    ap.add_argument("--cpu-reps", type=int, default=40)
+                    help="comma list of extra configs: gf4,q8,q4k,q6k,prefill,stack,codecs (all = every one "
+                         "but codecs; none)")
+    ap.add_argument("--cpu-reps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it (--gpus 1)"}),
@@ -382,8 +562,9 @@ def main() -> int:
     from qwowl35_amd import runtime as rt
 
     b = Bench(torch, rt)
+    cpu = None if args.no_cpu else CpuBaseline(cpu_threads(), args.cpu_reps)
     rows, k = 12288, 4096
-    log(f"config 1: GF4 {rows}x{k} b1, {args.copies} copies")
+    log(f"config 1: GF4 {rows}x{k} b1, {args.copies} copies, {args.steps} timed launches")
     weights = [b.weight(rt.TYPE_GF4, rows, k) for _ in range(args.copies)]
     x = b.normal((1, k))
     y = torch.zeros((1, rows), dtype=torch.float32, device=b.dev)
@@ -392,14 +573,14 @@ def main() -> int:
     torch.cuda.synchronize()
     del calib
 
-    ms, _, launches = b.time_calls(gemv_calls(rt, weights, x, y), args.steps, args.warmup)
-    algo = gemv_bytes(rt.TYPE_GF4, rows, k, 1, rt)
+    ms, launches = b.time_launches(gemv_calls(rt, weights, x, y), args.steps, args.warmup)
+    kern = rt.gemv_kernel(weights[0], 1)["name"]
+    algo = gemv_bytes(rt, rt.TYPE_GF4, rows, k, 1)
     value = algo / (ms * 1e-3) / 1e9
-    log(f"GF4 b1: {ms * 1e3:.3f} us/launch, {value:.0f} GB/s")
-    traffic, traffic_kernel = read_traffic("gf4_mfma_gemv<1,")
+    log(f"GF4 b1: {ms * 1e3:.3f} us/launch, {value:.0f} GB/s ({kern})")
 
-    extra = {}
-    ceil = stream_ceiling(b, rt, torch, [w.storage for w in weights])
+    extra = {"headline_kernel": kern}
+    ceil = stream_ceiling(b, [w.storage for w in weights])
     extra["stream_read_ceiling"] = ceil
     extra["gf4_b1_frac_of_stream_ceiling"] = round(value / ceil["GB/s_25MB"], 4)
     # Best frac of 8 TB/s one dependent launch of these bytes could reach here:
@@ -407,106 +588,39 @@ def main() -> int:
     best_us = ceil["launch_floor_us"] + algo / (ceil["GB/s_1GiB"] * 1e3)
     extra["single_launch_frac_bound"] = round(algo / (best_us * 1e3) / HBM_PEAK_GBS, 4)
     want = set() if args.headline_only or args.extras == "none" else (
-        {"gf4", "q8", "q4k", "q6k", "codecs", "prefill", "stack"} if args.extras == "all"
-        else set(args.extras.split(",")))
+        {"gf4", "q8", "q4k", "q6k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
+
+    cpu_line = None
+    cpu_rates = None
+    if cpu is not None:
+        t_dq, t_mv = cpu.gemv(rt.TYPE_GF4, host_bytes(weights[0]), rows, k, 1)
+        cpu_line = cpu.record(round(algo / (t_dq + t_mv) / 1e9, 3), "GB/s",
+                              f"GF4 12288x4096 b1 at full size: dequant {t_dq * 1e3:.1f} ms + matvec "
+                              f"{t_mv * 1e3:.2f} ms per call")
+        cpu_rates = {"gf4": algo / (t_dq + t_mv), "threads": cpu.threads, "nb": 1}
     if "gf4" in want:
-        for nb in (2, 4, 8):
-            xb = b.normal((nb, k))
-            yb = torch.zeros((nb, rows), dtype=torch.float32, device=b.dev)
-            m, _, _ = b.time_calls(gemv_calls(rt, weights, xb, yb), args.steps // 2, args.warmup)
-            extra[f"gf4_b{nb}_12288x4096"] = {"us": round(m * 1e3, 3),
-                                              "GB/s": round(gemv_bytes(rt.TYPE_GF4, rows, k, nb, rt) / m / 1e6, 1)}
+        extra.update(bench_gf4_extra(b, weights, cpu, args.steps, args.warmup))
     del weights
-    if "gf4" in want:
-        wt = [b.weight(rt.TYPE_GF4, 4096, 12288) for _ in range(args.copies)]
-        xt = b.normal((1, 12288))
-        yt = torch.zeros((1, 4096), dtype=torch.float32, device=b.dev)
-        m, _, _ = b.time_calls(gemv_calls(rt, wt, xt, yt), args.steps // 2, args.warmup)
-        extra["gf4_b1_4096x12288"] = {"us": round(m * 1e3, 3),
-                                      "GB/s": round(gemv_bytes(rt.TYPE_GF4, 4096, 12288, 1, rt) / m / 1e6, 1)}
-        del wt
     if "q8" in want:
-        # config 2: q8_0 projections of one decoder layer, 3 distinct sets (670 MB)
-        shapes = [(8192, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096),
-                  (4096, 12288)]
-        sets = [[b.weight(rt.TYPE_Q8_0, r, kk) for r, kk in shapes] for _ in range(3)]
-        acts = {kk: b.normal((1, kk)) for kk in (4096, 12288)}
-        outs = {r: torch.zeros((1, r), dtype=torch.float32, device=b.dev) for r, _ in shapes}
-        calls = [lambda s, w=w: rt.decode_matvec(w, acts[w.k], outs[w.rows], stream=s) for st in sets for w in st]
-        m, _, _ = b.time_calls(calls, args.steps // 2, args.warmup)
-        per_set_ms = m * len(shapes)
-        set_bytes = sum(gemv_bytes(rt.TYPE_Q8_0, r, kk, 1, rt) for r, kk in shapes)
-        extra["q8_0_layer_set_b1"] = {"us_per_set": round(per_set_ms * 1e3, 3), "bytes": set_bytes,
-                                      "GB/s": round(set_bytes / per_set_ms / 1e6, 1)}
-        # The same sets as one recorded decode plan, each projection reading
-        # the input it has in a layer: q/k/v share the attention input and
-        # gate/up the FFN input, so each group is one launch (4 per set).
-        xin = {name: b.normal((1, kk)) for name, kk in
-               (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 12288))}
-        role = ["attn", "attn", "attn", "o", "ffn", "ffn", "down"]
-        ys = [torch.zeros((1, r), dtype=torch.float32, device=b.dev) for r, _ in shapes]
-        plan = rt.DecodePlan()
-        for st in sets:
-            for w, r, y in zip(st, role, ys):
-                plan.matvec(w, xin[r], y)
-        plan.record()
-        with torch.cuda.stream(b.stream):
-            for _ in range(3):
-                plan.launch(stream=b.stream)
-        torch.cuda.synchronize()
-        reps = max(20, args.steps // 40)
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(b.stream):
-            ev0.record(b.stream)
-            for _ in range(reps):
-                plan.launch(stream=b.stream)
-            ev1.record(b.stream)
-        torch.cuda.synchronize()
-        plan_set_ms = ev0.elapsed_time(ev1) / reps / len(sets)
-        extra["q8_0_layer_set_b1_plan"] = {"us_per_set": round(plan_set_ms * 1e3, 3), "merged": "q/k/v, o, gate/up, down",
-                                           "GB/s": round(set_bytes / plan_set_ms / 1e6, 1)}
-        plan.close()
-        del sets
+        extra.update(bench_q8_layer(b, cpu, args.steps, args.warmup))
     if "q4k" in want:
-        # config 3: Q4_K down 4096x12288 (24 copies) and LM head 248320x4096, batch 1 and 8
-        down = [b.weight(rt.TYPE_Q4_K, 4096, 12288) for _ in range(24)]
-        head = b.weight(rt.TYPE_Q4_K, 248320, 4096, tile_rows=16384)
-        for nb in (1, 8):
-            xd = b.normal((nb, 12288))
-            yd = torch.zeros((nb, 4096), dtype=torch.float32, device=b.dev)
-            m, _, _ = b.time_calls(gemv_calls(rt, down, xd, yd), args.steps // 4, args.warmup // 2)
-            extra[f"q4_k_down_b{nb}_4096x12288"] = {
-                "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 4096, 12288, nb, rt) / m / 1e6, 1)}
-            xh = b.normal((nb, 4096))
-            yh = torch.zeros((nb, 248320), dtype=torch.float32, device=b.dev)
-            m, _, _ = b.time_calls(gemv_calls(rt, [head], xh, yh), 200, 20)
-            extra[f"q4_k_head_b{nb}_248320x4096"] = {
-                "us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(rt.TYPE_Q4_K, 248320, 4096, nb, rt) / m / 1e6, 1)}
-        del down, head
+        extra.update(bench_q4k(b, cpu, args.steps, args.warmup))
     if "q6k" in want:
-        extra.update(bench_q6k_head(b, rt, torch))
+        extra.update(bench_q6k_head(b, args.steps))
     if "codecs" in want:
-        extra.update(bench_codecs(b, rt, torch, args.steps // 4, args.warmup // 2))
+        extra.update(bench_codecs(b, args.steps // 4, args.warmup // 2))
     if "prefill" in want:
-        extra.update(bench_prefill(b, rt, torch))
+        extra.update(bench_prefill(b, cpu))
     if "stack" in want:
-        extra.update(bench_decode_stack(b, rt, torch))
+        if cpu_rates is not None and "q8_0_layer_set_b1" in extra and "q4_k_head_b1_248320x4096" in extra:
+            cpu_rates["q8_0"] = extra["q8_0_layer_set_b1"]["cpu_baseline"]["value"] * 1e9
+            cpu_rates["q4_k"] = extra["q4_k_head_b1_248320x4096"]["cpu_baseline"]["value"] * 1e9
+        else:
+            cpu_rates = None
+        extra.update(bench_stack(b, cpu_rates))
     for key, v in extra.items():
         log(f"{key}: {v}")
 
-    cpu = None
-    if not args.no_cpu:
-        t_dq, t_mv, blas = cpu_baseline_gf4(rows, k, seed=1, reps=args.cpu_reps)
-        cpu = {
-            "value": round(algo / (t_dq + t_mv) / 1e9, 3),
-            "unit": "GB/s",
-            "cores": blas,
-            "kind": "port",
-            "sample": f"numpy oracle on the host: GF4 dequant of the 12288x4096 b1 weight (1 thread, "
-                      f"{t_dq * 1e3:.1f} ms) + fp32 W@x ({blas} BLAS threads, {t_mv * 1e3:.2f} ms), "
-                      f"median of {args.cpu_reps}; {cpu_model()}, {os.cpu_count()} logical CPUs visible",
-        }
     out = {
         "metric": "GF4 b1 matvec HBM GB/s (12288x4096)",
         "value": round(value, 2),
@@ -518,13 +632,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "gf4-weights/fp32-acc",
+        "dtype": DTYPE,
         "data": "synthetic",
         "config": {"workload": "gf4_matvec_b1_12288x4096", "rows": rows, "k": k, "batch": 1,
                    "weight_copies": args.copies},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic},
-        "cpu_baseline": cpu,
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_for(kern)},
+        "cpu_baseline": cpu_line,
         "extra": extra,
     }
     print(json.dumps(out), flush=True)

@@ -149,6 +149,16 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weig
                                 const float *awq, float *dst, uint32_t n_batch, void *stream, char *err,
                                 uintptr_t err_len);
 
+/* The kernel a qw35_hip_decode_matvec (w_up NULL) or qw35_hip_ffn_gate_up_swiglu
+ * (w_up set) call with this weight, batch and AWQ presence launches, named as
+ * the profiler names it (e.g. "gf4_mfma_gemv<1, 3, 8, 2, false, false, true>"),
+ * with its grid, workgroup size and LDS bytes; nothing is launched.  For a
+ * batch the GF4 kernel splits, its first launch.  No counterpart in the
+ * reference: it matches measurements and tests to the launch plan. */
+int qw35_hip_gemv_kernel(const qw35_hip_weight *w, const qw35_hip_weight *w_up, uint32_t n_batch, int has_awq,
+                         char *name, uintptr_t name_len, uint32_t *grid, uint32_t *block, uint32_t *lds_bytes,
+                         char *err, uintptr_t err_len);
+
 /* Greedy LM head: per batch row b, the largest of
  *   logit[r] = sum_k W[r][k] * awq[k] * x[b][k]
  * over the rows r, written as token[b] = r (uint32) and logit[b], without

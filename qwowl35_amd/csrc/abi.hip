@@ -284,6 +284,27 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight* gate, const qw35_hip_weig
                : 0;
 }
 
+int qw35_hip_gemv_kernel(const qw35_hip_weight* w, const qw35_hip_weight* w_up, uint32_t n_batch, int has_awq,
+                         char* name, uintptr_t name_len, uint32_t* grid, uint32_t* block, uint32_t* lds_bytes,
+                         char* err, uintptr_t err_len) {
+    // Stand-in addresses for the validation: nothing is launched or read.
+    const float* fake = reinterpret_cast<const float*>(uintptr_t{256});
+    const float* awq = has_awq ? fake : nullptr;
+    float* dst = const_cast<float*>(fake);
+    const bool ok = w_up ? check_swiglu(w, w_up, fake, awq, dst, n_batch, "gemv_kernel", err, err_len)
+                         : check_matvec(w, fake, awq, dst, n_batch, "gemv_kernel", err, err_len);
+    if (!ok) return 0;
+    qw35::LaunchInfo info{};
+    qw35::GemvArgs a = gemv_args(w, w_up, fake, awq, dst, n_batch, 0);
+    a.info = &info;
+    if (!check_hip(dispatch_gemv(w->type_id, a, nullptr), "gemv_kernel", err, err_len)) return 0;
+    if (name && name_len) snprintf(name, (size_t)name_len, "%s", info.name);
+    if (grid) *grid = info.grid;
+    if (block) *block = info.block;
+    if (lds_bytes) *lds_bytes = info.lds;
+    return 1;
+}
+
 void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* err, uintptr_t err_len) {
     if (!ops || n_ops == 0) {
         set_err(err, err_len, "plan_create: no ops");

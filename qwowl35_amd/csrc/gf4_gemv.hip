@@ -41,6 +41,8 @@
 #include "qw35_device.h"
 #include "qw35_kernels.h"
 
+#include <stdio.h>
+
 #include <type_traits>
 
 namespace qw35 {
@@ -393,6 +395,14 @@ hipError_t launch_cfg(const GemvArgs& a, hipStream_t stream) {
     const size_t lds = lds_bytes<NB, RT, KS, CPW, SWIGLU, BD>();
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
     const int grid = (a.rows + 16 * RT - 1) / (16 * RT);
+    if (a.info) {
+        snprintf(a.info->name, sizeof a.info->name, "gf4_mfma_gemv<%d, %d, %d, %d, %s, %s, %s>", NB, RT, KS, CPW,
+                 SWIGLU ? "true" : "false", a.awq ? "true" : "false", BD ? "true" : "false");
+        a.info->grid = (unsigned)grid;
+        a.info->block = 64u * KS;
+        a.info->lds = (unsigned)lds;
+        return hipSuccess;
+    }
     if (a.awq) {
         hipLaunchKernelGGL((gf4_mfma_gemv<NB, RT, KS, CPW, SWIGLU, true, BD>), dim3(grid), dim3(64 * KS), lds, stream,
                            a);
@@ -478,6 +488,7 @@ hipError_t launch_gf4_any(const GemvArgs& a, hipStream_t stream) {
         else if (s.n_batch <= 4) e = launch_nb<4, SWIGLU>(s, stream);
         else e = launch_nb<8, SWIGLU>(s, stream);
         if (e != hipSuccess) return e;
+        if (a.info) break;  // describe the first slice's launch only
     }
     return hipSuccess;
 }

@@ -78,7 +78,7 @@ hipError_t launch_argmax_gemv(uint32_t type_id, const GemvArgs& a, uint32_t* tok
         case kTypeQ6_K: e = launch_q6_k_gemv(a, stream); break;
         default: e = kq_gf4_plain(a, stream); break;
     }
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.info) return e;
     const int groups = argmax_groups(type_id, a.rows, a.k, a.n_batch);
     hipLaunchKernelGGL(argmax_reduce_kernel, dim3(a.n_batch), dim3(kArgmaxThreads), 0, stream, a.am_token,
                        a.am_logit, groups, a.n_batch, token, logit);

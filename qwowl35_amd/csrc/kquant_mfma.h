@@ -56,6 +56,8 @@
 #include "qw35_device.h"
 #include "qw35_kernels.h"
 
+#include <stdio.h>
+
 #include <type_traits>
 namespace qw35 {
 
@@ -750,6 +752,14 @@ hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
     // The greedy head's partial workspace holds argmax_groups() entries per
     // batch row: refuse a launch shape with more workgroups than that.
     if (a.am_token && grid != argmax_groups(Fmt<FMT>::kTypeId, a.rows, a.k, a.n_batch)) return hipErrorInvalidValue;
+    if (a.info) {
+        snprintf(a.info->name, sizeof a.info->name, "kq_mfma_gemv<%d, %d, %d, %d, %d, %d, %s, %s>", FMT, NB, RT, KS,
+                 CPW, P, SWIGLU ? "true" : "false", a.awq ? "true" : "false");
+        a.info->grid = (unsigned)grid;
+        a.info->block = 64u * KS;
+        a.info->lds = (unsigned)lds;
+        return hipSuccess;
+    }
     if (a.awq)
         hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds,
                            stream, a);

@@ -23,6 +23,15 @@ constexpr int kMaxDecodeBatch = 8;
 // (q8_0 / Q4_K kernels): segment s covers the rows of seg_w[s], written to seg_y[s].
 constexpr int kMaxSegments = 4;
 
+// Filled instead of launching when GemvArgs::info is set: the kernel
+// instantiation as the profiler names it, and its launch shape.
+struct LaunchInfo {
+    char name[160];
+    unsigned grid;
+    unsigned block;
+    unsigned lds;
+};
+
 struct GemvArgs {
     const void* w;        // raw tensor bytes, row-major, rows x row_bytes
     const float* x;       // [n_batch][k]
@@ -43,6 +52,9 @@ struct GemvArgs {
     // am_logit / am_token[blockIdx.x * n_batch + b].
     uint32_t* am_token;
     float* am_logit;
+    // Host pointer: when set, the launchers describe the (first) launch here
+    // and launch nothing.
+    LaunchInfo* info;
 };
 
 // Each launcher validates nothing (the C ABI does) and returns the launch status.

@@ -263,6 +263,16 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
     return dst
 
 
+def gemv_kernel(w: HipWeight, n_batch: int = 1, w_up: HipWeight | None = None, awq: bool = False) -> dict:
+    """The kernel a ``decode_matvec`` (or, with ``w_up``, ``ffn_gate_up_swiglu``)
+    call launches: ``{"name", "grid", "block", "lds"}`` (``qw35_hip_gemv_kernel``)."""
+    name = C.create_string_buffer(160)
+    g, b, l = C.c_uint32(), C.c_uint32(), C.c_uint32()
+    _ffi.call("qw35_hip_gemv_kernel", C.byref(w.view), C.byref(w_up.view) if w_up is not None else None, n_batch,
+              int(bool(awq)), name, C.sizeof(name), C.byref(g), C.byref(b), C.byref(l))
+    return {"name": name.value.decode(), "grid": g.value, "block": b.value, "lds": l.value}
+
+
 def output_argmax_workspace(w: HipWeight, n_batch: int, device="cuda") -> torch.Tensor:
     """Device bytes for ``output_argmax`` (size from the C ABI, +256 for alignment)."""
     need = int(_ffi.load().qw35_hip_output_argmax_workspace_size(C.byref(w.view), n_batch))

@@ -128,19 +128,30 @@ def test_gf4_gate_up_swiglu_12288(cuda, gf4_ffn, nb):
     assert om.rel_l2(y, om.swiglu_f64(dg, du, x, a)) <= GEMV_REL_L2
 
 
+@pytest.mark.parametrize("awq", [True, False])
 @pytest.mark.parametrize("nb", [1, 2, 4, 8])
-def test_gf4_down_residual_4096x12288(cuda, gf4_ffn, nb):
+def test_gf4_down_residual_4096x12288(cuda, gf4_ffn, nb, awq):
     import torch
 
     rng = np.random.default_rng(400 + nb)
     x = rng.standard_normal((nb, 12288), dtype=np.float32)
-    a = rng.uniform(0.5, 2.0, 12288).astype(np.float32)
+    a = rng.uniform(0.5, 2.0, 12288).astype(np.float32) if awq else None
     base = rng.standard_normal((nb, 4096)).astype(np.float32)
     w, deq = gf4_ffn["down"]
     dst = torch.from_numpy(base.copy()).to(cuda)
-    _rt().decode_matvec(w, _t(x, cuda), dst=dst, residual=True, awq=_t(a, cuda))
+    _rt().decode_matvec(w, _t(x, cuda), dst=dst, residual=True, awq=_t(a, cuda) if awq else None)
     want = base.astype(np.float64) + om.matvec_f64(deq, x, a)
     assert om.rel_l2(dst.cpu().numpy(), want) <= GEMV_REL_L2
+
+
+@pytest.mark.parametrize("nb", [1, 2, 4, 8])
+def test_gf4_plain_12288x4096(cuda, gf4_ffn, nb):
+    """The GF4 12288 x 4096 GEMV without SwiGLU or AWQ (config 1 and its batches)."""
+    rng = np.random.default_rng(450 + nb)
+    x = rng.standard_normal((nb, 4096), dtype=np.float32)
+    w, deq = gf4_ffn["gate"]
+    y = _rt().decode_matvec(w, _t(x, cuda)).cpu().numpy()
+    assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
 
 
 def _outlier_x(rng, nb, k, frac=0.01, gain=100.0):

@@ -47,8 +47,9 @@ def _rel(got, want):
     return om.rel_l2(got.cpu().numpy(), want.cpu().numpy())
 
 
+@pytest.mark.parametrize("awq", [True, False])
 @pytest.mark.parametrize("nb", [1, 8])
-def test_stack9b_every_output(cuda, stack9b, nb):
+def test_stack9b_every_output(cuda, stack9b, nb, awq):
     import torch
 
     from qwowl35_amd import qwen35
@@ -56,18 +57,18 @@ def test_stack9b_every_output(cuda, stack9b, nb):
     hp = stack9b.hp
     gen = torch.Generator(device=cuda)
     gen.manual_seed(100 + nb)
-    bufs = qwen35.StepBuffers.make(hp, nb, gen, awq=True, shared_outputs=False)
+    bufs = qwen35.StepBuffers.make(hp, nb, gen, awq=awq, shared_outputs=False)
     act0 = bufs.act.clone()
     plan = qwen35.build_plan(stack9b, bufs)
     assert len(plan) == qwen35.gemv_count(hp) == 217
-    print(f"stack9b nb={nb}: launching the recorded plan", flush=True)
+    print(f"stack9b nb={nb} awq={awq}: launching the recorded plan", flush=True)
     plan.launch()
     torch.cuda.synchronize()
     first = {"act": bufs.act.clone(), "logits": bufs.logits.clone(),
              "ffn_act": [a.clone() for a in bufs.ffn_act]}
 
     x = bufs.norm.double().T
-    fx = (bufs.ffn_norm.double() * bufs.awq.double()).T
+    fx = (bufs.ffn_norm.double() * (bufs.awq.double() if awq else 1.0)).T
     want_act = act0.double().clone()
     worst = 0.0
     for il, ws in enumerate(stack9b.layers):
