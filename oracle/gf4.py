@@ -105,6 +105,35 @@ def gf4_dequant(words: np.ndarray) -> np.ndarray:
     return vals.reshape(*w.shape[:-1], w.shape[-1] * 8).astype(np.float32)
 
 
+def gf4_dequant_metal(words: np.ndarray) -> np.ndarray:
+    """GF4 words [R, G] -> fp32 [R, 8G] as the reference's Metal decoder computes them.
+
+    ``qw35_gf4_dot8_vec_f32`` / ``qw35_dequantize_gf4`` (``qw35_gf4.metal:8-20,41-58``)
+    repack the codes as ``packed = (w & 0xfff00000) | ((w >> 4) & 0x0000fff0)``,
+    shift by ``9 - 3i`` and read the two 16-bit halves as signed shorts, masking
+    with ``0xe000e000`` for ``i != 0`` only, and scale by
+    ``fp16(b << 8) * -0.25 * 2^-13``.  Elements 0..3 and 5..7 equal
+    ``gf4_dequant``; element 4's high short keeps, below its code, the bits of
+    codes 1..3, so it is ``gf4_dequant``'s value minus
+    ``s/4 * (c1 | c2 << 3 | c3 << 6) / 8192``.  Test infrastructure: this build
+    follows the cook formula (``gf4_dequant``); this form measures the
+    difference to the reference server's kernels.
+    """
+    w = np.asarray(words, dtype=np.uint32)
+    packed = ((w & np.uint32(0xFFF00000)) | ((w >> np.uint32(4)) & np.uint32(0x0000FFF0))).astype(np.uint32)
+    scale = (e5m2_byte_to_fp32((w & np.uint32(0xFF)).astype(np.uint8)) * _F32(-0.25) * _F32(2.0 ** -13))
+    out = np.empty(w.shape + (8,), dtype=np.float32)
+    for i in range(4):
+        shifted = (packed << np.uint32(9 - 3 * i)) & np.uint32(0xFFFFFFFF)
+        if i != 0:
+            shifted &= np.uint32(0xE000E000)
+        lo = (shifted & np.uint32(0xFFFF)).astype(np.uint16).view(np.int16).astype(np.float32)
+        hi = (shifted >> np.uint32(16)).astype(np.uint16).view(np.int16).astype(np.float32)
+        out[..., i] = lo * scale
+        out[..., i + 4] = hi * scale
+    return out.reshape(*w.shape[:-1], w.shape[-1] * 8)
+
+
 def gf4_nbytes(rows: int, k: int) -> int:
     """Tensor byte size, ``tensor_nbytes(100, n)`` (``loader/tensors.rs:165-167``)."""
     return rows * ((k + 7) // 8) * 4

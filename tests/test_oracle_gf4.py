@@ -14,6 +14,8 @@ import numpy as np
 import pytest
 
 from oracle import gf4
+from oracle import matvec as om
+from tests.helpers import random_gf4_words
 
 
 def e5m2_closed_form(b: int) -> float:
@@ -172,3 +174,47 @@ def test_gf4_nbytes_matches_loader_rule():
     # tensor_nbytes(100, n) = ceil(n/8) * 4 (qw35-server/src/loader/tensors.rs:165-167)
     assert gf4.gf4_nbytes(12288, 4096) == 25_165_824
     assert gf4.gf4_nbytes(4096, 12288) == 25_165_824
+
+
+def test_metal_form_hand_word():
+    """Scale byte 0x3C (s = 1.0), codes c0..c7 = 1, 2, 3, 4, 5, 6, 7, 0.  By hand:
+    element i = -sext3(c_i) / 4 (c = 4 -> +1.0, c = 5 -> +0.75, c = 7 -> +0.25),
+    and the Metal element 4 = 0.75 - (2 | 3 << 3 | 4 << 6) / 8192 / 4 = 0.74139404296875."""
+    codes = [1, 2, 3, 4, 5, 6, 7, 0]
+    word = 0x3C
+    for i, c in enumerate(codes):
+        word |= c << (8 + 3 * i)
+    w = np.array([[word]], dtype=np.uint32)
+    cook = [-0.25, -0.5, -0.75, 1.0, 0.75, 0.5, 0.25, 0.0]
+    assert gf4.gf4_dequant(w)[0].tolist() == cook
+    metal = gf4.gf4_dequant_metal(w)[0].tolist()
+    assert metal == cook[:4] + [0.74139404296875] + cook[5:]
+
+
+def test_metal_form_differs_only_in_element_4_and_gemv_bound():
+    """On arbitrary finite words, the Metal form equals the cook formula except
+    element 4, which differs by exactly -s/4 * (c1 | c2 << 3 | c3 << 6) / 8192
+    (< 1/16 of a quantisation step; zeros may differ in sign); a GEMV's
+    difference is bounded by the sum of those terms times |x_{8g+4}|, and on
+    the config-1 weight distribution it is about 0.6% relative L2."""
+    rng = np.random.default_rng(17)
+    w = random_gf4_words(rng, (64, 512))
+    cook = gf4.gf4_dequant(w).reshape(64, 512, 8)
+    metal = gf4.gf4_dequant_metal(w).reshape(64, 512, 8)
+    others = [0, 1, 2, 3, 5, 6, 7]
+    assert np.array_equal(cook[..., others], metal[..., others])  # by value: zeros differ in sign
+    s = gf4.e5m2_byte_to_fp32((w & 0xFF).astype(np.uint8)).astype(np.float64)
+    e = (((w >> 11) & 7) | (((w >> 14) & 7) << 3) | (((w >> 17) & 7) << 6)).astype(np.float64)
+    assert np.array_equal(metal[..., 4].astype(np.float64) - cook[..., 4].astype(np.float64), -s / 4 * e / 8192)
+    assert np.all(e <= 511) and np.all(np.abs(s / 4 * e / 8192) <= np.abs(s) / 4 * 0.0624)
+    x = rng.standard_normal(4096).astype(np.float64)
+    dy = metal.reshape(64, 4096).astype(np.float64) @ x - cook.reshape(64, 4096).astype(np.float64) @ x
+    bound = (np.abs(s) / 4 * e / 8192 * np.abs(x[4::8])[None, :]).sum(axis=1)
+    assert np.all(np.abs(dy) <= bound * (1 + 1e-12))
+    # config-1 distribution (bf16 0.02 N(0,1) rows packed by pack_gf4_prepared): rel-L2 of the difference
+    wts = om.bf16_round((rng.standard_normal((256, 4096), dtype=np.float32) * np.float32(0.02)))
+    words = gf4.gf4_pack(wts)
+    y_cook = gf4.gf4_dequant(words).astype(np.float64) @ x
+    y_metal = gf4.gf4_dequant_metal(words).astype(np.float64) @ x
+    rel = np.linalg.norm(y_metal - y_cook) / np.linalg.norm(y_cook)
+    assert 1e-4 < rel < 5e-2, rel
