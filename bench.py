@@ -165,8 +165,8 @@ class Bench:
         return ev0.elapsed_time(ev1) / reps
 
 
-def gemv_calls(rt, weights, x, y, awq=None):
-    return [lambda s, w=w: rt.decode_matvec(w, x, y, awq=awq, stream=s) for w in weights]
+def gemv_calls(rt, weights, x, y, awq=None, workspace=None):
+    return [lambda s, w=w: rt.decode_matvec(w, x, y, awq=awq, stream=s, workspace=workspace) for w in weights]
 
 
 def gemv_bytes(rt, type_id, rows, k, nb):
@@ -174,12 +174,15 @@ def gemv_bytes(rt, type_id, rows, k, nb):
 
 
 def gemv_line(b: Bench, weights, nb, launches, warmup, awq=None) -> dict:
-    """One GEMV configuration: µs per launch, algorithmic GB/s and its roofline."""
+    """One GEMV configuration: µs per launch, algorithmic GB/s and its roofline.
+    Shapes whose launch splits K get a workspace (qw35_hip_decode_matvec_ws),
+    as the decode plans have."""
     rt, w0 = b.rt, weights[0]
     x = b.normal((nb, w0.k))
     y = b.torch.zeros((nb, w0.rows), dtype=b.torch.float32, device=b.dev)
-    ms, _ = b.time_launches(gemv_calls(rt, weights, x, y, awq), launches, warmup)
-    kern = rt.gemv_kernel(w0, nb, awq=awq is not None)["name"]
+    ws = rt.decode_matvec_workspace(w0, nb, device=b.dev)
+    ms, _ = b.time_launches(gemv_calls(rt, weights, x, y, awq, ws), launches, warmup)
+    kern = rt.gemv_kernel(w0, nb, awq=awq is not None, workspace=ws is not None)["name"]
     nbytes = gemv_bytes(rt, w0.type_id, w0.rows, w0.k, nb)
     return {"us": round(ms * 1e3, 3), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms * 1e3, kern)}
 

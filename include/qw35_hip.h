@@ -149,15 +149,38 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight *gate, const qw35_hip_weig
                                 const float *awq, float *dst, uint32_t n_batch, void *stream, char *err,
                                 uintptr_t err_len);
 
+/* Decode GEMV with a K-split workspace (otherwise qw35_hip_decode_matvec):
+ * at batch 3..8 on k = 12288 matrices of at most 4096 rows (the down
+ * projection) every workgroup of the plain launch would convert the whole
+ * activation batch, so with a workspace the launch splits K four ways across
+ * workgroups of four row tiles; each writes its partial sums to the workspace
+ * and the last of a
+ * row group to finish adds them in a fixed order (so results do not depend
+ * on timing) and writes dst.  workspace: device memory of at least
+ * qw35_hip_decode_matvec_workspace_size(w, n_batch) bytes (0: this call never
+ * splits; a smaller workspace disables the split), 256-byte aligned,
+ * zero-filled before its first use; its first 1 KiB holds the row-group
+ * counters, which every call returns to zero, so a workspace can be reused
+ * by later calls of any shape and by plans on the same stream, but not by
+ * calls that overlap.  NULL behaves as qw35_hip_decode_matvec.  No
+ * counterpart in the reference, whose decode dispatch allocates per runtime. */
+uint64_t qw35_hip_decode_matvec_workspace_size(const qw35_hip_weight *w, uint32_t n_batch);
+int qw35_hip_decode_matvec_ws(const qw35_hip_weight *w, const float *x, const float *awq, float *dst,
+                              uint32_t n_batch, int residual, void *workspace, uint64_t workspace_bytes, void *stream,
+                              char *err, uintptr_t err_len);
+
 /* The kernel a qw35_hip_decode_matvec (w_up NULL) or qw35_hip_ffn_gate_up_swiglu
- * (w_up set) call with this weight, batch and AWQ presence launches, named as
- * the profiler names it (e.g. "gf4_mfma_gemv<1, 3, 8, 2, false, false, true>"),
- * with its grid, workgroup size and LDS bytes; nothing is launched.  For a
- * batch the GF4 kernel splits, its first launch.  No counterpart in the
- * reference: it matches measurements and tests to the launch plan. */
+ * (w_up set) call with this weight, batch and AWQ presence launches -- with a
+ * K-split workspace when with_workspace != 0 (as plans and
+ * qw35_hip_decode_matvec_ws have) -- named as the profiler names it (e.g.
+ * "gf4_mfma_gemv<1, 3, 8, 2, false, false, true>"), with its grid, workgroup
+ * size, LDS bytes and K-split workspace bytes (0: no split); nothing is
+ * launched.  For a batch the GF4 kernel splits, its first launch.  No
+ * counterpart in the reference: it matches measurements and tests to the
+ * launch plan. */
 int qw35_hip_gemv_kernel(const qw35_hip_weight *w, const qw35_hip_weight *w_up, uint32_t n_batch, int has_awq,
-                         char *name, uintptr_t name_len, uint32_t *grid, uint32_t *block, uint32_t *lds_bytes,
-                         char *err, uintptr_t err_len);
+                         int with_workspace, char *name, uintptr_t name_len, uint32_t *grid, uint32_t *block,
+                         uint32_t *lds_bytes, uint64_t *workspace_bytes, char *err, uintptr_t err_len);
 
 /* Greedy LM head: per batch row b, the largest of
  *   logit[r] = sum_k W[r][k] * awq[k] * x[b][k]
@@ -242,7 +265,10 @@ typedef struct {
 } qw35_hip_plan_op;
 
 /* Validate the ops (same rules as the single calls) and record them; NULL on
- * error.  Recording launches nothing. */
+ * error.  Recording launches nothing.  A plan whose launches split K (see
+ * qw35_hip_decode_matvec_ws) allocates and zeroes one workspace for them at
+ * creation, freed by qw35_hip_plan_destroy; replays of one plan must not
+ * overlap. */
 void *qw35_hip_plan_create(const qw35_hip_plan_op *ops, uint32_t n_ops, char *err, uintptr_t err_len);
 /* Replay the recorded sequence on `stream` (asynchronous). */
 int qw35_hip_plan_launch(void *plan, void *stream, char *err, uintptr_t err_len);

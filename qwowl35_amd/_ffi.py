@@ -142,8 +142,15 @@ PROTOTYPES: dict[str, tuple] = {
     ),
     "qw35_hip_gemv_kernel": (
         C.c_int,
-        [C.POINTER(Weight), C.POINTER(Weight), C.c_uint32, C.c_int, C.c_char_p, C.c_size_t, C.POINTER(C.c_uint32),
-         C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_char_p, C.c_size_t],
+        [C.POINTER(Weight), C.POINTER(Weight), C.c_uint32, C.c_int, C.c_int, C.c_char_p, C.c_size_t,
+         C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.c_char_p,
+         C.c_size_t],
+    ),
+    "qw35_hip_decode_matvec_workspace_size": (C.c_uint64, [C.POINTER(Weight), C.c_uint32]),
+    "qw35_hip_decode_matvec_ws": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_void_p, C.c_uint64,
+         C.c_void_p, C.c_char_p, C.c_size_t],
     ),
     "qw35_hip_output_argmax_workspace_size": (C.c_uint64, [C.POINTER(Weight), C.c_uint32]),
     "qw35_hip_output_argmax": (

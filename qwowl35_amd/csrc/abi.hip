@@ -205,12 +205,14 @@ struct Plan {
     uint32_t n_ops = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    void* ws = nullptr;  // K-split workspace shared by the plan's launches (they run in order)
 };
 
 void plan_free(Plan* p) {
     if (!p) return;
     if (p->exec) (void)hipGraphExecDestroy(p->exec);
     if (p->graph) (void)hipGraphDestroy(p->graph);
+    if (p->ws) (void)hipFree(p->ws);
     delete p;
 }
 
@@ -285,8 +287,8 @@ int qw35_hip_ffn_gate_up_swiglu(const qw35_hip_weight* gate, const qw35_hip_weig
 }
 
 int qw35_hip_gemv_kernel(const qw35_hip_weight* w, const qw35_hip_weight* w_up, uint32_t n_batch, int has_awq,
-                         char* name, uintptr_t name_len, uint32_t* grid, uint32_t* block, uint32_t* lds_bytes,
-                         char* err, uintptr_t err_len) {
+                         int with_workspace, char* name, uintptr_t name_len, uint32_t* grid, uint32_t* block,
+                         uint32_t* lds_bytes, uint64_t* workspace_bytes, char* err, uintptr_t err_len) {
     // Stand-in addresses for the validation: nothing is launched or read.
     const float* fake = reinterpret_cast<const float*>(uintptr_t{256});
     const float* awq = has_awq ? fake : nullptr;
@@ -295,14 +297,46 @@ int qw35_hip_gemv_kernel(const qw35_hip_weight* w, const qw35_hip_weight* w_up, 
                          : check_matvec(w, fake, awq, dst, n_batch, "gemv_kernel", err, err_len);
     if (!ok) return 0;
     qw35::LaunchInfo info{};
+    info.splits = 1;
     qw35::GemvArgs a = gemv_args(w, w_up, fake, awq, dst, n_batch, 0);
     a.info = &info;
+    if (with_workspace) {  // a workspace large enough for any plan
+        a.ks_ws = const_cast<float*>(fake);
+        a.ks_ws_bytes = UINT64_MAX;
+    }
     if (!check_hip(dispatch_gemv(w->type_id, a, nullptr), "gemv_kernel", err, err_len)) return 0;
     if (name && name_len) snprintf(name, (size_t)name_len, "%s", info.name);
     if (grid) *grid = info.grid;
     if (block) *block = info.block;
     if (lds_bytes) *lds_bytes = info.lds;
+    if (workspace_bytes) *workspace_bytes = info.ws_bytes;
     return 1;
+}
+
+uint64_t qw35_hip_decode_matvec_workspace_size(const qw35_hip_weight* w, uint32_t n_batch) {
+    char msg[8];
+    uint64_t bytes = 0;
+    if (!qw35_hip_gemv_kernel(w, nullptr, n_batch, 0, 1, nullptr, 0, nullptr, nullptr, nullptr, &bytes, msg,
+                              sizeof msg))
+        return 0;
+    return bytes;
+}
+
+int qw35_hip_decode_matvec_ws(const qw35_hip_weight* w, const float* x, const float* awq, float* dst,
+                              uint32_t n_batch, int residual, void* workspace, uint64_t workspace_bytes, void* stream,
+                              char* err, uintptr_t err_len) {
+    if (!check_matvec(w, x, awq, dst, n_batch, "decode_matvec_ws", err, err_len)) return 0;
+    if (workspace && ((uintptr_t)workspace & 255u)) {
+        set_err(err, err_len, "decode_matvec_ws: workspace must be 256-byte aligned");
+        return 0;
+    }
+    qw35::GemvArgs a = gemv_args(w, nullptr, x, awq, dst, n_batch, residual);
+    a.ks_ws = workspace;
+    a.ks_ws_bytes = workspace ? workspace_bytes : 0;
+    return check_hip(dispatch_gemv(w->type_id, a, static_cast<hipStream_t>(stream)), "decode_matvec_ws", err,
+                     err_len)
+               ? 1
+               : 0;
 }
 
 void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* err, uintptr_t err_len) {
@@ -349,14 +383,29 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
     }
     Plan* plan = new Plan();
     plan->n_ops = n_ops;
-    hipStream_t s = nullptr;
-    if (!check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "plan_create: stream", err, err_len)) {
-        plan_free(plan);
-        return nullptr;
-    }
-    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    // Size the K-split workspace for the launches (described, not launched),
+    // then allocate and zero it once, outside the capture: the launches run in
+    // order and each returns its counters to zero.
+    uint64_t ws_bytes = 0;
     hipError_t launch = hipSuccess;
-    if (e == hipSuccess) {
+    for (int pass = 0; pass < 2 && launch == hipSuccess; ++pass) {
+        hipStream_t s = nullptr;
+        hipError_t e = hipSuccess;
+        if (pass == 1) {
+            if (ws_bytes) {
+                e = hipMalloc(&plan->ws, ws_bytes);
+                if (e == hipSuccess) e = hipMemset(plan->ws, 0, ws_bytes);
+            }
+            if (e == hipSuccess) e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+            if (e == hipSuccess) e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+            if (e != hipSuccess) {
+                if (s) (void)hipStreamDestroy(s);
+                check_hip(e, "plan_create: workspace / stream", err, err_len);
+                plan_free(plan);
+                return nullptr;
+            }
+        }
+        qw35::LaunchInfo info{};
         for (uint32_t i = 0; i < n_ops && launch == hipSuccess;) {
             const qw35_hip_plan_op& o = ops[i];
             if (o.kind == QW35_HIP_OP_ARGMAX) {
@@ -364,7 +413,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                 a.am_token = static_cast<uint32_t*>(o.workspace);
                 a.am_logit = reinterpret_cast<float*>(static_cast<uint8_t*>(o.workspace) +
                                                       argmax_ws_part(o.w, o.n_batch));
-                launch = qw35::launch_argmax_gemv(o.w->type_id, a, o.token, o.dst, s);
+                if (pass == 1) launch = qw35::launch_argmax_gemv(o.w->type_id, a, o.token, o.dst, s);
                 ++i;
                 continue;
             }
@@ -389,15 +438,32 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                     a.seg_rows[q - i] = (int)ops[q].w->rows;
                 }
             }
-            launch = dispatch_gemv(o.w->type_id, a, s);
+            if (pass == 0) {  // describe with an unbounded workspace: the bytes this launch would use
+                a.info = &info;
+                a.ks_ws = reinterpret_cast<void*>(uintptr_t{256});
+                a.ks_ws_bytes = UINT64_MAX;
+                info.ws_bytes = 0;
+                launch = dispatch_gemv(o.w->type_id, a, nullptr);
+                if (info.ws_bytes > ws_bytes) ws_bytes = info.ws_bytes;
+            } else {
+                a.ks_ws = plan->ws;
+                a.ks_ws_bytes = ws_bytes;
+                launch = dispatch_gemv(o.w->type_id, a, s);
+            }
             i = j;
         }
-        e = hipStreamEndCapture(s, &plan->graph);
+        if (pass == 1) {
+            e = hipStreamEndCapture(s, &plan->graph);
+            if (e == hipSuccess) e = launch;
+            if (e == hipSuccess) e = hipGraphInstantiate(&plan->exec, plan->graph, nullptr, nullptr, 0);
+            (void)hipStreamDestroy(s);
+            if (!check_hip(e, "plan_create: record", err, err_len)) {
+                plan_free(plan);
+                return nullptr;
+            }
+        }
     }
-    if (e == hipSuccess) e = launch;
-    if (e == hipSuccess) e = hipGraphInstantiate(&plan->exec, plan->graph, nullptr, nullptr, 0);
-    (void)hipStreamDestroy(s);
-    if (!check_hip(e, "plan_create: record", err, err_len)) {
+    if (!check_hip(launch, "plan_create: describe", err, err_len)) {
         plan_free(plan);
         return nullptr;
     }

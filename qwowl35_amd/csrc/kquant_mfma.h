@@ -194,6 +194,7 @@ __device__ __forceinline__ void u4x4_to_h(uint32_t t, const half2_t bias, uint32
 }
 
 typedef uint32_t uint2_t_ __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 
 // Per-wave LDS block: one transpose buffer (16 rows of a chunk), one activation
 // buffer (2*NB rows x 264 halves: one chunk, fp16 hi/lo), a zero row, and
@@ -223,7 +224,10 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     constexpr int NM = SWIGLU ? 2 : 1;
     constexpr int LPT = (16 * F::kSegs + 63) / 64;  // 16-byte weight loads per lane per tile
     constexpr int WPC = RT * NM * LPT;                // weight loads per chunk
-    constexpr int LPC = NB + (HAS_AWQ ? 1 : 0) + WPC; // loads per chunk
+    // GF4 reads each activation row as two 8-byte pieces per lane (the column
+    // pairing of its operand, see issue()); the other formats one 16-byte piece.
+    constexpr int XL = FMT == kFmtGF4 ? 2 : 1;
+    constexpr int LPC = XL * (NB + (HAS_AWQ ? 1 : 0)) + WPC;  // loads per chunk
     static_assert(P >= 1 && P <= CPW && P * LPC <= 60, "vmcnt budget");
     const int k = args.k;
     const int n_batch = args.n_batch;
@@ -235,7 +239,11 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     const void* wmat = args.w;
     float* yout = args.y;
     int rows = args.rows;
-    int blk = blockIdx.x;
+    // K split: consecutive workgroups take the splits of one row group.
+    const int splits = args.splits > 1 ? args.splits : 1;
+    const int split = (int)blockIdx.x % splits;
+    const int group = (int)blockIdx.x / splits;
+    int blk = group;
     if (args.n_seg > 1) {
         int seg = 0;
 #pragma unroll
@@ -253,9 +261,16 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     const int row0 = blk * 16 * RT;
     const int chunks = k >> 8;
     const size_t row_bytes = (size_t)chunks * F::kChunkBytes;
+    const int cps = chunks / splits;  // chunks of this workgroup's K slice
+    const int cbase = split * cps;
 
     uint8_t* wblk = smem + (size_t)wave * L::kBytes;
-    float* part = reinterpret_cast<float*>(smem + (size_t)KS * L::kBytes);  // [KS][RT][NM][NB][16]
+    // Wave w's partials [RT][NM][NB][16] go to the start of its own LDS block
+    // once its last chunk is done (no other wave touches that block).
+    static_assert(RT * NM * NB * 16 * 4 <= L::kBytes, "partials fit a wave's block");
+    auto part = [&](int w, int t, int m, int b, int nn) -> float& {
+        return reinterpret_cast<float*>(smem + (size_t)w * L::kBytes)[((t * NM + m) * NB + b) * 16 + nn];
+    };
     if (lane < 32) reinterpret_cast<uint32_t*>(wblk + L::kZeroOff)[lane] = 0u;
     _Float16* xs = reinterpret_cast<_Float16*>(wblk + L::kActOff);
     float* sx = reinterpret_cast<float*>(wblk + L::kSxOff);
@@ -284,14 +299,28 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
         constexpr int c = decltype(CI)::value;
         constexpr int sl = c % P;
         int chunk = wave * CPW + c;
-        chunk = chunk < chunks ? chunk : 0;
+        chunk = cbase + (chunk < cps ? chunk : 0);
         const float* xc = args.x + (size_t)chunk * 256;
+        if constexpr (FMT == kFmtGF4) {
+            // Columns 8g..8g+7 are staged as x0 x4 x1 x5 | x2 x6 x3 x7: lane 2g
+            // reads (x0, x1) and (x4, x5), lane 2g + 1 (x2, x3) and (x6, x7).
+            const int c0 = 8 * (lane >> 1) + 2 * (lane & 1);
+            auto pairs = [&](const float* p) {
+                const float2_t lo = *reinterpret_cast<const float2_t*>(p + c0);
+                const float2_t hi = *reinterpret_cast<const float2_t*>(p + c0 + 4);
+                return float4_t{lo[0], lo[1], hi[0], hi[1]};
+            };
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int bb = b < n_batch ? b : 0;
-            xv[sl][b] = *reinterpret_cast<const float4_t*>(xc + (size_t)bb * k + 4 * lane);
+            for (int b = 0; b < NB; ++b) xv[sl][b] = pairs(xc + (size_t)(b < n_batch ? b : 0) * k);
+            if (HAS_AWQ) av[sl] = pairs(args.awq + (size_t)chunk * 256);
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int bb = b < n_batch ? b : 0;
+                xv[sl][b] = *reinterpret_cast<const float4_t*>(xc + (size_t)bb * k + 4 * lane);
+            }
+            if (HAS_AWQ) av[sl] = *reinterpret_cast<const float4_t*>(args.awq + (size_t)chunk * 256 + 4 * lane);
         }
-        if (HAS_AWQ) av[sl] = *reinterpret_cast<const float4_t*>(args.awq + (size_t)chunk * 256 + 4 * lane);
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? wmat : args.w_up) +
@@ -322,30 +351,34 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
         constexpr int sl = c % P;
         constexpr int later = (CPW - 1 - c) < (P - 1) ? (CPW - 1 - c) : (P - 1);  // chunks issued after c
         kq_wait_vmcnt<later * LPC>();
-        const bool live = wave * CPW + c < chunks;
+        const bool live = wave * CPW + c < cps;
         if (live) {
-            // Stage chunk c's activations: fp16 hi/lo with a per-chunk power-of-two scale.
-            float isc[NB];
+            // Stage chunk c's activations: fp16 hi/lo with a per-chunk power-of-two
+            // scale.  The NB row maxima are reduced together (wave_max_rows); the
+            // scale and its inverse are uniform integer work; hi = fp16(v s) and
+            // lo = fp16(v s - hi) are single mixed-precision FMAs (v s is exact).
+            float4_t v[NB];
+            uint32_t mx[NB];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                float4_t v = xv[sl][b];
-                if (HAS_AWQ) v *= av[sl];
-                const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-                const float sc = fp16_range_scale(wave_max_abs(mx));
-                isc[b] = pow2_inverse(sc);
-                v *= sc;
-                float e[4] = {v[0], v[1], v[2], v[3]};
-                if constexpr (FMT == kFmtGF4) {
-                    // Columns 8g..8g+7 stored as x0 x4 x1 x5 x2 x6 x3 x7: even lanes (columns
-                    // 0..3 of the group) write pairs (x0,x4) (x1,x5), odd lanes (x2,x6) (x3,x7).
-                    float u[4];
+                v[b] = xv[sl][b];
+                if (HAS_AWQ) v[b] *= av[sl];
+                mx[b] = __builtin_bit_cast(uint32_t, fmaxf(fmaxf(fabsf(v[b][0]), fabsf(v[b][1])),
+                                                           fmaxf(fabsf(v[b][2]), fabsf(v[b][3]))));
+            }
+            uint32_t smax[NB];
+            wave_max_rows<NB>(mx, smax, lane);
+            uint32_t isc_bits[NB];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor1>(v[q]);
-                    if (lane & 1) {
-                        e[0] = u[2]; e[1] = v[2]; e[2] = u[3]; e[3] = v[3];
-                    } else {
-                        e[0] = v[0]; e[1] = u[0]; e[2] = v[1]; e[3] = u[1];
-                    }
+            for (int b = 0; b < NB; ++b) {
+                float sc, isc;
+                fp16_range_scale_bits(smax[b], sc, isc);
+                isc_bits[b] = __builtin_bit_cast(uint32_t, isc);
+                float e[4] = {v[b][0], v[b][1], v[b][2], v[b][3]};
+                if constexpr (FMT == kFmtGF4) {
+                    // (x0, x1, x4, x5) -> x0 x4 x1 x5 (and the odd lane's likewise)
+                    e[1] = v[b][2];
+                    e[2] = v[b][1];
                 } else if constexpr (FMT == kFmtGF2) {
                     // Columns 16w..16w+15 stored as x0 x8 x1 x9 .. x3 x11 | x4 x12 .. x7 x15
                     // (MFMA k-slots of lane groups 2(w&1), 2(w&1)+1): the lanes holding
@@ -353,42 +386,47 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                     // columns, the lanes holding 8..11 / 12..15 those of the last two.
                     float u[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor2>(v[q]);
+                    for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor2>(v[b][q]);
                     if (lane & 2) {
-                        e[0] = u[2]; e[1] = v[2]; e[2] = u[3]; e[3] = v[3];
+                        e[0] = u[2]; e[1] = v[b][2]; e[2] = u[3]; e[3] = v[b][3];
                     } else {
-                        e[0] = v[0]; e[1] = u[0]; e[2] = v[1]; e[3] = u[1];
+                        e[0] = v[b][0]; e[1] = u[0]; e[2] = v[b][1]; e[3] = u[1];
                     }
                 }
                 // GF2 k-slot of the lane's four values (natural order otherwise)
                 const int apos = FMT == kFmtGF2 ? 32 * (lane >> 3) + 16 * ((lane >> 2) & 1) + 8 * (lane & 1) +
                                                       4 * ((lane >> 1) & 1)
                                                 : 4 * lane;
-                const half2_t hi0 = h2(e[0], e[1]);
-                const half2_t hi1 = h2(e[2], e[3]);
-                const half2_t lo0 = h2(e[0] - (float)hi0.x, e[1] - (float)hi0.y);
-                const half2_t lo1 = h2(e[2] - (float)hi1.x, e[3] - (float)hi1.y);
+                half2_t hi0, hi1, lo0, lo1;
+                hi0.x = (_Float16)__builtin_fmaf(e[0], sc, 0.0f);
+                hi0.y = (_Float16)__builtin_fmaf(e[1], sc, 0.0f);
+                hi1.x = (_Float16)__builtin_fmaf(e[2], sc, 0.0f);
+                hi1.y = (_Float16)__builtin_fmaf(e[3], sc, 0.0f);
+                lo0.x = (_Float16)__builtin_fmaf(e[0], sc, -(float)hi0.x);
+                lo0.y = (_Float16)__builtin_fmaf(e[1], sc, -(float)hi0.y);
+                lo1.x = (_Float16)__builtin_fmaf(e[2], sc, -(float)hi1.x);
+                lo1.y = (_Float16)__builtin_fmaf(e[3], sc, -(float)hi1.y);
                 *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + apos) =
                     uint2_t_{as_u32(hi0), as_u32(hi1)};
                 *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + apos) =
                     uint2_t_{as_u32(lo0), as_u32(lo1)};
                 if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K) {
                     // sum of the scaled activations of each 32-column sub-block (8 lanes)
-                    float s4 = (v[0] + v[1]) + (v[2] + v[3]);
+                    float s4 = (v[b][0] + v[b][1]) + (v[b][2] + v[b][3]);
                     s4 += dpp_f32<kDppQuadXor1>(s4);
                     s4 += dpp_f32<kDppQuadXor2>(s4);
                     s4 += dpp_f32<kDppRowHalfMirror>(s4);
-                    if ((lane & 7) == 7) sx[b * 8 + (lane >> 3)] = s4;
+                    if ((lane & 7) == 7) sx[b * 8 + (lane >> 3)] = s4 * sc;
                 }
             }
             float inv_sc[2];  // batches 2kq and 2kq+1
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
-                float v = 1.0f;
+                uint32_t bits = 0x3F800000u;
 #pragma unroll
                 for (int b = 0; b < NB; ++b)
-                    if (b == 2 * kq + jj) v = isc[b];
-                inv_sc[jj] = v;
+                    if (b == 2 * kq + jj) bits = isc_bits[b];
+                inv_sc[jj] = __builtin_bit_cast(float, bits);
             }
             const bool a_live = n < 2 * n_batch;
             const _Float16* arow =
@@ -492,7 +530,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                         // The super-block starts `off` bytes into the row buffer
                         // (even, wave-uniform); words are read 4-aligned and, for the
                         // chunks at 2 mod 4, realigned by two bytes.
-                        const int off = ((wave * CPW + c) * 210) & 15;
+                        const int off = ((cbase + wave * CPW + c) * 210) & 15;
                         const uint8_t* sb = wrow + (off & ~3);
                         const _Float16* abase = a_live ? arow + 4 * kq : arow;  // arow: the zero row when !a_live
                         const int astep = a_live ? 16 : 0;
@@ -640,7 +678,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 const int b = 2 * kq + jj;
-                if (b < NB) part[(((wave * RT + t) * NM + m) * NB + b) * 16 + n] = acc[t][m][jj];
+                if (b < NB) part(wave, t, m, b, n) = acc[t][m][jj];
             }
     __syncthreads();
     if (args.am_token) {
@@ -654,13 +692,69 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                 const int r = row0 + o;
                 float sum = 0.0f;
 #pragma unroll
-                for (int w = 0; w < KS; ++w) sum += part[(((w * RT + t) * NM) * NB + b) * 16 + nn];
+                for (int w = 0; w < KS; ++w) sum += part(w, t, 0, b, nn);
                 if (r < rows && !__builtin_isnan(sum)) argmax_take(best, best_id, sum, (uint32_t)r);
             }
             wave_argmax(best, best_id);
             if (lane == 0) {
                 args.am_logit[(size_t)blockIdx.x * n_batch + b] = best;
                 args.am_token[(size_t)blockIdx.x * n_batch + b] = best_id;
+            }
+        }
+        return;
+    }
+    constexpr int PART = RT * NB * 16 * NM;  // floats of one workgroup's partial
+    if (splits > 1) {
+        // This workgroup's partial over its K slice goes to the workspace with
+        // agent-coherent stores; each thread waits for its stores to complete
+        // before the barrier, so they are visible device-wide before the row
+        // group's counter moves.  The workgroup that moves it last sums the
+        // group's partials in split order (the same order whichever arrives
+        // last) and resets the counter for the next launch; nothing waits.
+        float* mine = args.ks_part + (size_t)blockIdx.x * PART;
+        for (int o = threadIdx.x; o < RT * NB * 16; o += 64 * KS) {
+            const int t = o / (NB * 16);
+            const int b = (o / 16) % NB;
+            const int nn = o & 15;
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int w = 0; w < KS; ++w) sum += part(w, t, m, b, nn);
+                __hip_atomic_store(mine + o * NM + m, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        kq_wait_vmcnt<0>();
+        __shared__ uint32_t last_arrival;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(args.ks_count + group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_arrival = prev == (uint32_t)(splits - 1);
+            if (last_arrival) __hip_atomic_store(args.ks_count + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_arrival) return;
+        const float* first = args.ks_part + (size_t)(blockIdx.x - split) * PART;
+        for (int o = threadIdx.x; o < RT * NB * 16; o += 64 * KS) {
+            const int t = o / (NB * 16);
+            const int b = (o / 16) % NB;
+            const int nn = o & 15;
+            const int r = row0 + 16 * t + nn;
+            float tot[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                float sum = 0.0f;
+                for (int sp = 0; sp < splits; ++sp)
+                    sum += __hip_atomic_load(first + (size_t)sp * PART + o * NM + m, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+                tot[m] = sum;
+            }
+            if (r < rows && b < n_batch) {
+                float* yp = yout + (size_t)b * rows + r;
+                float v = SWIGLU ? silu(tot[0]) * tot[NM - 1] : tot[0];
+                if (args.residual) v += *yp;
+                *yp = v;
             }
         }
         return;
@@ -675,7 +769,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
         for (int m = 0; m < NM; ++m) {
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < KS; ++w) sum += part[(((w * RT + t) * NM + m) * NB + b) * 16 + nn];
+            for (int w = 0; w < KS; ++w) sum += part(w, t, m, b, nn);
             tot[m] = sum;
         }
         if (r < rows && b < n_batch) {
@@ -689,6 +783,7 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
 
 struct KqPlan {
     int rt, ks, cpw, p;
+    int s = 1;  // K splits across workgroups (needs a workspace)
 };
 
 // KS waves x CPW chunks cover k with P chunks in flight per wave; RT row tiles
@@ -700,9 +795,16 @@ struct KqPlan {
 // one sweep on one box: Q4_K {3, 8, 2, 2} 134-136 us ({2, 16, 1, 1} 142 us),
 // Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us), GF2 {3, 8, 2, 2} 113 us
 // ({2, 16, 1, 1} 119 us); Q5_K keeps {2, 16, 1, 1} 157 us ({3, 8, 2, 2} 160 us).
-inline KqPlan plan_kq(int fmt, int rows, int k, int nb) {
+inline KqPlan plan_kq(int fmt, int rows, int k, int nb, bool split_ok = false) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
+    // Batch 4..8, k = 12288, at most 256 row tiles (the 9B's down projection):
+    // with one tile per workgroup every workgroup would stage the whole
+    // activation batch, so K is split four ways across workgroups of four
+    // tiles, twelve waves, one chunk per wave (GF4 b8 13.0-13.7 us, Q4_K 15.7-16.4,
+    // against 17.9 / 21.0 unsplit; two-chunk waves or two-tile workgroups
+    // 14.6-22 us).  At k = 4096 no split beat the unsplit q8_0 launch.
+    if (split_ok && nb >= 4 && tiles <= 256 && chunks == 48) return {4, 12, 1, 1, 4};
     if (chunks <= 4) return {1, 4, 1, 1};
     if (chunks <= 8) return {1, 8, 1, 1};
     if (chunks <= 16) {
@@ -737,17 +839,40 @@ inline KqPlan plan_kq(int fmt, int rows, int k, int nb) {
 template <int FMT, int NB, int RT, int KS, int CPW, bool SWIGLU>
 size_t kq_lds_bytes() {
     constexpr int NM = SWIGLU ? 2 : 1;
-    return (size_t)KS * KqLds<FMT, NB>::kBytes + (size_t)KS * RT * NM * NB * 16 * 4;
+    (void)NM;
+    return (size_t)KS * KqLds<FMT, NB>::kBytes;
+}
+
+// K-split workspace: kKsCounters row-group counters at its start (the same
+// place for every shape, so a launch always finds the counters the previous
+// one returned to zero), then the partials (one RT x NB x 16 x NM block per
+// workgroup).  Split plans cover at most 256 row tiles, so at most 256 groups.
+constexpr int kKsCounters = 256;
+constexpr size_t kKsPartOffset = kKsCounters * 4;
+inline size_t kq_split_ws_bytes(int groups, int splits, int rt, int nb, int nm) {
+    return splits > 1 ? kKsPartOffset + ((size_t)groups * splits * rt * nb * 16 * nm * 4 + 255) / 256 * 256 : 0;
 }
 
 template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU>
-hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
+hipError_t kq_launch_cfg(const GemvArgs& a0, hipStream_t stream, int splits = 1) {
     const size_t lds = kq_lds_bytes<FMT, NB, RT, KS, CPW, SWIGLU>();
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+    GemvArgs a = a0;
     int grid = (a.rows + 16 * RT - 1) / (16 * RT);
     if (a.n_seg > 1) {
         grid = 0;
         for (int s = 0; s < a.n_seg; ++s) grid += (a.seg_rows[s] + 16 * RT - 1) / (16 * RT);
+    }
+    const int groups = grid;
+    const size_t ws_need = kq_split_ws_bytes(groups, splits, RT, NB, SWIGLU ? 2 : 1);
+    if (splits > 1 && (a.am_token || !a.ks_ws || a.ks_ws_bytes < ws_need || (a.k >> 8) % splits != 0 ||
+                       (a.k >> 8) / splits > KS * CPW || groups > kKsCounters))
+        return hipErrorInvalidValue;
+    a.splits = splits;
+    if (splits > 1) {
+        a.ks_count = static_cast<uint32_t*>(a.ks_ws);
+        a.ks_part = reinterpret_cast<float*>(static_cast<uint8_t*>(a.ks_ws) + kKsPartOffset);
+        grid *= splits;
     }
     // The greedy head's partial workspace holds argmax_groups() entries per
     // batch row: refuse a launch shape with more workgroups than that.
@@ -758,6 +883,8 @@ hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
         a.info->grid = (unsigned)grid;
         a.info->block = 64u * KS;
         a.info->lds = (unsigned)lds;
+        a.info->splits = (unsigned)splits;
+        a.info->ws_bytes = ws_need;
         return hipSuccess;
     }
     if (a.awq)
@@ -773,7 +900,8 @@ hipError_t kq_launch_cfg(const GemvArgs& a, hipStream_t stream) {
 template <int FMT, int NB, int RT, int P, bool SWIGLU>
 constexpr bool kq_fits() {
     constexpr int lpt = (16 * Fmt<FMT>::kSegs + 63) / 64;
-    return P * (NB + 1 + RT * (SWIGLU ? 2 : 1) * lpt) <= 60;
+    constexpr int xl = FMT == kFmtGF4 ? 2 : 1;
+    return P * (xl * (NB + 1) + RT * (SWIGLU ? 2 : 1) * lpt) <= 60;
 }
 
 template <int FMT, int NB, bool SWIGLU>
@@ -783,13 +911,22 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
         total_rows = 0;
         for (int s = 0; s < a.n_seg; ++s) total_rows += a.seg_rows[s];
     }
-    KqPlan p = plan_kq(FMT, total_rows, a.k, NB);
+    KqPlan p = plan_kq(FMT, total_rows, a.k, NB, a.ks_ws != nullptr && !a.am_token);
+    if (p.s > 1) {
+        int groups = (a.rows + 16 * p.rt - 1) / (16 * p.rt);
+        if (a.n_seg > 1) {
+            groups = 0;
+            for (int s = 0; s < a.n_seg; ++s) groups += (a.seg_rows[s] + 16 * p.rt - 1) / (16 * p.rt);
+        }
+        if (a.ks_ws_bytes < kq_split_ws_bytes(groups, p.s, p.rt, NB, SWIGLU ? 2 : 1))
+            p = plan_kq(FMT, total_rows, a.k, NB, false);
+    }
     // Fused gate/up holds two matrices' loads per tile: more than two row tiles
     // per workgroup spill registers, so those take the one-tile shape below.
 #define QW35_KQ_PLAN(RT, KS, CPW, P)                                                             \
     if constexpr (kq_fits<FMT, NB, RT, P, SWIGLU>() && (!SWIGLU || RT <= 2)) {                     \
         if (p.rt == RT && p.ks == KS && p.cpw == CPW && p.p == P)                                  \
-            return kq_launch_cfg<FMT, NB, RT, KS, CPW, P, SWIGLU>(a, stream);                      \
+            return kq_launch_cfg<FMT, NB, RT, KS, CPW, P, SWIGLU>(a, stream, p.s);                 \
     }
     QW35_KQ_PLAN(1, 4, 1, 1)
     QW35_KQ_PLAN(1, 8, 1, 1)
@@ -810,6 +947,9 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
     }
     if constexpr (NB == 8 && FMT == kFmtGF4) {
         QW35_KQ_PLAN(1, 12, 4, 2)
+    }
+    if constexpr (NB >= 4 && !SWIGLU) {  // the K-split plan
+        QW35_KQ_PLAN(4, 12, 1, 1)
     }
     if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtQ6K || FMT == kFmtGF2) {
         if constexpr (NB >= 4) {

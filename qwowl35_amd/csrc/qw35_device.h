@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace qw35 {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -21,6 +23,8 @@ constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
 constexpr int kDppRowBcast15 = 0x142;
 constexpr int kDppRowBcast31 = 0x143;
+constexpr int kDppRowRor4 = 0x124;      // row_ror:4 (within each 16-lane row)
+constexpr int kDppRowRor8 = 0x128;      // row_ror:8
 
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -66,6 +70,58 @@ __device__ __forceinline__ float wave_max_abs(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)u, 63));
 }
 
+// Lanes l and l ^ 16 (v_permlane16_swap), l and l ^ 32 (v_permlane32_swap):
+// the larger of the two values in both.
+__device__ __forceinline__ uint32_t max_xor16_u32(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return dpp_max_u32(p[0], p[1]);
+}
+__device__ __forceinline__ uint32_t max_xor32_u32(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return dpp_max_u32(p[0], p[1]);
+}
+
+// Wave maxima of NB rows at once (NB = 1, 2, 4, 8): m[r] is lane's value of
+// row r (non-negative fp32 bit patterns, compared as integers); returns the
+// maximum of row r over the 64 lanes in out[r] (uniform).
+// The first log2(NB) steps each halve the rows a lane carries: at the step on
+// lane bit j a lane keeps the half of its rows selected by its bit j, merged
+// with the same rows of its partner across that bit (row_ror:4 for bit 2,
+// quad permutations for bits 1 and 0).  Lane l is then left with row l % NB
+// over the lanes that agree with it outside those bits, and the remaining
+// steps (one value each) pair lanes that agree on those bits.  8 rows cost 28
+// VALU operations instead of 48 for eight separate reductions.
+template <int NB>
+__device__ __forceinline__ void wave_max_rows(const uint32_t (&m)[NB], uint32_t (&out)[NB], int lane) {
+    static_assert(NB == 1 || NB == 2 || NB == 4 || NB == 8, "NB");
+    uint32_t a[NB];
+#pragma unroll
+    for (int r = 0; r < NB; ++r) a[r] = m[r];
+    auto halve = [&](auto CTRL, int held, bool upper) {
+        constexpr int ctrl = decltype(CTRL)::value;
+#pragma unroll
+        for (int r = 0; r < NB / 2; ++r) {
+            if (r < held / 2) {
+                const uint32_t lo = dpp_max_u32(a[r], dpp_u32<ctrl>(a[r]));
+                const uint32_t hi = dpp_max_u32(a[r + held / 2], dpp_u32<ctrl>(a[r + held / 2]));
+                a[r] = upper ? hi : lo;
+            }
+        }
+    };
+    if constexpr (NB == 8) halve(std::integral_constant<int, kDppRowRor4>{}, 8, (lane & 4) != 0);
+    if constexpr (NB >= 4) halve(std::integral_constant<int, kDppQuadXor2>{}, 4, (lane & 2) != 0);
+    if constexpr (NB >= 2) halve(std::integral_constant<int, kDppQuadXor1>{}, 2, (lane & 1) != 0);
+    uint32_t u = a[0];
+    if constexpr (NB == 1) u = dpp_max_u32(u, dpp_u32<kDppQuadXor1>(u));
+    if constexpr (NB <= 2) u = dpp_max_u32(u, dpp_u32<kDppQuadXor2>(u));
+    if constexpr (NB <= 4) u = dpp_max_u32(u, dpp_u32<kDppRowRor4>(u));
+    u = dpp_max_u32(u, dpp_u32<kDppRowRor8>(u));
+    u = max_xor16_u32(u);
+    u = max_xor32_u32(u);
+#pragma unroll
+    for (int r = 0; r < NB; ++r) out[r] = (uint32_t)__builtin_amdgcn_readlane((int)u, r);
+}
+
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }
@@ -102,6 +158,23 @@ __device__ __forceinline__ float fp16_range_scale(float max_abs) {
     if (shift > 125) shift = 125;
     if (shift < -125) shift = -125;
     return ldexpf(1.0f, shift);
+}
+
+// fp16_range_scale and its inverse from the bit pattern of max_abs (a
+// non-negative fp32 or an inf/NaN pattern), in integer operations, so that a
+// uniform maximum is scaled on the scalar unit.  For a normal maximum with
+// biased exponent E the factor is 2^(140 - E); subnormal maxima (E = 0) and
+// everything below 2^-111 take 2^125.
+__device__ __forceinline__ void fp16_range_scale_bits(uint32_t max_bits, float& sc, float& inv) {
+    if (max_bits == 0u || max_bits >= 0x7F800000u) {
+        sc = 1.0f;
+        inv = 1.0f;
+        return;
+    }
+    int shift = 140 - (int)(max_bits >> 23);
+    shift = shift < 125 ? shift : 125;
+    sc = __builtin_bit_cast(float, (uint32_t)(127 + shift) << 23);
+    inv = __builtin_bit_cast(float, (uint32_t)(127 - shift) << 23);
 }
 
 // 1 / s for s = 2^e, |e| <= 126 (fp16_range_scale returns |e| <= 125, the

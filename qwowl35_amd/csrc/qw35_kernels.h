@@ -30,6 +30,8 @@ struct LaunchInfo {
     unsigned grid;
     unsigned block;
     unsigned lds;
+    unsigned splits;    // K splits of the launch (1: none)
+    uint64_t ws_bytes;  // K-split workspace the launch uses (0: none)
 };
 
 struct GemvArgs {
@@ -55,6 +57,15 @@ struct GemvArgs {
     // Host pointer: when set, the launchers describe the (first) launch here
     // and launch nothing.
     LaunchInfo* info;
+    // K-split workspace (nullable, 256-byte aligned, zero-filled before its
+    // first use): with it the chunked kernel's planner may split K across
+    // workgroups (partials, then one counter per row group, which the kernel
+    // returns to zero).  splits / ks_part / ks_count are set by the launcher.
+    void* ks_ws;
+    uint64_t ks_ws_bytes;
+    int splits;
+    float* ks_part;
+    uint32_t* ks_count;
 };
 
 // Each launcher validates nothing (the C ABI does) and returns the launch status.

@@ -237,16 +237,31 @@ def _check_awq(awq: torch.Tensor | None, k: int, x: torch.Tensor, name: str = "a
         raise Qw35Error(f"{name} must be a contiguous fp32 tensor of k={k} values on {x.device}")
 
 
+def decode_matvec_workspace(w: HipWeight, n_batch: int, device="cuda") -> torch.Tensor | None:
+    """A zero-filled K-split workspace for ``decode_matvec(..., workspace=)``
+    (``qw35_hip_decode_matvec_workspace_size``), or None when the shape never splits."""
+    n = int(_ffi.load().qw35_hip_decode_matvec_workspace_size(C.byref(w.view), n_batch))
+    return torch.zeros(n, dtype=torch.uint8, device=device) if n else None
+
+
 def decode_matvec(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, residual: bool = False,
-                  awq: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-    """``dst (+)= W @ (awq * x)`` for x [k] or [n_batch, k] (n_batch <= 8)."""
+                  awq: torch.Tensor | None = None, stream=None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``dst (+)= W @ (awq * x)`` for x [k] or [n_batch, k] (n_batch <= 8).
+    ``workspace`` (from ``decode_matvec_workspace``) lets batch 3..8 split K
+    across workgroups (``qw35_hip_decode_matvec_ws``)."""
     nb = _check_act(x, w.k, "x")
     _check_awq(awq, w.k, x)
     if dst is None:
         dst = torch.zeros((nb, w.rows) if x.dim() == 2 else (w.rows,), dtype=torch.float32, device=x.device)
     _check_out(dst, nb, w.rows, x, "dst")
-    _ffi.call("qw35_hip_decode_matvec", C.byref(w.view), _ptr(x), _ptr(awq), _ptr(dst), nb, int(bool(residual)),
-              _stream(stream))
+    if workspace is None:
+        _ffi.call("qw35_hip_decode_matvec", C.byref(w.view), _ptr(x), _ptr(awq), _ptr(dst), nb,
+                  int(bool(residual)), _stream(stream))
+        return dst
+    if workspace.device != x.device or not workspace.is_contiguous() or workspace.data_ptr() % 256:
+        raise Qw35Error("workspace must be a contiguous, 256-byte aligned tensor on x's device")
+    _ffi.call("qw35_hip_decode_matvec_ws", C.byref(w.view), _ptr(x), _ptr(awq), _ptr(dst), nb, int(bool(residual)),
+              _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream))
     return dst
 
 
@@ -263,14 +278,18 @@ def ffn_gate_up_swiglu(gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: tor
     return dst
 
 
-def gemv_kernel(w: HipWeight, n_batch: int = 1, w_up: HipWeight | None = None, awq: bool = False) -> dict:
+def gemv_kernel(w: HipWeight, n_batch: int = 1, w_up: HipWeight | None = None, awq: bool = False,
+                workspace: bool = False) -> dict:
     """The kernel a ``decode_matvec`` (or, with ``w_up``, ``ffn_gate_up_swiglu``)
-    call launches: ``{"name", "grid", "block", "lds"}`` (``qw35_hip_gemv_kernel``)."""
+    call launches, with a K-split workspace when ``workspace``:
+    ``{"name", "grid", "block", "lds", "workspace_bytes"}`` (``qw35_hip_gemv_kernel``)."""
     name = C.create_string_buffer(160)
-    g, b, l = C.c_uint32(), C.c_uint32(), C.c_uint32()
+    g, b, l, ws = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_uint64()
     _ffi.call("qw35_hip_gemv_kernel", C.byref(w.view), C.byref(w_up.view) if w_up is not None else None, n_batch,
-              int(bool(awq)), name, C.sizeof(name), C.byref(g), C.byref(b), C.byref(l))
-    return {"name": name.value.decode(), "grid": g.value, "block": b.value, "lds": l.value}
+              int(bool(awq)), int(bool(workspace)), name, C.sizeof(name), C.byref(g), C.byref(b), C.byref(l),
+              C.byref(ws))
+    return {"name": name.value.decode(), "grid": g.value, "block": b.value, "lds": l.value,
+            "workspace_bytes": ws.value}
 
 
 def output_argmax_workspace(w: HipWeight, n_batch: int, device="cuda") -> torch.Tensor:

@@ -199,6 +199,56 @@ def test_extreme_activation_magnitudes(cuda, name, nb):
         assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2, mag
 
 
+# k = 12288 on at most 256 row tiles splits; k = 4096 takes the workspace and ignores it
+SPLIT_CASES = [("gf4", 4096, 12288), ("q4_k", 4096, 12288), ("q8_0", 4096, 12288), ("q6_k", 4000, 12288),
+               ("q5_k", 1000, 12288), ("gf2", 4096, 12288), ("gf4", 2072, 12288), ("q8_0", 4096, 4096)]
+
+
+@pytest.mark.parametrize("nb", [4, 5, 8])
+@pytest.mark.parametrize("name,rows,k", SPLIT_CASES)
+def test_k_split_workspace(cuda, name, rows, k, nb):
+    """The K-split launch (batch 3..8, k = 12288, at most 256 row tiles, with a workspace):
+    each workgroup sums one K slice, the last of a row group adds the partials
+    in a fixed order.  Against the oracle (with AWQ and the residual add), equal
+    on 12 repeated calls bit for bit (no dependence on which workgroup finishes
+    last; the counters return to zero), and within the bar of the unsplit call;
+    the same workspace then serves a second shape."""
+    import torch
+
+    rt = _rt()
+    print(f"k-split {name} {rows}x{k} b{nb}", flush=True)
+    w, raw = _gpu_weight(cuda, TYPES[name], rows, k, seed=rows + k + nb)
+    assert (rt.gemv_kernel(w, nb, workspace=True)["workspace_bytes"] > 0) == (k == 12288)
+    deq = _oracle_deq(cuda, w, raw)
+    rng = np.random.default_rng(700 + nb)
+    x = rng.standard_normal((nb, k), dtype=np.float32)
+    a = rng.uniform(0.5, 2.0, k).astype(np.float32)
+    base = rng.standard_normal((nb, rows)).astype(np.float32)
+    ws = rt.decode_matvec_workspace(w, nb, device=cuda)
+    xt, at, bt = _t(x, cuda), _t(a, cuda), _t(base, cuda)
+    first = None
+    for _ in range(12):
+        dst = bt.clone()
+        rt.decode_matvec(w, xt, dst=dst, residual=True, awq=at, workspace=ws)
+        if first is None:
+            first = dst
+        else:
+            assert torch.equal(dst, first)
+    want = base.astype(np.float64) + om.matvec_f64(deq, x, a)
+    assert om.rel_l2(first.cpu().numpy(), want) <= GEMV_REL_L2
+    plain = rt.decode_matvec(w, xt, dst=bt.clone(), residual=True, awq=at)
+    assert om.rel_l2(first.cpu().numpy(), plain.double().cpu().numpy()) <= GEMV_REL_L2
+    # the same workspace for another split shape right after (16 row groups)
+    w2, raw2 = _gpu_weight(cuda, TYPES["gf4"], 1000, 12288, seed=5)
+    need = rt.gemv_kernel(w2, nb, workspace=True)["workspace_bytes"]
+    assert need > 0
+    x2 = rng.standard_normal((nb, 12288), dtype=np.float32)
+    y2 = rt.decode_matvec(w2, _t(x2, cuda), workspace=ws if ws is not None and ws.numel() >= need else
+                          rt.decode_matvec_workspace(w2, nb, device=cuda))
+    assert om.rel_l2(y2.cpu().numpy(), om.matvec_f64(om.dequant(w2.type_id, raw2, 1000, 12288), x2)) \
+        <= GEMV_REL_L2
+
+
 HEAD_ROWS = 65549  # > 4096 row tiles: the LM-head launch plans, ragged last tile
 
 
