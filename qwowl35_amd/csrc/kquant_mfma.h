@@ -864,6 +864,8 @@ hipError_t kq_launch_cfg(const GemvArgs& a0, hipStream_t stream, int splits = 1)
         for (int s = 0; s < a.n_seg; ++s) grid += (a.seg_rows[s] + 16 * RT - 1) / (16 * RT);
     }
     const int groups = grid;
+    // every chunk of K must belong to some wave of some split
+    if ((a.k >> 8) > KS * CPW * splits) return hipErrorInvalidValue;
     const size_t ws_need = kq_split_ws_bytes(groups, splits, RT, NB, SWIGLU ? 2 : 1);
     if (splits > 1 && (a.am_token || !a.ks_ws || a.ks_ws_bytes < ws_need || (a.k >> 8) % splits != 0 ||
                        (a.k >> 8) / splits > KS * CPW || groups > kKsCounters))

@@ -472,27 +472,47 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const int a_rd = l32 * kLdsRow + half * 64;
 
+    // A step's four 16-k sub-steps run as a two-stage pipeline: the weight
+    // decode and token-tile LDS reads of sub-step kk + 1 are issued between
+    // the MFMAs of sub-step kk (explicit scheduling groups), so the decode
+    // VALU and the LDS latency overlap the matrix pipe instead of preceding it.
     auto compute = [&](const Words& w, const uint8_t* buf) {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            half8_t wf[FN], af[FM];
+        half8_t wf[2][FN], af[2][FM];
+        auto fetch = [&](int kk, int s) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 if constexpr (F16W) {
-                    wf[j] = __builtin_bit_cast(half8_t, w[j][kk]);
+                    wf[s][j] = __builtin_bit_cast(half8_t, w[j][kk]);
                 } else {
                     const uint32_t word = kk == 0 ? w[j][0].x : kk == 1 ? w[j][0].y : kk == 2 ? w[j][0].z : w[j][0].w;
-                    wf[j] = gf4_word_to_b(word, gc);
+                    wf[s][j] = gf4_word_to_b(word, gc);
                 }
             }
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                af[i] = *reinterpret_cast<const half8_t*>(buf + a_rd + i * 32 * kLdsRow + kk * 16);
+                af[s][i] = *reinterpret_cast<const half8_t*>(buf + a_rd + i * 32 * kLdsRow + kk * 16);
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int s = kk & 1;
+            if (kk < 3) fetch(kk + 1, s ^ 1);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], af[i], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[s][j], af[s][i], acc[i][j], 0, 0, 0);
+            if (kk < 3) {
+                // per MFMA: one LDS read (the first FM of them) and a share of
+                // the next sub-step's decode (15 VALU per word, FN words)
+                constexpr int kValuPerMfma = F16W ? 0 : (15 * FN + FM * FN - 1) / (FM * FN);
+#pragma unroll
+                for (int q = 0; q < FM * FN; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    if (q < FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    if (kValuPerMfma > 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
+                }
+            }
         }
     };
 
