@@ -448,9 +448,10 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
     """Config 4: GF4 prefill dequant-matmul, W 12288x4096 and 4096x12288 (12
     rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out; the staged
     path (workspace, fp16 MFMA; the time includes the staging pass) and the
-    direct path (bf16 MFMA).  Then the q8_0 projections through their fp16
-    prefill image (6 rotated copies).  Utilisation is against the nominal
-    2.5 PFLOP/s and against the MFMA probe's sustained rate on this box."""
+    direct path (bf16 MFMA).  Then the q8_0 projections (6 rotated copies),
+    dequantised inside the staged kernel and, for comparison, through their
+    fp16 prefill image.  Utilisation is against the nominal 2.5 PFLOP/s and
+    against the MFMA probe's sustained rate on this box."""
     rt, torch = b.rt, b.torch
     ceiling = mfma_ceiling(b)
     out = {"mfma_probe_TFLOP/s": round(ceiling, 1)}
@@ -484,17 +485,19 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
         q8 = [b.weight(rt.TYPE_Q8_0, rows, k) for _ in range(6)]
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
-        imgs = [w.prefill for w in q8]
+        imgs = [rt.prefill_image(w) for w in q8]
         ev1.record()
         torch.cuda.synchronize()
         out[f"prefill_image_q8_0_{rows}x{k}_us"] = round(ev0.elapsed_time(ev1) * 1e3 / len(q8), 2)
         for m in (128, 512, 2048):
             a = b.normal((m, k)).to(torch.bfloat16)
             c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
-            wsp = rt.prefill_workspace(imgs[0], m, device=b.dev)
-            calls = [lambda s, w=w: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in imgs]
-            ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
-            out[f"prefill_q8_0_f16img_m{m}_{rows}x{k}"] = line(ms, m, rows, k, "gf4_prefill_f16_kernel")
+            for tag, wl in (("", q8), ("_f16img", imgs)):
+                wsp = rt.prefill_workspace(wl[0], m, device=b.dev)
+                calls = [lambda s, w=w, wsp=wsp: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in wl]
+                ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
+                out[f"prefill_q8_0{tag}_m{m}_{rows}x{k}"] = line(
+                    ms, m, rows, k, "gf4_prefill_f16_kernel" + (" (F16 weights)" if tag else " (q8_0 weights)"))
         del q8, imgs
     return out
 

@@ -526,6 +526,8 @@ uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32
     if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || n_tokens < 1 || n_tokens > 65536) return 0;
     if (w->type_id == qw35::kTypeF16)
         return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
+    if (w->type_id == qw35::kTypeQ8_0)
+        return (uint64_t)qw35::q8_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
     if (w->type_id != qw35::kTypeGF4) return 0;
     return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
 }
@@ -534,10 +536,10 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
                             uint32_t c_dtype, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes,
                             void* stream, char* err, uintptr_t err_len) {
     if (!check_weight(w, "matmul_prefill", err, err_len)) return 0;
-    if (w->type_id != qw35::kTypeGF4 && w->type_id != qw35::kTypeF16) {
+    if (w->type_id != qw35::kTypeGF4 && w->type_id != qw35::kTypeF16 && w->type_id != qw35::kTypeQ8_0) {
         set_err(err, err_len,
-                "matmul_prefill: GF4 (type 100) or F16 (type 1) weights, got %s; make the fp16 prefill image of a "
-                "k-quant weight with qw35_hip_dequantize_f16",
+                "matmul_prefill: GF4 (type 100), q8_0 (type 8) or F16 (type 1) weights, got %s; make the fp16 "
+                "prefill image of another k-quant weight with qw35_hip_dequantize_f16",
                 type_name(w->type_id));
         return 0;
     }
@@ -561,20 +563,23 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         set_err(err, err_len, "matmul_prefill: a/awq must be 16-byte aligned and c 4-byte aligned");
         return 0;
     }
-    if (w->type_id == qw35::kTypeF16) {
+    if (w->type_id == qw35::kTypeF16 || w->type_id == qw35::kTypeQ8_0) {
+        const bool q8 = w->type_id == qw35::kTypeQ8_0;
         const uint64_t need =
             qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, qw35::PrefillCfg{32, 2, 1});
         if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
-            set_err(err, err_len, "matmul_prefill: f16 weights need a 256-byte aligned workspace of >= %llu bytes",
-                    (unsigned long long)need);
+            set_err(err, err_len, "matmul_prefill: %s weights need a 256-byte aligned workspace of >= %llu bytes",
+                    q8 ? "q8_0" : "f16", (unsigned long long)need);
             return 0;
         }
-        return check_hip(qw35::launch_f16w_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
-                                                   awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace,
-                                                   workspace_bytes, static_cast<hipStream_t>(stream)),
-                         "matmul_prefill", err, err_len)
-                   ? 1
-                   : 0;
+        const hipError_t e =
+            q8 ? qw35::launch_q8_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32, awq, c,
+                                         (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace_bytes,
+                                         static_cast<hipStream_t>(stream))
+               : qw35::launch_f16w_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32, awq, c,
+                                           (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace_bytes,
+                                           static_cast<hipStream_t>(stream));
+        return check_hip(e, "matmul_prefill", err, err_len) ? 1 : 0;
     }
     if (workspace) {
         const uint64_t need =

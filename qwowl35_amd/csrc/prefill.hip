@@ -389,7 +389,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   k-quant projection) instead of GF4 words.  A lane's 32 columns of a step
 //   are four 16-byte loads, each the MFMA operand of one sub-step as it is:
 //   no decode, and the token tile is staged in column order.
-template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false>
+// * Q8W: the weights are q8_0 blocks (34 bytes: fp16 d, 32 int8 q) read and
+//   dequantised in the kernel, no image.  A step (64 columns) is two blocks
+//   of each row; lane half h takes block h, 8 columns per sub-step, in column
+//   order like F16W.  The lane's 34 bytes start 4-byte aligned (h = 0) or 2
+//   past it (h = 1); it loads the 16-byte aligned 48 bytes around its 36-byte
+//   span (the span's dword offset in them, kt mod 4, is static in the
+//   four-step loop body; at the last step of a range it is 3, so nothing past
+//   the range is read) and realigns with v_perm.  B = fp16(d * q): the int8
+//   to exact fp16 of the decode GEMVs, then one v_pk_mul_f16 by (d, d) -- the
+//   same bits as the F16 prefill image, fp16_rne(d * q).
+template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
     constexpr int NT = 64 * NW;
@@ -434,14 +444,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         a_off[i] = ((uint32_t)gm * (uint32_t)K + (uint32_t)k_begin + (uint32_t)col * 8u) * 2u;
         a_lds[i] = row * kLdsRow + col * 16;
     }
-    constexpr int WCH = F16W ? 4 : 1;  // 16-byte weight loads per lane per 32-row tile per step
+    constexpr int WCH = F16W ? 4 : Q8W ? 3 : 1;  // 16-byte weight loads per lane per 32-row tile per step
     const uint8_t* w_src[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const size_t row = (size_t)min(n0 + 32 * j + l32, p.n - 1);
-        w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(p.w) + (row * K + k_begin + 32 * half) * 2
-                        : reinterpret_cast<const uint8_t*>(p.w + row * words_per_row + (k_begin >> 3) + 4 * half);
+        if constexpr (Q8W)
+            w_src[j] = reinterpret_cast<const uint8_t*>(p.w) + row * (size_t)(K / 32 * 34) + (k_begin / 32) * 34 +
+                       32 * half;
+        else
+            w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(p.w) + (row * K + k_begin + 32 * half) * 2
+                            : reinterpret_cast<const uint8_t*>(p.w + row * words_per_row + (k_begin >> 3) + 4 * half);
     }
+    // Q8W: byte selectors for this lane half (span dword i -> q dword i; d -> (d, d))
+    const uint32_t q8_sel = half ? 0x07060504u : 0x05040302u;
+    const uint32_t q8_dsel = half ? 0x03020302u : 0x01000100u;
+    const half2_t q8_bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const uint8_t* a_base = static_cast<const uint8_t*>(p.a);
 
     typedef uint4_t Tokens[A_CHUNKS];
@@ -456,7 +474,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int c = 0; c < WCH; ++c) w[j][c] = load_stream16(w_src[j] + (F16W ? k0 * 2 + 16 * c : k0 / 2));
+            for (int c = 0; c < WCH; ++c)
+                w[j][c] = load_stream16(w_src[j] + (Q8W  ? (k0 / 64) * 68 - 4 * ((k0 / 64) & 3) + 16 * c
+                                                    : F16W ? k0 * 2 + 16 * c
+                                                           : k0 / 2));
     };
     auto store_tokens = [&](const Tokens& a, uint8_t* buf) {
 #pragma unroll
@@ -476,12 +497,31 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // decode and token-tile LDS reads of sub-step kk + 1 are issued between
     // the MFMAs of sub-step kk (explicit scheduling groups), so the decode
     // VALU and the LDS latency overlap the matrix pipe instead of preceding it.
-    auto compute = [&](const Words& w, const uint8_t* buf) {
+    auto compute = [&](const Words& w, const uint8_t* buf, auto SPAN) {
         half8_t wf[2][FN], af[2][FM];
+        // Q8W: the lane's span starts at dword kt mod 4 of its three loads
+        constexpr int s0 = decltype(SPAN)::value;
+        auto span = [&](int j, int i) -> uint32_t {
+            const int d = s0 + i;
+            const uint4_t v = w[j][d >> 2];
+            return (d & 3) == 0 ? v.x : (d & 3) == 1 ? v.y : (d & 3) == 2 ? v.z : v.w;
+        };
         auto fetch = [&](int kk, int s) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                if constexpr (F16W) {
+                if constexpr (Q8W) {
+                    const half2_t d2 = as_half2(__builtin_amdgcn_perm(span(j, 0), span(j, 0), q8_dsel));
+                    uint32_t b[4];
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const uint32_t qs = __builtin_amdgcn_perm(span(j, 2 * kk + q + 1), span(j, 2 * kk + q), q8_sel);
+                        const uint32_t t = qs ^ 0x80808080u;  // q + 128 in each byte
+                        b[2 * q] = as_u32((as_half2(__builtin_amdgcn_perm(0x64646464u, t, 0x04010400u)) + q8_bias) * d2);
+                        b[2 * q + 1] =
+                            as_u32((as_half2(__builtin_amdgcn_perm(0x64646464u, t, 0x04030402u)) + q8_bias) * d2);
+                    }
+                    wf[s][j] = __builtin_bit_cast(half8_t, uint4_t{b[0], b[1], b[2], b[3]});
+                } else if constexpr (F16W) {
                     wf[s][j] = __builtin_bit_cast(half8_t, w[j][kk]);
                 } else {
                     const uint32_t word = kk == 0 ? w[j][0].x : kk == 1 ? w[j][0].y : kk == 2 ? w[j][0].z : w[j][0].w;
@@ -505,7 +545,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             if (kk < 3) {
                 // per MFMA: one LDS read (the first FM of them) and a share of
                 // the next sub-step's decode (15 VALU per word, FN words)
-                constexpr int kValuPerMfma = F16W ? 0 : (15 * FN + FM * FN - 1) / (FM * FN);
+                constexpr int kValuPerMfma = F16W ? 0 : ((Q8W ? 16 : 15) * FN + FM * FN - 1) / (FM * FN);
 #pragma unroll
                 for (int q = 0; q < FM * FN; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -539,20 +579,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     store_tokens(t0, buf0);
     __syncthreads();
     auto step = [&](int kt, Tokens& t_next, Words& w_next, const Words& w_cur, const uint8_t* cur,
-                    const Tokens& t_fill, uint8_t* fill) {
+                    const Tokens& t_fill, uint8_t* fill, auto SPAN) {
         const int ahead = min(kt + 2, KT - 1);
         load_tokens(ahead, t_next);
         load_words(ahead, w_next);
         __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this step's math
-        compute(w_cur, cur);
+        compute(w_cur, cur, SPAN);
         store_tokens(t_fill, fill);
         __syncthreads();
     };
     for (int kt = 0; kt < KT; kt += 4) {
-        step(kt, t0, w2, w0, buf0, t1, buf1);
-        step(kt + 1, t1, w3, w1, buf1, t0, buf0);
-        step(kt + 2, t0, w0, w2, buf0, t1, buf1);
-        step(kt + 3, t1, w1, w3, buf1, t0, buf0);
+        step(kt, t0, w2, w0, buf0, t1, buf1, std::integral_constant<int, 0>{});
+        step(kt + 1, t1, w3, w1, buf1, t0, buf0, std::integral_constant<int, 1>{});
+        step(kt + 2, t0, w0, w2, buf0, t1, buf1, std::integral_constant<int, 2>{});
+        step(kt + 3, t1, w1, w3, buf1, t0, buf0, std::integral_constant<int, 3>{});
     }
 
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
@@ -647,7 +687,7 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     }
 }
 
-template <int BM, int NW, int FN, int WPE, bool F16W = false>
+template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     constexpr int BN = 32 * FN * NW;
     const size_t lds = 2 * (size_t)BM * kLdsRow;
@@ -656,9 +696,10 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (out_f32)
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W>), grid, dim3(64 * NW), lds, s, p);
     else
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W, Q8W>), grid, dim3(64 * NW), lds, s,
+                           p);
     return hipGetLastError();
 }
 
@@ -745,22 +786,29 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // pick is the fastest or within 5% of it.
 // F16 weights (2 bytes per weight against GF4's half byte) use FN = 2 only:
 // their four-slot register ring of 16-byte loads is four times GF4's.
-PrefillCfg plan_prefill(int m, int rows, int k, bool f16w) {
+PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
     constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9;
     // K-split partial sums cost less relative to fp16 weight tiles than to GF4
     // ones: with 0.5 the F16 plan for 8192x4096 M=128 was {64,2,4} 57.1 us,
     // with 0.35 it is {128,2,8} 47.0 us; the other F16 shapes of the sweep
     // (4096 / 8192 / 12288 rows, M = 128..2048) keep their plans.
-    const double kUsPerPartialMB = f16w ? 0.35 : 0.5;
+    // q8_0 in-kernel (sweep on 8192x4096 M = 512): split 2 of 128-token tiles
+    // 100 us, 64-token tiles unsplit 140 us; with 0.5 the model picked the latter.
+    const double kUsPerPartialMB = (f16w || q8w) ? 0.35 : 0.5;
     const int cus = num_cus();
     const int chunks = k / 256;
-    const double w_bytes = f16w ? 2.0 : 0.5;
-    static constexpr int kShapes[][2] = {{128, 4}, {128, 2}, {64, 4}, {64, 2}, {32, 2}};
+    const double w_bytes = f16w ? 2.0 : q8w ? 34.0 / 32.0 : 0.5;
+    // 256-token tiles (one wave per SIMD, 256 accumulator registers) only for
+    // F16 and q8_0 weights: q8_0 8192x4096 M = 2048 200 us against 331 with
+    // 128 tokens, F16 172 against 244; GF4 was slower with them (236-260 us
+    // against 210 at 12288x4096).
+    static constexpr int kShapes[][2] = {{256, 2}, {128, 4}, {128, 2}, {64, 4}, {64, 2}, {32, 2}};
     PrefillCfg best{32, 2, 1};
     double best_us = 0;
     for (const auto& sh : kShapes) {
         const int bm = sh[0], fn = sh[1], bn = 128 * fn;
-        if (f16w && fn != 2) continue;
+        if ((f16w || q8w) && fn != 2) continue;
+        if (bm == 256 && !(f16w || q8w)) continue;
         if (bm > 32 && m <= bm / 2) continue;  // half the token tile or more would be padding
         const long tiles = (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn);
         for (int sp = 1; sp <= 16 && sp <= chunks; ++sp) {
@@ -783,7 +831,17 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w) {
     // 72.9 us.  At three blocks per CU (M=2048) it was slower, 216 -> 233 us.
     const long blocks = (long)((m + best.bm - 1) / best.bm) * ((rows + 255) / 256) * best.splits;
     if (!f16w && best.fn == 2 && best.bm >= 64 && blocks <= cus) best.waves = 8;
+    // q8_0: three 16-byte loads per 32-row tile and step in a four-slot ring
+    // (96 VGPRs at two tiles per wave), so a 256-row tile of 64 or more
+    // tokens always runs on 8 waves of one tile each.
+    if (q8w && best.bm >= 64 && best.bm <= 128) best.waves = 8;
     return best;
+}
+
+PrefillCfg plan_q8_prefill(int m, int rows, int k) { return plan_prefill(m, rows, k, false, true); }
+
+size_t q8_prefill_workspace_bytes(int m, int rows, int k) {
+    return gf4_prefill_workspace_bytes(m, rows, k, plan_q8_prefill(m, rows, k));
 }
 
 PrefillCfg plan_gf4_prefill(int m, int rows, int k) { return plan_prefill(m, rows, k, false); }
@@ -798,9 +856,11 @@ size_t gf4_prefill_workspace_bytes(int m, int rows, int k) {
     return gf4_prefill_workspace_bytes(m, rows, k, plan_gf4_prefill(m, rows, k));
 }
 
+// wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks (1 and 2 take column-order tokens and a workspace).
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
-                                  hipStream_t stream, bool f16w) {
+                                  hipStream_t stream, int wkind) {
+    const bool f16w = wkind == 1, q8w = wkind == 2;
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
     p.a = a;
@@ -822,7 +882,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
 #define QW35_STAGE(AF, AW, ORD)                                                                          \
     hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, ORD>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, \
                        a16, rs)
-        if (f16w) {
+        if (f16w || q8w) {
             if (af) {
                 if (aw) QW35_STAGE(true, true, false); else QW35_STAGE(true, false, false);
             } else {
@@ -846,8 +906,17 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const bool split = cfg.splits > 1;
         if (split) p.c = partial;
         const bool kf32 = of || split;
-        if (f16w) {
+        if (q8w) {
             switch (cfg.bm * 10 + cfg.fn) {
+                case 2562: e = launch_f16_tile<256, 4, 2, 1, false, true>(p, kf32, stream); break;
+                case 1282: e = launch_f16_tile<128, 8, 1, 2, false, true>(p, kf32, stream); break;
+                case 642: e = launch_f16_tile<64, 8, 1, 2, false, true>(p, kf32, stream); break;
+                case 322: e = launch_f16_tile<32, 4, 2, 2, false, true>(p, kf32, stream); break;
+                default: return hipErrorInvalidValue;
+            }
+        } else if (f16w) {
+            switch (cfg.bm * 10 + cfg.fn) {
+                case 2562: e = launch_f16_tile<256, 4, 2, 1, true>(p, kf32, stream); break;
                 case 1282: e = launch_f16_tile<128, 4, 2, 1, true>(p, kf32, stream); break;
                 case 642: e = launch_f16_tile<64, 4, 2, 2, true>(p, kf32, stream); break;
                 case 322: e = launch_f16_tile<32, 4, 2, 2, true>(p, kf32, stream); break;
@@ -898,7 +967,18 @@ hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, in
         do --cfg.splits;
         while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
     }
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, true);
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 1);
+}
+
+hipError_t launch_q8_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
+                             int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!workspace) return hipErrorInvalidValue;
+    PrefillCfg cfg = plan_q8_prefill(m, rows, k);
+    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
+        do --cfg.splits;
+        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
+    }
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 2);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {
@@ -915,7 +995,7 @@ hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int
         do --cfg.splits;
         while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
     }
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, false);
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 0);
 }
 
 }  // namespace qw35

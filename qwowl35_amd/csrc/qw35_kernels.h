@@ -115,7 +115,7 @@ hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, h
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream);
 
 struct PrefillCfg {
-    int bm;      // tokens per block: 128, 64 or 32
+    int bm;      // tokens per block: 256 (F16 / q8_0 weights), 128, 64 or 32
     int fn;      // 32-row weight tiles per wave (4 waves per block): 2 or 4 (4 needs bm >= 64)
     int splits;  // K splits; k / splits must be a multiple of 256
     // 8: the same bm x 256 tile on 8 waves of one 32-row weight tile each
@@ -127,7 +127,7 @@ size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg);
 size_t gf4_prefill_workspace_bytes(int m, int rows, int k);
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
-                                  bool f16w = false);
+                                  int wkind = 0);  // 0 GF4, 1 F16, 2 q8_0
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
@@ -136,6 +136,12 @@ hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int
 // workspace is required (at least the staged tokens and scales; its full
 // size, f16w_prefill_workspace_bytes, also holds the K-split partials).
 size_t f16w_prefill_workspace_bytes(int m, int rows, int k);
+// q8_0 weights dequantised inside the staged kernel (no image); a workspace of
+// at least gf4_prefill_workspace_bytes(m, rows, k, {.., 1}) is required.
+PrefillCfg plan_q8_prefill(int m, int rows, int k);
+size_t q8_prefill_workspace_bytes(int m, int rows, int k);
+hipError_t launch_q8_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
+                             int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
                                int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 

@@ -68,9 +68,10 @@ class HipWeight:
 
     @property
     def prefill(self) -> "HipWeight":
-        """The weight ``matmul_prefill`` takes: itself for GF4 / F16, else its fp16
-        prefill image (``prefill_image``), made on first use and kept."""
-        if self.type_id in (TYPE_GF4, TYPE_F16):
+        """The weight ``matmul_prefill`` takes: itself for GF4 / F16 / q8_0 (q8_0
+        is dequantised inside the prefill kernel), else its fp16 prefill image
+        (``prefill_image``), made on first use and kept."""
+        if self.type_id in (TYPE_GF4, TYPE_F16, TYPE_Q8_0):
             return self
         img = getattr(self, "_prefill", None)
         if img is None:
@@ -335,8 +336,9 @@ def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tenso
 def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = None,
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
                    workspace: torch.Tensor | None | bool = True, stream=None) -> torch.Tensor:
-    """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4 or F16 weight (``encodeTiledKMatmul``;
-    a k-quant weight enters as its fp16 image, ``w.prefill``).
+    """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4, q8_0 or F16 weight
+    (``encodeTiledKMatmul``; the other k-quants enter as their fp16 image,
+    ``w.prefill``).  q8_0 and F16 need a workspace.
 
     ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
     ``out_dtype`` (bfloat16, rounded to nearest even, or float32).
@@ -370,9 +372,9 @@ def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None,
     """Multi-token matvec of fp32 activations [n_tokens, k] (``encodeMatvecBatch``, +FFN.m:260-306).
 
     1..8 tokens run the decode GEMV (fp32 activations); longer chunks run the
-    prefill matmul with fp32 output (GF4 directly, the k-quants through
-    their fp16 prefill image), as the reference switches to its tiled matmul
-    for multi-token chunks.
+    prefill matmul with fp32 output (GF4 and q8_0 directly, the other
+    k-quants through their fp16 prefill image), as the reference switches to
+    its tiled matmul for multi-token chunks.
     """
     if x.dim() != 2:
         raise Qw35Error("matvec_batch takes [n_tokens, k] activations")
