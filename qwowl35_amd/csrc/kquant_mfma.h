@@ -463,8 +463,11 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                         for (int j = 0; j < 8; ++j)
                             dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(ga[j], gf4_word_to_b(ww[j], gc), dd, 0, 0, 0);
                         acc[t][m][0] = __builtin_fmaf(inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
-                        acc[t][m][1] = __builtin_fmaf(inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
+                        if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
                     } else if constexpr (FMT == kFmtQ8) {
+                        // sum_j d_j (hi + lo partial of block j) per batch row; the chunk's
+                        // inverse activation scale (a power of two) once at the end
+                        float cs0 = 0.0f, cs1 = 0.0f;
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
                             // qs bytes [2 + 8 kq, +8) of block j: 4-byte aligned for odd j, 2 mod 4 for even j
@@ -487,9 +490,11 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
                             const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
                             const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                                 aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                            acc[t][m][0] = __builtin_fmaf(dsc * inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
-                            acc[t][m][1] = __builtin_fmaf(dsc * inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
+                            cs0 = __builtin_fmaf(dsc, dd[0] + dd[1], cs0);
+                            if constexpr (NB > 1) cs1 = __builtin_fmaf(dsc, dd[2] + dd[3], cs1);
                         }
+                        acc[t][m][0] = __builtin_fmaf(inv_sc[0], cs0, acc[t][m][0]);
+                        if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(inv_sc[1], cs1, acc[t][m][1]);
                     } else if constexpr (FMT == kFmtGF2) {
                         // Step j (32 columns): lane group kq decodes word 2j + (kq >> 1),
                         // codes m and m + 8 for m = 4(kq & 1) .. +3, as pairs in the order
