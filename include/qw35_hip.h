@@ -410,7 +410,11 @@ const void *qw35_hip_runtime_store(void *runtime);
  * largest) and contracted on fp16 MFMA; shapes with too few output tiles for
  * the device also split K, with fp32 partial sums in the workspace reduced in
  * a fixed order.  Without a workspace the loader converts the activations and
- * contracts on bf16 MFMA.  Both compute the same products.  The size depends
+ * contracts on bf16 MFMA.  Both compute the products of bf16_rne(awq * a) and
+ * the weights exactly for every activation of at least 2^-28 of its token
+ * row's largest magnitude (the fp16 staging holds every such bf16 value
+ * exactly); smaller activations are rounded by the staging, at most 2^-39 of
+ * the row's largest.  The size depends
  * on the weight's shape and n_tokens (0: invalid weight or n_tokens); a
  * smaller workspace that still holds the staged activations (2 bytes per
  * activation plus 4 per token, each part rounded up to 256 bytes) is
