@@ -30,10 +30,13 @@
  *   type   1  F16  1 elem / 2 B (tensors.rs:137): the prefill matmul's weight
  *             form for the k-quants (see qw35_hip_dequantize_f16); the GEMVs
  *             reject it
- * Shape limits of this build: k % 256 == 0 and 256 <= k <= 12288 (every
- * Qwen3.5-9B projection has k = 4096 or 12288; Q6_K also needs k % 2048 == 0
- * so that its 210-byte super-block rows stay 16-byte aligned), rows >= 1,
- * n_batch 1..8.
+ * Shape limits of this build: k % 256 == 0 and 256 <= k <= 65536 (the
+ * GEMVs take rows longer than 12288 in rounds of 32 chunks of 256 columns;
+ * q8_0, whose blocks are 32 columns, needs k % 256 == 0 too, as every
+ * Qwen3.5 projection has); Q6_K also needs k % 512 == 0 and rows * row bytes
+ * a multiple of 16 (its 210-byte super-blocks are read as the 16-byte
+ * segments that cover them); rows >= 1; n_batch 1..8; a prefill call takes
+ * n_tokens * k <= 2^30.
  */
 #ifndef QW35_HIP_H
 #define QW35_HIP_H

@@ -55,7 +55,12 @@ const char* type_name(uint32_t t) {
     }
 }
 
-constexpr uint64_t kMaxK = 12288;
+// Longest row: the GEMVs cover any k in rounds of their plan's chunks; 65536
+// keeps every in-kernel byte offset of a 64-row tile and of the prefill's
+// staged token rows within 32 bits.
+constexpr uint64_t kMaxK = 65536;
+// Largest n_tokens * k of a prefill call (its fp16 token rows span < 2^31 bytes).
+constexpr uint64_t kMaxPrefillElems = 1ull << 30;
 
 bool check_weight(const qw35_hip_weight* w, const char* what, char* err, uintptr_t err_len) {
     if (!w) {
@@ -79,14 +84,16 @@ bool check_weight(const qw35_hip_weight* w, const char* what, char* err, uintptr
                 (unsigned long long)w->k, (unsigned long long)kMaxK);
         return false;
     }
-    if (w->type_id == qw35::kTypeQ6_K && w->k % 2048 != 0) {
-        // 210-byte super-blocks: rows are 16-byte aligned only for k % 2048 == 0
-        set_err(err, err_len, "%s: q6_k needs k %% 2048 == 0 (16-byte aligned rows), got k=%llu", what,
-                (unsigned long long)w->k);
-        return false;
-    }
     if (w->rows == 0 || w->rows > 0x7fffffffull) {
         set_err(err, err_len, "%s: rows=%llu out of range", what, (unsigned long long)w->rows);
+        return false;
+    }
+    if (w->type_id == qw35::kTypeQ6_K && (w->k % 512 != 0 || row_bytes(w->type_id, w->k) * w->rows % 16 != 0)) {
+        // 210-byte super-blocks, read as the 16-byte segments that cover them: rows
+        // start at 4-byte boundaries for k % 512 == 0, and a matrix of a multiple of
+        // 16 bytes ends where the last row's last segment does
+        set_err(err, err_len, "%s: q6_k needs k %% 512 == 0 and rows * row bytes %% 16 == 0, got k=%llu rows=%llu",
+                what, (unsigned long long)w->k, (unsigned long long)w->rows);
         return false;
     }
     const uint64_t want = row_bytes(w->type_id, w->k) * w->rows;
@@ -523,7 +530,9 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight* w, void* dst, void* stream, c
 
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
     char msg[8];
-    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || n_tokens < 1 || n_tokens > 65536) return 0;
+    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || n_tokens < 1 || n_tokens > 65536 ||
+        (uint64_t)n_tokens * w->k > kMaxPrefillElems)
+        return 0;
     if (w->type_id == qw35::kTypeF16)
         return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
     if (w->type_id == qw35::kTypeQ8_0)
@@ -549,6 +558,11 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
     }
     if (n_tokens < 1 || n_tokens > 65536) {
         set_err(err, err_len, "matmul_prefill: n_tokens=%u must be in 1..65536", n_tokens);
+        return 0;
+    }
+    if ((uint64_t)n_tokens * w->k > kMaxPrefillElems) {  // staged token offsets are 32-bit byte offsets
+        set_err(err, err_len, "matmul_prefill: n_tokens * k = %llu must be <= %llu",
+                (unsigned long long)n_tokens * w->k, (unsigned long long)kMaxPrefillElems);
         return 0;
     }
     if (w->rows > (1ull << 24)) {  // keeps every launch grid within 2^31 blocks

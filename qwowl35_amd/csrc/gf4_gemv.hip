@@ -394,6 +394,7 @@ hipError_t launch_cfg(const GemvArgs& a, hipStream_t stream) {
     constexpr bool BD = NB <= QW35_GF4_BD_MAX_BATCH;
     const size_t lds = lds_bytes<NB, RT, KS, CPW, SWIGLU, BD>();
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+    if ((a.k >> 8) > KS * CPW) return hipErrorInvalidValue;  // every chunk belongs to a wave
     const int grid = (a.rows + 16 * RT - 1) / (16 * RT);
     if (a.info) {
         snprintf(a.info->name, sizeof a.info->name, "gf4_mfma_gemv<%d, %d, %d, %d, %s, %s, %s>", NB, RT, KS, CPW,
@@ -498,8 +499,10 @@ hipError_t launch_gf4_any(const GemvArgs& a, hipStream_t stream) {
 hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream) {
     // When the activations of the whole batch do not fit this kernel's LDS it
     // would stream the weights once per batch slice; the chunked kernel (per-chunk
-    // activation staging) takes the batch in one launch.
-    if (a.n_batch > gf4_batch_slice(a, a.w_up != nullptr)) return launch_gf4_gemv_chunked(a, stream);
+    // activation staging) takes the batch in one launch.  It also takes k beyond
+    // 48 chunks (12288), which no plan of this kernel covers.
+    if ((a.k >> 8) > 48 || a.n_batch > gf4_batch_slice(a, a.w_up != nullptr))
+        return launch_gf4_gemv_chunked(a, stream);
     return a.w_up ? launch_gf4_any<true>(a, stream) : launch_gf4_any<false>(a, stream);
 }
 

@@ -213,11 +213,13 @@ struct KqLds {
     static constexpr int kBytes = kSxOff + kSx;
 };
 
-// Wave w owns chunks [w*CPW, (w+1)*CPW) of all RT row tiles.  Loads run P
-// chunks ahead: chunk c's activations and weight segments are issued (in that
-// order) when chunk c-P has been consumed, into register slot c % P.
-template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU, bool HAS_AWQ>
-__global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
+// Wave w owns chunks [w*CPW, (w+1)*CPW) of all RT row tiles, and, when the K
+// slice is longer than KS*CPW chunks, the same chunks of each further round of
+// KS*CPW.  Loads run P chunks ahead within a round: chunk c's activations and
+// weight segments are issued (in that order) when chunk c-P has been consumed,
+// into register slot c % P.
+template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU, bool HAS_AWQ, bool ROUNDS>
+__device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     using F = Fmt<FMT>;
     using L = KqLds<FMT, NB>;
@@ -295,10 +297,13 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
             loff[t][i] = (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)(s % F::kSegs);
         }
 
+    // First chunk of the current round: a workgroup's KS x CPW chunks cover its
+    // K slice in rounds, one round unless k is longer than the plan covers.
+    int rb = 0;
     auto issue = [&](auto CI) {
         constexpr int c = decltype(CI)::value;
         constexpr int sl = c % P;
-        int chunk = wave * CPW + c;
+        int chunk = rb + wave * CPW + c;
         chunk = cbase + (chunk < cps ? chunk : 0);
         const float* xc = args.x + (size_t)chunk * 256;
         if constexpr (FMT == kFmtGF4) {
@@ -328,7 +333,17 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
 #pragma unroll
             for (int t = 0; t < RT; ++t)
 #pragma unroll
-                for (int i = 0; i < LPT; ++i) wv[sl][t * NM + m][i] = load_stream16(wbase + loff[t][i]);
+                for (int i = 0; i < LPT; ++i) {
+                    if constexpr (FMT == kFmtQ6K) {
+                        // Rows of k % 2048 != 0 start 4, 8 or 12 bytes past a 16-byte
+                        // boundary (the low bits of loff): the 16-byte segment holding
+                        // the chunk's first byte may then be the next one.
+                        const uint32_t q15 = (uint32_t)(chunk * 210) & 15u;
+                        wv[sl][t * NM + m][i] = load_stream16(wbase + ((loff[t][i] + q15) & ~15u));
+                    } else {
+                        wv[sl][t * NM + m][i] = load_stream16(wbase + loff[t][i]);
+                    }
+                }
         }
         // loads complete in issue order: keep chunk c's ahead of chunk c + 1's
         __builtin_amdgcn_sched_barrier(0);
@@ -346,334 +361,348 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) acc[t][m][0] = acc[t][m][1] = 0.0f;
 
-    kq_static_for<CPW>([&](auto CI) {
-        constexpr int c = decltype(CI)::value;
-        constexpr int sl = c % P;
-        constexpr int later = (CPW - 1 - c) < (P - 1) ? (CPW - 1 - c) : (P - 1);  // chunks issued after c
-        kq_wait_vmcnt<later * LPC>();
-        const bool live = wave * CPW + c < cps;
-        if (live) {
-            // Stage chunk c's activations: fp16 hi/lo with a per-chunk power-of-two
-            // scale.  The NB row maxima are reduced together (wave_max_rows); the
-            // scale and its inverse are uniform integer work; hi = fp16(v s) and
-            // lo = fp16(v s - hi) are single mixed-precision FMAs (v s is exact).
-            float4_t v[NB];
-            uint32_t mx[NB];
+    for (;;) {
+        kq_static_for<CPW>([&](auto CI) {
+            constexpr int c = decltype(CI)::value;
+            constexpr int sl = c % P;
+            constexpr int later = (CPW - 1 - c) < (P - 1) ? (CPW - 1 - c) : (P - 1);  // chunks issued after c
+            kq_wait_vmcnt<later * LPC>();
+            const bool live = rb + wave * CPW + c < cps;
+            if (live) {
+                // Stage chunk c's activations: fp16 hi/lo with a per-chunk power-of-two
+                // scale.  The NB row maxima are reduced together (wave_max_rows); the
+                // scale and its inverse are uniform integer work; hi = fp16(v s) and
+                // lo = fp16(v s - hi) are single mixed-precision FMAs (v s is exact).
+                float4_t v[NB];
+                uint32_t mx[NB];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                v[b] = xv[sl][b];
-                if (HAS_AWQ) v[b] *= av[sl];
-                mx[b] = __builtin_bit_cast(uint32_t, fmaxf(fmaxf(fabsf(v[b][0]), fabsf(v[b][1])),
-                                                           fmaxf(fabsf(v[b][2]), fabsf(v[b][3]))));
-            }
-            uint32_t smax[NB];
-            wave_max_rows<NB>(mx, smax, lane);
-            uint32_t isc_bits[NB];
+                for (int b = 0; b < NB; ++b) {
+                    v[b] = xv[sl][b];
+                    if (HAS_AWQ) v[b] *= av[sl];
+                    mx[b] = __builtin_bit_cast(uint32_t, fmaxf(fmaxf(fabsf(v[b][0]), fabsf(v[b][1])),
+                                                               fmaxf(fabsf(v[b][2]), fabsf(v[b][3]))));
+                }
+                uint32_t smax[NB];
+                wave_max_rows<NB>(mx, smax, lane);
+                uint32_t isc_bits[NB];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                float sc, isc;
-                fp16_range_scale_bits(smax[b], sc, isc);
-                isc_bits[b] = __builtin_bit_cast(uint32_t, isc);
-                float e[4] = {v[b][0], v[b][1], v[b][2], v[b][3]};
-                if constexpr (FMT == kFmtGF4) {
-                    // (x0, x1, x4, x5) -> x0 x4 x1 x5 (and the odd lane's likewise)
-                    e[1] = v[b][2];
-                    e[2] = v[b][1];
-                } else if constexpr (FMT == kFmtGF2) {
-                    // Columns 16w..16w+15 stored as x0 x8 x1 x9 .. x3 x11 | x4 x12 .. x7 x15
-                    // (MFMA k-slots of lane groups 2(w&1), 2(w&1)+1): the lanes holding
-                    // columns 0..3 / 4..7 write (x_c, x_c+8) pairs of their first two
-                    // columns, the lanes holding 8..11 / 12..15 those of the last two.
-                    float u[4];
+                for (int b = 0; b < NB; ++b) {
+                    float sc, isc;
+                    fp16_range_scale_bits(smax[b], sc, isc);
+                    isc_bits[b] = __builtin_bit_cast(uint32_t, isc);
+                    float e[4] = {v[b][0], v[b][1], v[b][2], v[b][3]};
+                    if constexpr (FMT == kFmtGF4) {
+                        // (x0, x1, x4, x5) -> x0 x4 x1 x5 (and the odd lane's likewise)
+                        e[1] = v[b][2];
+                        e[2] = v[b][1];
+                    } else if constexpr (FMT == kFmtGF2) {
+                        // Columns 16w..16w+15 stored as x0 x8 x1 x9 .. x3 x11 | x4 x12 .. x7 x15
+                        // (MFMA k-slots of lane groups 2(w&1), 2(w&1)+1): the lanes holding
+                        // columns 0..3 / 4..7 write (x_c, x_c+8) pairs of their first two
+                        // columns, the lanes holding 8..11 / 12..15 those of the last two.
+                        float u[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor2>(v[b][q]);
-                    if (lane & 2) {
-                        e[0] = u[2]; e[1] = v[b][2]; e[2] = u[3]; e[3] = v[b][3];
-                    } else {
-                        e[0] = v[b][0]; e[1] = u[0]; e[2] = v[b][1]; e[3] = u[1];
+                        for (int q = 0; q < 4; ++q) u[q] = dpp_f32<kDppQuadXor2>(v[b][q]);
+                        if (lane & 2) {
+                            e[0] = u[2]; e[1] = v[b][2]; e[2] = u[3]; e[3] = v[b][3];
+                        } else {
+                            e[0] = v[b][0]; e[1] = u[0]; e[2] = v[b][1]; e[3] = u[1];
+                        }
+                    }
+                    // GF2 k-slot of the lane's four values (natural order otherwise)
+                    const int apos = FMT == kFmtGF2 ? 32 * (lane >> 3) + 16 * ((lane >> 2) & 1) + 8 * (lane & 1) +
+                                                          4 * ((lane >> 1) & 1)
+                                                    : 4 * lane;
+                    half2_t hi0, hi1, lo0, lo1;
+                    hi0.x = (_Float16)__builtin_fmaf(e[0], sc, 0.0f);
+                    hi0.y = (_Float16)__builtin_fmaf(e[1], sc, 0.0f);
+                    hi1.x = (_Float16)__builtin_fmaf(e[2], sc, 0.0f);
+                    hi1.y = (_Float16)__builtin_fmaf(e[3], sc, 0.0f);
+                    lo0.x = (_Float16)__builtin_fmaf(e[0], sc, -(float)hi0.x);
+                    lo0.y = (_Float16)__builtin_fmaf(e[1], sc, -(float)hi0.y);
+                    lo1.x = (_Float16)__builtin_fmaf(e[2], sc, -(float)hi1.x);
+                    lo1.y = (_Float16)__builtin_fmaf(e[3], sc, -(float)hi1.y);
+                    *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + apos) =
+                        uint2_t_{as_u32(hi0), as_u32(hi1)};
+                    *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + apos) =
+                        uint2_t_{as_u32(lo0), as_u32(lo1)};
+                    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K) {
+                        // sum of the scaled activations of each 32-column sub-block (8 lanes)
+                        float s4 = (v[b][0] + v[b][1]) + (v[b][2] + v[b][3]);
+                        s4 += dpp_f32<kDppQuadXor1>(s4);
+                        s4 += dpp_f32<kDppQuadXor2>(s4);
+                        s4 += dpp_f32<kDppRowHalfMirror>(s4);
+                        if ((lane & 7) == 7) sx[b * 8 + (lane >> 3)] = s4 * sc;
                     }
                 }
-                // GF2 k-slot of the lane's four values (natural order otherwise)
-                const int apos = FMT == kFmtGF2 ? 32 * (lane >> 3) + 16 * ((lane >> 2) & 1) + 8 * (lane & 1) +
-                                                      4 * ((lane >> 1) & 1)
-                                                : 4 * lane;
-                half2_t hi0, hi1, lo0, lo1;
-                hi0.x = (_Float16)__builtin_fmaf(e[0], sc, 0.0f);
-                hi0.y = (_Float16)__builtin_fmaf(e[1], sc, 0.0f);
-                hi1.x = (_Float16)__builtin_fmaf(e[2], sc, 0.0f);
-                hi1.y = (_Float16)__builtin_fmaf(e[3], sc, 0.0f);
-                lo0.x = (_Float16)__builtin_fmaf(e[0], sc, -(float)hi0.x);
-                lo0.y = (_Float16)__builtin_fmaf(e[1], sc, -(float)hi0.y);
-                lo1.x = (_Float16)__builtin_fmaf(e[2], sc, -(float)hi1.x);
-                lo1.y = (_Float16)__builtin_fmaf(e[3], sc, -(float)hi1.y);
-                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b) * L::kActStride + apos) =
-                    uint2_t_{as_u32(hi0), as_u32(hi1)};
-                *reinterpret_cast<uint2_t_*>(xs + (size_t)(2 * b + 1) * L::kActStride + apos) =
-                    uint2_t_{as_u32(lo0), as_u32(lo1)};
-                if constexpr (FMT == kFmtQ4K || FMT == kFmtQ5K) {
-                    // sum of the scaled activations of each 32-column sub-block (8 lanes)
-                    float s4 = (v[b][0] + v[b][1]) + (v[b][2] + v[b][3]);
-                    s4 += dpp_f32<kDppQuadXor1>(s4);
-                    s4 += dpp_f32<kDppQuadXor2>(s4);
-                    s4 += dpp_f32<kDppRowHalfMirror>(s4);
-                    if ((lane & 7) == 7) sx[b * 8 + (lane >> 3)] = s4 * sc;
+                float inv_sc[2];  // batches 2kq and 2kq+1
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    uint32_t bits = 0x3F800000u;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        if (b == 2 * kq + jj) bits = isc_bits[b];
+                    inv_sc[jj] = __builtin_bit_cast(float, bits);
                 }
-            }
-            float inv_sc[2];  // batches 2kq and 2kq+1
+                const bool a_live = n < 2 * n_batch;
+                const _Float16* arow =
+                    a_live ? xs + (size_t)n * L::kActStride : reinterpret_cast<const _Float16*>(wblk + L::kZeroOff);
+                const int a_step = a_live ? 32 : 0;
+                // GF4: the chunk's activation operands, shared by every tile (words 8kq + j).
+                half8_t ga[FMT == kFmtGF4 ? 8 : 1];
+                if constexpr (FMT == kFmtGF4) {
+                    const _Float16* ap = a_live ? arow + 64 * kq : arow;
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                uint32_t bits = 0x3F800000u;
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-                    if (b == 2 * kq + jj) bits = isc_bits[b];
-                inv_sc[jj] = __builtin_bit_cast(float, bits);
-            }
-            const bool a_live = n < 2 * n_batch;
-            const _Float16* arow =
-                a_live ? xs + (size_t)n * L::kActStride : reinterpret_cast<const _Float16*>(wblk + L::kZeroOff);
-            const int a_step = a_live ? 32 : 0;
-            // GF4: the chunk's activation operands, shared by every tile (words 8kq + j).
-            half8_t ga[FMT == kFmtGF4 ? 8 : 1];
-            if constexpr (FMT == kFmtGF4) {
-                const _Float16* ap = a_live ? arow + 64 * kq : arow;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) ga[j] = *reinterpret_cast<const half8_t*>(ap + (a_live ? 8 * j : 0));
-            }
+                    for (int j = 0; j < 8; ++j) ga[j] = *reinterpret_cast<const half8_t*>(ap + (a_live ? 8 * j : 0));
+                }
 
 #pragma unroll
-            for (int t = 0; t < RT; ++t) {
+                for (int t = 0; t < RT; ++t) {
 #pragma unroll
-                for (int m = 0; m < NM; ++m) {
-                    // Transpose tile t of matrix m through LDS.
+                    for (int m = 0; m < NM; ++m) {
+                        // Transpose tile t of matrix m through LDS.
 #pragma unroll
-                    for (int q = 0; q < LPT; ++q) {
-                        const int s = lane + 64 * q;
-                        if (s < 16 * F::kSegs)
-                            *reinterpret_cast<uint4_t*>(xb + (s / F::kSegs) * F::kStride + 16 * (s % F::kSegs)) =
-                                wv[sl][t * NM + m][q];
-                    }
-                    wave_sync_lds();
-                    const uint8_t* wrow = xb + n * F::kStride;
-                    if constexpr (FMT == kFmtGF4) {
-                        const uint4_t w0 = *reinterpret_cast<const uint4_t*>(wrow + 32 * kq);
-                        const uint4_t w1 = *reinterpret_cast<const uint4_t*>(wrow + 32 * kq + 16);
-                        const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                        float4_t dd = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(ga[j], gf4_word_to_b(ww[j], gc), dd, 0, 0, 0);
-                        acc[t][m][0] = __builtin_fmaf(inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
-                        if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
-                    } else if constexpr (FMT == kFmtQ8) {
-                        // sum_j d_j (hi + lo partial of block j) per batch row; the chunk's
-                        // inverse activation scale (a power of two) once at the end
-                        float cs0 = 0.0f, cs1 = 0.0f;
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            // qs bytes [2 + 8 kq, +8) of block j: 4-byte aligned for odd j, 2 mod 4 for even j
-                            const int off = 34 * j + 2 + 8 * kq;
-                            uint32_t d0, d1;
-                            if ((j & 1) == 1) {
-                                d0 = *reinterpret_cast<const uint32_t*>(wrow + off);
-                                d1 = *reinterpret_cast<const uint32_t*>(wrow + off + 4);
-                            } else {
-                                const uint32_t* base = reinterpret_cast<const uint32_t*>(wrow + off - 2);
-                                const uint32_t e0 = base[0], e1 = base[1], e2 = base[2];
-                                d0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
-                                d1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
-                            }
-                            const float dsc = (float)*reinterpret_cast<const _Float16*>(wrow + 34 * j);
-                            uint32_t b4[4];
-                            s8x4_to_h(d0, bias, b4[0], b4[1]);
-                            s8x4_to_h(d1, bias, b4[2], b4[3]);
-                            const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
-                            const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
-                            const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                            cs0 = __builtin_fmaf(dsc, dd[0] + dd[1], cs0);
-                            if constexpr (NB > 1) cs1 = __builtin_fmaf(dsc, dd[2] + dd[3], cs1);
+                        for (int q = 0; q < LPT; ++q) {
+                            const int s = lane + 64 * q;
+                            if (s < 16 * F::kSegs)
+                                *reinterpret_cast<uint4_t*>(xb + (s / F::kSegs) * F::kStride + 16 * (s % F::kSegs)) =
+                                    wv[sl][t * NM + m][q];
                         }
-                        acc[t][m][0] = __builtin_fmaf(inv_sc[0], cs0, acc[t][m][0]);
-                        if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(inv_sc[1], cs1, acc[t][m][1]);
-                    } else if constexpr (FMT == kFmtGF2) {
-                        // Step j (32 columns): lane group kq decodes word 2j + (kq >> 1),
-                        // codes m and m + 8 for m = 4(kq & 1) .. +3, as pairs in the order
-                        // the activations were staged.  Mantissa 2q over 1024:
-                        // (1024 + 2q) / 4 - 256.75 = (2q - 3) / 4, exact; times s exact
-                        // (5 significant bits); y = 4/3 sum B x.
-                        const int hw = kq >> 1;
-                        const uint4_t scv = *reinterpret_cast<const uint4_t*>(wrow + 64);
-                        const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
-                        // (byte << 8) in both halves: byte hw (even j) or 2 + hw (odd j) of dword j/2
-                        const uint32_t sel_even = 0x000C000Cu | (uint32_t)hw * 0x01000100u;
-                        const uint32_t sel_odd = 0x020C020Cu | (uint32_t)hw * 0x01000100u;
-                        const uint32_t* words = reinterpret_cast<const uint32_t*>(wrow) + hw;
-                        const int csh = 8 * (kq & 1);
-                        float4_t dd = {0.f, 0.f, 0.f, 0.f};
+                        wave_sync_lds();
+                        const uint8_t* wrow = xb + n * F::kStride;
+                        if constexpr (FMT == kFmtGF4) {
+                            const uint4_t w0 = *reinterpret_cast<const uint4_t*>(wrow + 32 * kq);
+                            const uint4_t w1 = *reinterpret_cast<const uint4_t*>(wrow + 32 * kq + 16);
+                            const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                            float4_t dd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            const uint32_t cw = words[2 * j] >> csh;
-                            const half2_t s2 = as_half2(__builtin_amdgcn_perm(scw[j >> 1], scw[j >> 1],
-                                                                              (j & 1) ? sel_odd : sel_even));
-                            const uint32_t pr[4] = {cw << 1, cw >> 1, cw >> 3, cw >> 5};
-                            uint32_t b4[4];
-#pragma unroll
-                            for (int p = 0; p < 4; ++p) {
-                                const half2_t pq = as_half2(and_xor(pr[p], 0x00060006u, 0x64006400u));
-                                b4[p] = as_u32(__builtin_elementwise_fma(pq, h2(0.25f, 0.25f), h2(-256.75f, -256.75f)) *
-                                               s2);
-                            }
-                            const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
-                            const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
-                            dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, dd, 0, 0, 0);
-                        }
-                        constexpr float kFourThirds = 4.0f / 3.0f;
-                        acc[t][m][0] = __builtin_fmaf(inv_sc[0] * kFourThirds, dd[0] + dd[1], acc[t][m][0]);
-                        if constexpr (NB > 1)
-                            acc[t][m][1] = __builtin_fmaf(inv_sc[1] * kFourThirds, dd[2] + dd[3], acc[t][m][1]);
-                    } else if constexpr (FMT == kFmtQ6K) {
-                        // The super-block starts `off` bytes into the row buffer
-                        // (even, wave-uniform); words are read 4-aligned and, for the
-                        // chunks at 2 mod 4, realigned by two bytes.
-                        const int off = ((cbase + wave * CPW + c) * 210) & 15;
-                        const uint8_t* sb = wrow + (off & ~3);
-                        const _Float16* abase = a_live ? arow + 4 * kq : arow;  // arow: the zero row when !a_live
-                        const int astep = a_live ? 16 : 0;
-                        auto q6k_chunk = [&](auto ALIGNED) {
-                            auto ld = [&](int o) {
-                                const uint32_t* p = reinterpret_cast<const uint32_t*>(sb + o);
-                                if constexpr (decltype(ALIGNED)::value) return p[0];
-                                else return __builtin_amdgcn_alignbyte(p[1], p[0], 2);
-                            };
-                            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(ld(208) & 0xFFFFu));
-                            uint32_t scw[4];
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) scw[q] = ld(192 + 4 * q);
-                            // sum_s sc_s * sum (q - 32) x in fp32; d and the inverse
-                            // activation scale once per chunk.
+                            for (int j = 0; j < 8; ++j)
+                                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(ga[j], gf4_word_to_b(ww[j], gc), dd, 0, 0,
+                                                                            0);
+                            acc[t][m][0] = __builtin_fmaf(inv_sc[0], dd[0] + dd[1], acc[t][m][0]);
+                            if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(inv_sc[1], dd[2] + dd[3], acc[t][m][1]);
+                        } else if constexpr (FMT == kFmtQ8) {
+                            // sum_j d_j (hi + lo partial of block j) per batch row; the chunk's
+                            // inverse activation scale (a power of two) once at the end
                             float cs0 = 0.0f, cs1 = 0.0f;
 #pragma unroll
-                            for (int s4 = 0; s4 < 16; s4 += 4) {
-                                float4_t dd[4];
-#pragma unroll
-                                for (int u = 0; u < 4; ++u) {
-                                    const int sbk = s4 + u;
-                                    const int h = sbk >> 3, g = (sbk & 7) >> 1, p = sbk & 1;
-                                    const uint32_t qlw = ld(64 * h + 32 * (g & 1) + 16 * p + 4 * kq);
-                                    const uint32_t qhw = ld(128 + 32 * h + 16 * p + 4 * kq);
-                                    const uint32_t nib = ((g >> 1) ? (qlw >> 4) : qlw) & 0x0F0F0F0Fu;
-                                    const uint32_t qv = nib | (((qhw >> (2 * g)) & 0x03030303u) << 4);
-                                    uint32_t b0, b1;
-                                    u4x4_to_h(qv, bias, b0, b1);
-                                    const half4_t bop = __builtin_bit_cast(half4_t, uint2_t_{b0, b1});
-                                    const half4_t aop = *reinterpret_cast<const half4_t*>(abase + astep * sbk);
-                                    dd[u] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, bop, float4_t{0.f, 0.f, 0.f, 0.f},
-                                                                                0, 0, 0);
+                            for (int j = 0; j < 8; ++j) {
+                                // qs bytes [2 + 8 kq, +8) of block j: 4-byte aligned for odd j, 2 mod 4 for even j
+                                const int off = 34 * j + 2 + 8 * kq;
+                                uint32_t d0, d1;
+                                if ((j & 1) == 1) {
+                                    d0 = *reinterpret_cast<const uint32_t*>(wrow + off);
+                                    d1 = *reinterpret_cast<const uint32_t*>(wrow + off + 4);
+                                } else {
+                                    const uint32_t* base = reinterpret_cast<const uint32_t*>(wrow + off - 2);
+                                    const uint32_t e0 = base[0], e1 = base[1], e2 = base[2];
+                                    d0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
+                                    d1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
                                 }
-#pragma unroll
-                                for (int u = 0; u < 4; ++u) {
-                                    const int sbk = s4 + u;
-                                    const float scf = (float)(int)(int8_t)((scw[sbk >> 2] >> (8 * (sbk & 3))) & 0xFFu);
-                                    cs0 = __builtin_fmaf(scf, dd[u][0] + dd[u][1], cs0);
-                                    if constexpr (NB > 1) cs1 = __builtin_fmaf(scf, dd[u][2] + dd[u][3], cs1);
-                                }
-                            }
-                            acc[t][m][0] = __builtin_fmaf(d * inv_sc[0], cs0, acc[t][m][0]);
-                            if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(d * inv_sc[1], cs1, acc[t][m][1]);
-                        };
-                        if ((off & 3) == 0)
-                            q6k_chunk(std::true_type{});
-                        else
-                            q6k_chunk(std::false_type{});
-                    } else {  // Q4_K, Q5_K
-                        const uint4_t hd = *reinterpret_cast<const uint4_t*>(wrow);
-                        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)hd.x);
-                        const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x >> 16));
-                        // 6-bit scales and mins of the 8 sub-blocks, one per byte (get_scale_min_k4).
-                        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu;
-                        const uint32_t mn_lo = hd.z & 0x3F3F3F3Fu;
-                        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-                        const uint32_t mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-                        // batches past NB read row NB-1 (their results are never stored)
-                        const int b0 = min(2 * kq, NB - 1), b1 = min(2 * kq + 1, NB - 1);
-                        const float4_t sxa = *reinterpret_cast<const float4_t*>(sx + b0 * 8);
-                        const float4_t sxb = *reinterpret_cast<const float4_t*>(sx + b0 * 8 + 4);
-                        const float4_t sxc = *reinterpret_cast<const float4_t*>(sx + b1 * 8);
-                        const float4_t sxd = *reinterpret_cast<const float4_t*>(sx + b1 * 8 + 4);
-                        const float sx0[8] = {sxa[0], sxa[1], sxa[2], sxa[3], sxb[0], sxb[1], sxb[2], sxb[3]};
-                        const float sx1[8] = {sxc[0], sxc[1], sxc[2], sxc[3], sxd[0], sxd[1], sxd[2], sxd[3]};
-                        // Sub-block scales as exact fp16 pairs (sc_2i, sc_2i+1) and their
-                        // -1024 multiples (|sc| < 64, so -1024 sc is exact).
-                        half2_t scp[4], nbp[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const uint32_t w = i < 2 ? sc_lo : sc_hi;
-                            scp[i] = as_half2(__builtin_amdgcn_perm(0x64646464u, w, (i & 1) ? 0x04030402u : 0x04010400u)) +
-                                     h2(-1024.0f, -1024.0f);
-                            nbp[i] = scp[i] * h2(-1024.0f, -1024.0f);
-                        }
-                        // B = sc_j * q as one fused multiply-add of the biased 1024 + q:
-                        // (1024 + q) sc - 1024 sc = sc q <= 63 * 31, exact; the eight MFMAs
-                        // then accumulate sum_j sc_j sum q x in one register set.
-                        // Q5_K: bit j of qh byte l (bytes 8kq.. of this lane) is bit 4 of q.
-                        constexpr int kQs = FMT == kFmtQ5K ? 48 : 16;
-                        const uint2_t_ qh = FMT == kFmtQ5K ? *reinterpret_cast<const uint2_t_*>(wrow + 16 + 8 * kq)
-                                                           : uint2_t_{0u, 0u};
-                        float4_t dd = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int cc = 0; cc < 4; ++cc) {
-                            const uint2_t_ qd = *reinterpret_cast<const uint2_t_*>(wrow + kQs + 32 * cc + 8 * kq);
-#pragma unroll
-                            for (int hi = 0; hi < 2; ++hi) {
-                                const int j = 2 * cc + hi;
-                                uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
-                                uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
-                                if constexpr (FMT == kFmtQ5K) {
-                                    const uint32_t h0 = j <= 4 ? qh.x << (4 - j) : qh.x >> (j - 4);
-                                    const uint32_t h1 = j <= 4 ? qh.y << (4 - j) : qh.y >> (j - 4);
-                                    t0 |= h0 & 0x10101010u;
-                                    t1 |= h1 & 0x10101010u;
-                                }
-                                const half2_t sp = scp[j >> 1], np = nbp[j >> 1];
-                                const half2_t s2 = (j & 1) ? half2_t{sp.y, sp.y} : half2_t{sp.x, sp.x};
-                                const half2_t n2 = (j & 1) ? half2_t{np.y, np.y} : half2_t{np.x, np.x};
+                                const float dsc = (float)*reinterpret_cast<const _Float16*>(wrow + 34 * j);
                                 uint32_t b4[4];
-                                b4[0] = as_u32(__builtin_elementwise_fma(
-                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04010400u)), s2, n2));
-                                b4[1] = as_u32(__builtin_elementwise_fma(
-                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04030402u)), s2, n2));
-                                b4[2] = as_u32(__builtin_elementwise_fma(
-                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04010400u)), s2, n2));
-                                b4[3] = as_u32(__builtin_elementwise_fma(
-                                    as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04030402u)), s2, n2));
+                                s8x4_to_h(d0, bias, b4[0], b4[1]);
+                                s8x4_to_h(d1, bias, b4[2], b4[3]);
+                                const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
+                                const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
+                                const float4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                                cs0 = __builtin_fmaf(dsc, dd[0] + dd[1], cs0);
+                                if constexpr (NB > 1) cs1 = __builtin_fmaf(dsc, dd[2] + dd[3], cs1);
+                            }
+                            acc[t][m][0] = __builtin_fmaf(inv_sc[0], cs0, acc[t][m][0]);
+                            if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(inv_sc[1], cs1, acc[t][m][1]);
+                        } else if constexpr (FMT == kFmtGF2) {
+                            // Step j (32 columns): lane group kq decodes word 2j + (kq >> 1),
+                            // codes m and m + 8 for m = 4(kq & 1) .. +3, as pairs in the order
+                            // the activations were staged.  Mantissa 2q over 1024:
+                            // (1024 + 2q) / 4 - 256.75 = (2q - 3) / 4, exact; times s exact
+                            // (5 significant bits); y = 4/3 sum B x.
+                            const int hw = kq >> 1;
+                            const uint4_t scv = *reinterpret_cast<const uint4_t*>(wrow + 64);
+                            const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+                            // (byte << 8) in both halves: byte hw (even j) or 2 + hw (odd j) of dword j/2
+                            const uint32_t sel_even = 0x000C000Cu | (uint32_t)hw * 0x01000100u;
+                            const uint32_t sel_odd = 0x020C020Cu | (uint32_t)hw * 0x01000100u;
+                            const uint32_t* words = reinterpret_cast<const uint32_t*>(wrow) + hw;
+                            const int csh = 8 * (kq & 1);
+                            float4_t dd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const uint32_t cw = words[2 * j] >> csh;
+                                const half2_t s2 = as_half2(__builtin_amdgcn_perm(scw[j >> 1], scw[j >> 1],
+                                                                                  (j & 1) ? sel_odd : sel_even));
+                                const uint32_t pr[4] = {cw << 1, cw >> 1, cw >> 3, cw >> 5};
+                                uint32_t b4[4];
+#pragma unroll
+                                for (int p = 0; p < 4; ++p) {
+                                    const half2_t pq = as_half2(and_xor(pr[p], 0x00060006u, 0x64006400u));
+                                    b4[p] = as_u32(
+                                        __builtin_elementwise_fma(pq, h2(0.25f, 0.25f), h2(-256.75f, -256.75f)) * s2);
+                                }
                                 const half8_t bop = __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
                                 const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
                                 dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, dd, 0, 0, 0);
                             }
-                        }
-                        // y += d sum_j sc_j sum q x - dmin sum_j m_j sum x
-                        float ms0 = 0.0f, ms1 = 0.0f;
+                            constexpr float kFourThirds = 4.0f / 3.0f;
+                            acc[t][m][0] = __builtin_fmaf(inv_sc[0] * kFourThirds, dd[0] + dd[1], acc[t][m][0]);
+                            if constexpr (NB > 1)
+                                acc[t][m][1] = __builtin_fmaf(inv_sc[1] * kFourThirds, dd[2] + dd[3], acc[t][m][1]);
+                        } else if constexpr (FMT == kFmtQ6K) {
+                            // The super-block starts `off` bytes into the row buffer: the
+                            // chunk's offset past a 16-byte boundary plus the row's own
+                            // (n row_bytes mod 16, a multiple of 4; rows past the matrix,
+                            // whose results are never stored, take row n's, so reads stay
+                            // inside the buffer).  Words are read 4-aligned and, for the
+                            // chunks at 2 mod 4, realigned by two bytes.
+                            const int q15 = ((cbase + rb + wave * CPW + c) * 210) & 15;
+                            const int off = (q15 + (int)(((uint32_t)n * (uint32_t)row_bytes) & 15u)) & 15;
+                            const uint8_t* sb = wrow + (off & ~3);
+                            const _Float16* abase = a_live ? arow + 4 * kq : arow;  // arow: the zero row when !a_live
+                            const int astep = a_live ? 16 : 0;
+                            auto q6k_chunk = [&](auto ALIGNED) {
+                                auto ld = [&](int o) {
+                                    const uint32_t* p = reinterpret_cast<const uint32_t*>(sb + o);
+                                    if constexpr (decltype(ALIGNED)::value) return p[0];
+                                    else return __builtin_amdgcn_alignbyte(p[1], p[0], 2);
+                                };
+                                const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(ld(208) & 0xFFFFu));
+                                uint32_t scw[4];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
-                            const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
-                            ms0 = __builtin_fmaf(mnj, sx0[j], ms0);
-                            if constexpr (NB > 1) ms1 = __builtin_fmaf(mnj, sx1[j], ms1);
+                                for (int q = 0; q < 4; ++q) scw[q] = ld(192 + 4 * q);
+                                // sum_s sc_s * sum (q - 32) x in fp32; d and the inverse
+                                // activation scale once per chunk.
+                                float cs0 = 0.0f, cs1 = 0.0f;
+#pragma unroll
+                                for (int s4 = 0; s4 < 16; s4 += 4) {
+                                    float4_t dd[4];
+#pragma unroll
+                                    for (int u = 0; u < 4; ++u) {
+                                        const int sbk = s4 + u;
+                                        const int h = sbk >> 3, g = (sbk & 7) >> 1, p = sbk & 1;
+                                        const uint32_t qlw = ld(64 * h + 32 * (g & 1) + 16 * p + 4 * kq);
+                                        const uint32_t qhw = ld(128 + 32 * h + 16 * p + 4 * kq);
+                                        const uint32_t nib = ((g >> 1) ? (qlw >> 4) : qlw) & 0x0F0F0F0Fu;
+                                        const uint32_t qv = nib | (((qhw >> (2 * g)) & 0x03030303u) << 4);
+                                        uint32_t b0, b1;
+                                        u4x4_to_h(qv, bias, b0, b1);
+                                        const half4_t bop = __builtin_bit_cast(half4_t, uint2_t_{b0, b1});
+                                        const half4_t aop = *reinterpret_cast<const half4_t*>(abase + astep * sbk);
+                                        dd[u] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                                            aop, bop, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                                    }
+#pragma unroll
+                                    for (int u = 0; u < 4; ++u) {
+                                        const int sbk = s4 + u;
+                                        const float scf =
+                                            (float)(int)(int8_t)((scw[sbk >> 2] >> (8 * (sbk & 3))) & 0xFFu);
+                                        cs0 = __builtin_fmaf(scf, dd[u][0] + dd[u][1], cs0);
+                                        if constexpr (NB > 1) cs1 = __builtin_fmaf(scf, dd[u][2] + dd[u][3], cs1);
+                                    }
+                                }
+                                acc[t][m][0] = __builtin_fmaf(d * inv_sc[0], cs0, acc[t][m][0]);
+                                if constexpr (NB > 1) acc[t][m][1] = __builtin_fmaf(d * inv_sc[1], cs1, acc[t][m][1]);
+                            };
+                            if ((q15 & 3) == 0)  // off & 3 == q15 & 3 on every lane
+                                q6k_chunk(std::true_type{});
+                            else
+                                q6k_chunk(std::false_type{});
+                        } else {  // Q4_K, Q5_K
+                            const uint4_t hd = *reinterpret_cast<const uint4_t*>(wrow);
+                            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)hd.x);
+                            const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x >> 16));
+                            // 6-bit scales and mins of the 8 sub-blocks, one per byte (get_scale_min_k4).
+                            const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu;
+                            const uint32_t mn_lo = hd.z & 0x3F3F3F3Fu;
+                            const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+                            const uint32_t mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                            // batches past NB read row NB-1 (their results are never stored)
+                            const int b0 = min(2 * kq, NB - 1), b1 = min(2 * kq + 1, NB - 1);
+                            const float4_t sxa = *reinterpret_cast<const float4_t*>(sx + b0 * 8);
+                            const float4_t sxb = *reinterpret_cast<const float4_t*>(sx + b0 * 8 + 4);
+                            const float4_t sxc = *reinterpret_cast<const float4_t*>(sx + b1 * 8);
+                            const float4_t sxd = *reinterpret_cast<const float4_t*>(sx + b1 * 8 + 4);
+                            const float sx0[8] = {sxa[0], sxa[1], sxa[2], sxa[3], sxb[0], sxb[1], sxb[2], sxb[3]};
+                            const float sx1[8] = {sxc[0], sxc[1], sxc[2], sxc[3], sxd[0], sxd[1], sxd[2], sxd[3]};
+                            // Sub-block scales as exact fp16 pairs (sc_2i, sc_2i+1) and their
+                            // -1024 multiples (|sc| < 64, so -1024 sc is exact).
+                            half2_t scp[4], nbp[4];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const uint32_t w = i < 2 ? sc_lo : sc_hi;
+                                scp[i] = as_half2(__builtin_amdgcn_perm(0x64646464u, w,
+                                                                        (i & 1) ? 0x04030402u : 0x04010400u)) +
+                                         h2(-1024.0f, -1024.0f);
+                                nbp[i] = scp[i] * h2(-1024.0f, -1024.0f);
+                            }
+                            // B = sc_j * q as one fused multiply-add of the biased 1024 + q:
+                            // (1024 + q) sc - 1024 sc = sc q <= 63 * 31, exact; the eight MFMAs
+                            // then accumulate sum_j sc_j sum q x in one register set.
+                            // Q5_K: bit j of qh byte l (bytes 8kq.. of this lane) is bit 4 of q.
+                            constexpr int kQs = FMT == kFmtQ5K ? 48 : 16;
+                            const uint2_t_ qh = FMT == kFmtQ5K ? *reinterpret_cast<const uint2_t_*>(wrow + 16 + 8 * kq)
+                                                               : uint2_t_{0u, 0u};
+                            float4_t dd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int cc = 0; cc < 4; ++cc) {
+                                const uint2_t_ qd = *reinterpret_cast<const uint2_t_*>(wrow + kQs + 32 * cc + 8 * kq);
+#pragma unroll
+                                for (int hi = 0; hi < 2; ++hi) {
+                                    const int j = 2 * cc + hi;
+                                    uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
+                                    uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
+                                    if constexpr (FMT == kFmtQ5K) {
+                                        const uint32_t h0 = j <= 4 ? qh.x << (4 - j) : qh.x >> (j - 4);
+                                        const uint32_t h1 = j <= 4 ? qh.y << (4 - j) : qh.y >> (j - 4);
+                                        t0 |= h0 & 0x10101010u;
+                                        t1 |= h1 & 0x10101010u;
+                                    }
+                                    const half2_t sp = scp[j >> 1], np = nbp[j >> 1];
+                                    const half2_t s2 = (j & 1) ? half2_t{sp.y, sp.y} : half2_t{sp.x, sp.x};
+                                    const half2_t n2 = (j & 1) ? half2_t{np.y, np.y} : half2_t{np.x, np.x};
+                                    uint32_t b4[4];
+                                    b4[0] = as_u32(__builtin_elementwise_fma(
+                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04010400u)), s2, n2));
+                                    b4[1] = as_u32(__builtin_elementwise_fma(
+                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04030402u)), s2, n2));
+                                    b4[2] = as_u32(__builtin_elementwise_fma(
+                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04010400u)), s2, n2));
+                                    b4[3] = as_u32(__builtin_elementwise_fma(
+                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04030402u)), s2, n2));
+                                    const half8_t bop =
+                                        __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
+                                    const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
+                                    dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, dd, 0, 0, 0);
+                                }
+                            }
+                            // y += d sum_j sc_j sum q x - dmin sum_j m_j sum x
+                            float ms0 = 0.0f, ms1 = 0.0f;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
+                                const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
+                                ms0 = __builtin_fmaf(mnj, sx0[j], ms0);
+                                if constexpr (NB > 1) ms1 = __builtin_fmaf(mnj, sx1[j], ms1);
+                            }
+                            const float v0 = __builtin_fmaf(-dmin, ms0, d * (dd[0] + dd[1]));
+                            acc[t][m][0] = __builtin_fmaf(inv_sc[0], v0, acc[t][m][0]);
+                            if constexpr (NB > 1) {
+                                const float v1 = __builtin_fmaf(-dmin, ms1, d * (dd[2] + dd[3]));
+                                acc[t][m][1] = __builtin_fmaf(inv_sc[1], v1, acc[t][m][1]);
+                            }
                         }
-                        const float v0 = __builtin_fmaf(-dmin, ms0, d * (dd[0] + dd[1]));
-                        acc[t][m][0] = __builtin_fmaf(inv_sc[0], v0, acc[t][m][0]);
-                        if constexpr (NB > 1) {
-                            const float v1 = __builtin_fmaf(-dmin, ms1, d * (dd[2] + dd[3]));
-                            acc[t][m][1] = __builtin_fmaf(inv_sc[1], v1, acc[t][m][1]);
-                        }
+                        // The next tile (or chunk) rewrites the transpose and activation buffers.
+                        wave_sync_lds();
                     }
-                    // The next tile (or chunk) rewrites the transpose and activation buffers.
-                    wave_sync_lds();
                 }
             }
-        }
-        if constexpr (c + P < CPW) issue(std::integral_constant<int, c + P>{});
-    });
+            if constexpr (c + P < CPW) issue(std::integral_constant<int, c + P>{});
+        });
+        if constexpr (!ROUNDS) break;
+        rb += KS * CPW;
+        if (rb >= cps) break;
+        kq_static_for<P>([&](auto CI) { issue(CI); });
+    }
 
     // Partials of the KS waves meet in LDS; lane group kq holds batches 2kq, 2kq+1.
 #pragma unroll
@@ -786,6 +815,18 @@ __global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
     }
 }
 
+// One round: the plan's KS x CPW chunks cover the K slice.
+template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU, bool HAS_AWQ>
+__global__ __launch_bounds__(64 * KS) void kq_mfma_gemv(GemvArgs args) {
+    kq_gemv_body<FMT, NB, RT, KS, CPW, P, SWIGLU, HAS_AWQ, false>(args);
+}
+
+// Rows longer than one round covers (k beyond 12288 columns).
+template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU, bool HAS_AWQ>
+__global__ __launch_bounds__(64 * KS) void kq_mfma_gemv_long(GemvArgs args) {
+    kq_gemv_body<FMT, NB, RT, KS, CPW, P, SWIGLU, HAS_AWQ, true>(args);
+}
+
 struct KqPlan {
     int rt, ks, cpw, p;
     int s = 1;  // K splits across workgroups (needs a workspace)
@@ -810,6 +851,8 @@ inline KqPlan plan_kq(int fmt, int rows, int k, int nb, bool split_ok = false) {
     // against 17.9 / 21.0 unsplit; two-chunk waves or two-tile workgroups
     // 14.6-22 us).  At k = 4096 no split beat the unsplit q8_0 launch.
     if (split_ok && nb >= 4 && tiles <= 256 && chunks == 48) return {4, 12, 1, 1, 4};
+    // Longer rows: eight waves of four chunks per round (kq_mfma_gemv_long).
+    if (chunks > 48) return {1, 8, 4, 2};
     if (chunks <= 4) return {1, 4, 1, 1};
     if (chunks <= 8) return {1, 8, 1, 1};
     if (chunks <= 16) {
@@ -858,7 +901,7 @@ inline size_t kq_split_ws_bytes(int groups, int splits, int rt, int nb, int nm) 
     return splits > 1 ? kKsPartOffset + ((size_t)groups * splits * rt * nb * 16 * nm * 4 + 255) / 256 * 256 : 0;
 }
 
-template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU>
+template <int FMT, int NB, int RT, int KS, int CPW, int P, bool SWIGLU, bool LONG = false>
 hipError_t kq_launch_cfg(const GemvArgs& a0, hipStream_t stream, int splits = 1) {
     const size_t lds = kq_lds_bytes<FMT, NB, RT, KS, CPW, SWIGLU>();
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
@@ -869,11 +912,11 @@ hipError_t kq_launch_cfg(const GemvArgs& a0, hipStream_t stream, int splits = 1)
         for (int s = 0; s < a.n_seg; ++s) grid += (a.seg_rows[s] + 16 * RT - 1) / (16 * RT);
     }
     const int groups = grid;
-    // every chunk of K must belong to some wave of some split
-    if ((a.k >> 8) > KS * CPW * splits) return hipErrorInvalidValue;
+    // every chunk of K belongs to some wave of some split, in one round or (LONG) several
+    if (!LONG && (a.k >> 8) > KS * CPW * splits) return hipErrorInvalidValue;
     const size_t ws_need = kq_split_ws_bytes(groups, splits, RT, NB, SWIGLU ? 2 : 1);
     if (splits > 1 && (a.am_token || !a.ks_ws || a.ks_ws_bytes < ws_need || (a.k >> 8) % splits != 0 ||
-                       (a.k >> 8) / splits > KS * CPW || groups > kKsCounters))
+                       (!LONG && (a.k >> 8) / splits > KS * CPW) || groups > kKsCounters))
         return hipErrorInvalidValue;
     a.splits = splits;
     if (splits > 1) {
@@ -885,8 +928,9 @@ hipError_t kq_launch_cfg(const GemvArgs& a0, hipStream_t stream, int splits = 1)
     // batch row: refuse a launch shape with more workgroups than that.
     if (a.am_token && grid != argmax_groups(Fmt<FMT>::kTypeId, a.rows, a.k, a.n_batch)) return hipErrorInvalidValue;
     if (a.info) {
-        snprintf(a.info->name, sizeof a.info->name, "kq_mfma_gemv<%d, %d, %d, %d, %d, %d, %s, %s>", FMT, NB, RT, KS,
-                 CPW, P, SWIGLU ? "true" : "false", a.awq ? "true" : "false");
+        snprintf(a.info->name, sizeof a.info->name, "%s<%d, %d, %d, %d, %d, %d, %s, %s>",
+                 LONG ? "kq_mfma_gemv_long" : "kq_mfma_gemv", FMT, NB, RT, KS, CPW, P, SWIGLU ? "true" : "false",
+                 a.awq ? "true" : "false");
         a.info->grid = (unsigned)grid;
         a.info->block = 64u * KS;
         a.info->lds = (unsigned)lds;
@@ -894,12 +938,21 @@ hipError_t kq_launch_cfg(const GemvArgs& a0, hipStream_t stream, int splits = 1)
         a.info->ws_bytes = ws_need;
         return hipSuccess;
     }
-    if (a.awq)
-        hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds,
-                           stream, a);
-    else
-        hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, false>), dim3(grid), dim3(64 * KS), lds,
-                           stream, a);
+    if constexpr (LONG) {
+        if (a.awq)
+            hipLaunchKernelGGL((kq_mfma_gemv_long<FMT, NB, RT, KS, CPW, P, SWIGLU, true>), dim3(grid), dim3(64 * KS),
+                               lds, stream, a);
+        else
+            hipLaunchKernelGGL((kq_mfma_gemv_long<FMT, NB, RT, KS, CPW, P, SWIGLU, false>), dim3(grid),
+                               dim3(64 * KS), lds, stream, a);
+    } else {
+        if (a.awq)
+            hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, true>), dim3(grid), dim3(64 * KS), lds,
+                               stream, a);
+        else
+            hipLaunchKernelGGL((kq_mfma_gemv<FMT, NB, RT, KS, CPW, P, SWIGLU, false>), dim3(grid), dim3(64 * KS),
+                               lds, stream, a);
+    }
     return hipGetLastError();
 }
 
@@ -918,6 +971,8 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
         total_rows = 0;
         for (int s = 0; s < a.n_seg; ++s) total_rows += a.seg_rows[s];
     }
+    if ((a.k >> 8) > 48)  // the long-row plan of plan_kq, in rounds of 32 chunks
+        return kq_launch_cfg<FMT, NB, 1, 8, 4, (kq_fits<FMT, NB, 1, 2, SWIGLU>() ? 2 : 1), SWIGLU, true>(a, stream);
     KqPlan p = plan_kq(FMT, total_rows, a.k, NB, a.ks_ws != nullptr && !a.am_token);
     if (p.s > 1) {
         int groups = (a.rows + 16 * p.rt - 1) / (16 * p.rt);

@@ -90,31 +90,29 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
                                                                       const float* __restrict__ awq, int k,
                                                                       uint16_t* __restrict__ a16,
                                                                       float* __restrict__ row_scale) {
-    constexpr int kMaxGroups = 12288 / 8 / kStageThreads;  // groups of 8 columns per thread
+    // Up to 12288 columns stay in registers between the two passes; longer rows
+    // are read again for the second.
+    constexpr int kMaxGroups = 12288 / 8 / kStageThreads;  // resident groups of 8 columns per thread
     const int row = blockIdx.x;
     const int groups = k >> 3;
-    float v[kMaxGroups][8];
-    float mx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxGroups; ++j) {
-        const int g = threadIdx.x + j * kStageThreads;
-        if (g >= groups) break;
+    // A' = bf16_rne(awq * A) of columns 8g..8g+7, as fp32
+    auto load8 = [&](int g, float (&o)[8]) {
         const size_t e0 = (size_t)row * k + 8 * g;
         if constexpr (A_F32) {
             const float4_t lo = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a) + e0);
             const float4_t hi = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a) + e0 + 4);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                v[j][q] = lo[q];
-                v[j][4 + q] = hi[q];
+                o[q] = lo[q];
+                o[4 + q] = hi[q];
             }
         } else {
             const uint4_t u = *reinterpret_cast<const uint4_t*>(static_cast<const uint16_t*>(a) + e0);
             const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                v[j][2 * q] = bf16_lo(w4[q]);
-                v[j][2 * q + 1] = bf16_hi(w4[q]);
+                o[2 * q] = bf16_lo(w4[q]);
+                o[2 * q + 1] = bf16_hi(w4[q]);
             }
         }
         if constexpr (HAS_AWQ || A_F32) {
@@ -129,14 +127,28 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
                 }
             }
 #pragma unroll
-            for (int q = 0; q < 8; q += 2) {  // A' = bf16_rne(awq * A), kept as fp32
-                const uint32_t pk = pack_bf16(v[j][q] * s8[q], v[j][q + 1] * s8[q + 1]);
-                v[j][q] = bf16_lo(pk);
-                v[j][q + 1] = bf16_hi(pk);
+            for (int q = 0; q < 8; q += 2) {
+                const uint32_t pk = pack_bf16(o[q] * s8[q], o[q + 1] * s8[q + 1]);
+                o[q] = bf16_lo(pk);
+                o[q + 1] = bf16_hi(pk);
             }
         }
+    };
+    float v[kMaxGroups][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxGroups; ++j) {
+        const int g = threadIdx.x + j * kStageThreads;
+        if (g >= groups) break;
+        load8(g, v[j]);
 #pragma unroll
         for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
+    }
+    for (int g = threadIdx.x + kMaxGroups * kStageThreads; g < groups; g += kStageThreads) {
+        float t[8];
+        load8(g, t);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(t[q]));
     }
     __shared__ float red[kStageThreads / 64];
     mx = wave_max_abs(mx);
@@ -145,16 +157,23 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float sc = 2.0f * fp16_range_scale(mx);  // max in [2^14, 2^15)
     if (threadIdx.x == 0) row_scale[row] = pow2_inverse(sc);
-#pragma unroll
-    for (int j = 0; j < kMaxGroups; ++j) {
-        const int g = threadIdx.x + j * kStageThreads;
-        if (g >= groups) break;
-        const float* x = v[j];
+    auto store8 = [&](int g, const float (&x)[8]) {
         const uint4_t out = GF4_ORDER ? uint4_t{as_u32(h2(x[0] * sc, x[4] * sc)), as_u32(h2(x[1] * sc, x[5] * sc)),
                                                 as_u32(h2(x[2] * sc, x[6] * sc)), as_u32(h2(x[3] * sc, x[7] * sc))}
                                       : uint4_t{as_u32(h2(x[0] * sc, x[1] * sc)), as_u32(h2(x[2] * sc, x[3] * sc)),
                                                 as_u32(h2(x[4] * sc, x[5] * sc)), as_u32(h2(x[6] * sc, x[7] * sc))};
         *reinterpret_cast<uint4_t*>(a16 + (size_t)row * k + 8 * g) = out;
+    };
+#pragma unroll
+    for (int j = 0; j < kMaxGroups; ++j) {
+        const int g = threadIdx.x + j * kStageThreads;
+        if (g >= groups) break;
+        store8(g, v[j]);
+    }
+    for (int g = threadIdx.x + kMaxGroups * kStageThreads; g < groups; g += kStageThreads) {
+        float t[8];
+        load8(g, t);
+        store8(g, t);
     }
 }
 

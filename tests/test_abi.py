@@ -128,7 +128,7 @@ def _call_matvec(w, x=4096, dst=4096, nb=1, awq=None):
     [
         (dict(type_id=15), "unsupported tensor type 15"),
         (dict(k=100), "multiple of 256"),
-        (dict(k=16384), "<= 12288"),
+        (dict(k=65792), "<= 65536"),
         (dict(rows=0), "rows=0"),
         (dict(nbytes=5), "must be 32768 bytes, got 5"),
         (dict(data=4097), "16-byte aligned"),
@@ -273,9 +273,14 @@ def test_stream_read_validates(lib):
 
 
 def test_q6k_weight_needs_aligned_rows(lib):
-    with pytest.raises(_ffi.Qw35Error, match=re.escape("q6_k needs k % 2048 == 0")):
-        _call_matvec(_weight(type_id=14, k=1280))
-    _ffi.call("qw35_hip_weight_view", C.byref(_q6k_desc(4096)), C.c_void_p(1 << 20), C.byref(_ffi.Weight()))
+    needle = "q6_k needs k % 512 == 0 and rows * row bytes % 16 == 0"
+    with pytest.raises(_ffi.Qw35Error, match=re.escape(needle + ", got k=1280 rows=16")):
+        _call_matvec(_weight(type_id=14, k=1280))  # 1050-byte rows: 2-byte aligned
+    # 2100-byte rows (4 mod 16): 4-byte aligned, the matrix a multiple of 16 bytes only for rows % 4 == 0
+    with pytest.raises(_ffi.Qw35Error, match=re.escape(needle + ", got k=2560 rows=6")):
+        _call_matvec(_weight(type_id=14, k=2560, rows=6))
+    for k, rows in ((4096, 8), (2560, 8), (5120, 2)):
+        _ffi.call("qw35_hip_weight_view", C.byref(_q6k_desc(k, rows)), C.c_void_p(1 << 20), C.byref(_ffi.Weight()))
 
 
 def _q6k_desc(k, rows=8):
@@ -319,3 +324,13 @@ def test_output_argmax_workspace_and_validation(lib):
         call(ws=(1 << 20) + 16)
     with pytest.raises(_ffi.Qw35Error, match="16-byte aligned"):
         call(x=4100)
+
+
+def test_matmul_prefill_rejects_oversized_token_rows(lib):
+    """n_tokens * k beyond 2^30 is refused before anything is launched (the
+    staged fp16 token rows are addressed with 32-bit byte offsets)."""
+    w = _weight(type_id=100, k=65536, rows=16)
+    assert lib.qw35_hip_matmul_prefill_workspace_size(C.byref(w), 16385) == 0
+    with pytest.raises(_ffi.Qw35Error, match=re.escape("n_tokens * k = 1073807360 must be <= 1073741824")):
+        _ffi.call("qw35_hip_matmul_prefill", C.byref(w), C.c_void_p(4096), 1, None, C.c_void_p(4096), 0, 16385,
+                  C.c_void_p(4096), C.c_uint64(1 << 40), None)

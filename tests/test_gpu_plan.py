@@ -132,7 +132,7 @@ def test_plan_merges_projections_sharing_inputs(cuda, name, nb):
 
     rt = _rt()
     t = TYPES[name]
-    k = 2048 if name == "q6_k" else 512  # Q6_K rows are 16-byte aligned for k % 2048 == 0
+    k = 2048 if name == "q6_k" else 512  # Q6_K: a 7-row matrix is a multiple of 16 bytes at k = 2048
     rng = np.random.default_rng(40 + nb)
     rows = [160, 32, 48, 7, 96]
     ws = [rt.HipWeight.upload(make_weight(t, r, k, seed=100 + i)[0], t, r, k, device=cuda)

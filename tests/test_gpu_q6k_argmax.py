@@ -100,6 +100,51 @@ def test_q6k_gemv(cuda, nb, rows, k):
     assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
 
 
+# Rows of k % 2048 != 0 start 4, 8 or 12 bytes past a 16-byte boundary:
+# 2560 -> 2100-byte rows (4 mod 16), 5120 -> 4200 (8), 9728 -> 7980 (12).
+@pytest.mark.parametrize("rows,k", [(100, 2560), (102, 5120), (36, 9728), (2, 5120), (4, 2560)])
+@pytest.mark.parametrize("nb", [1, 3, 8])
+def test_q6k_gemv_unaligned_rows(cuda, rows, k, nb):
+    import torch
+
+    print(f"q6_k gemv {rows}x{k} nb={nb}", flush=True)
+    rng = np.random.default_rng(rows + k + nb)
+    raw = _random_q6k_raw(rng, rows, k)
+    deq = oq6.q6_k_dequant(raw, rows, k)
+    x = activations(rng, nb, k)
+    w = _rt().HipWeight.upload(raw, om.TYPE_Q6_K, rows, k)
+    y = _rt().decode_matvec(w, _t(x, cuda)).cpu().numpy()
+    assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
+    a = awq_scales(rng, k)
+    y0 = rng.standard_normal((nb, rows)).astype(np.float32)
+    dst = torch.from_numpy(y0.copy()).to(cuda)
+    _rt().decode_matvec(w, _t(x, cuda), dst=dst, residual=True, awq=_t(a, cuda))
+    assert om.rel_l2(dst.cpu().numpy(), y0.astype(np.float64) + om.matvec_f64(deq, x, a)) <= GEMV_REL_L2
+    # every row within the bar relative to its batch row's RMS output: a misread row (the last
+    # one's final 16-byte segment ends the matrix) fails here even where rel-L2 over all would not
+    ref = om.matvec_f64(deq, x)
+    scale = np.linalg.norm(ref, axis=1, keepdims=True) / np.sqrt(rows)
+    assert np.all(np.abs(y - ref) <= GEMV_REL_L2 * scale + 1e-6)
+
+
+@pytest.mark.parametrize("nb", [1, 5])
+def test_q6k_head_unaligned_rows(cuda, nb):
+    """The fused greedy head on a 5120-column Q6_K head (4200-byte rows) equals
+    the rule on the same launch shape's logits, and its logits match fp64."""
+    rows, k = 4000, 5120
+    rng = np.random.default_rng(nb)
+    raw, deq = _q6k(rows, k, seed=nb)
+    x = activations(rng, nb, k)
+    w = _rt().HipWeight.upload(raw, om.TYPE_Q6_K, rows, k)
+    xt = _t(x, cuda)
+    logits = _rt().decode_matvec(w, xt).cpu().numpy()
+    assert om.rel_l2(logits, om.matvec_f64(deq, x)) <= GEMV_REL_L2
+    tok, lg = _rt().output_argmax(w, xt)
+    ids, best = om.argmax_rule(logits)
+    assert np.array_equal(tok.cpu().numpy().view(np.uint32), ids)
+    assert np.array_equal(_bits(lg.cpu().numpy()), _bits(best))
+
+
 def test_q6k_gemv_awq_residual_and_random_blocks(cuda):
     import torch
 
@@ -119,7 +164,7 @@ def test_q6k_gemv_awq_residual_and_random_blocks(cuda):
 
 def test_q6k_rejects_unaligned_rows_and_swiglu(cuda):
     raw, _ = _q6k(4, 2048, seed=1)
-    with pytest.raises(_rt().Qw35Error, match="k % 2048"):
+    with pytest.raises(_rt().Qw35Error, match="k % 512"):
         _rt().HipWeight.upload(np.zeros(4 * 5 * 210, np.uint8), om.TYPE_Q6_K, 4, 1280)
     w = _rt().HipWeight.upload(raw, om.TYPE_Q6_K, 4, 2048)
     import torch
