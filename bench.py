@@ -499,6 +499,30 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
                 out[f"prefill_q8_0{tag}_m{m}_{rows}x{k}"] = line(
                     ms, m, rows, k, "gf4_prefill_f16_kernel" + (" (F16 weights)" if tag else " (q8_0 weights)"))
         del q8, imgs
+    # Reference point, not this library: the vendor's dense fp16 GEMM (torch.mm,
+    # served by hipBLASLt) on the same shapes with fp16 weights in HBM (4 rotated
+    # copies), timed eagerly with events on the bench stream.
+    for rows, k in ((12288, 4096), (8192, 4096)):
+        wl = [b.normal((rows, k)).to(torch.float16) for _ in range(4)]
+        for m in (128, 2048):
+            a = b.normal((m, k)).to(torch.float16)
+            reps = max(24, 4800 // m)
+            with torch.cuda.stream(b.stream):
+                for w in wl:
+                    torch.mm(a, w.t())
+                torch.cuda.synchronize()
+                ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                ev0.record(b.stream)
+                for i in range(reps):
+                    torch.mm(a, wl[i % len(wl)].t())
+                ev1.record(b.stream)
+            torch.cuda.synchronize()
+            us = ev0.elapsed_time(ev1) * 1e3 / reps
+            out[f"library_fp16_gemm_m{m}_{rows}x{k}"] = {
+                "us": round(us, 2), "TFLOP/s": round(2.0 * m * rows * k / us / 1e6, 1),
+                "blas": str(torch.backends.cuda.preferred_blas_library()),
+                "note": "torch.mm fp16 (hipBLASLt), fp16 weights: a reference rate on this box, not this library"}
+        del wl
     return out
 
 
