@@ -617,6 +617,10 @@ def main() -> int:
     # the measured per-launch floor plus the bytes at the 1 GiB read rate.
     best_us = ceil["launch_floor_us"] + algo / (ceil["GB/s_1GiB"] * 1e3)
     extra["single_launch_frac_bound"] = round(algo / (best_us * 1e3) / HBM_PEAK_GBS, 4)
+    # The same kernel with its weights cache-resident: every launch reads one
+    # copy (25 MB, inside the 256 MB last-level cache), so HBM is not the limit.
+    ms_hot, _ = b.time_launches(gemv_calls(rt, [weights[0]] * len(weights), x, y), 960, 96)
+    extra["gf4_b1_same_weights_us"] = round(ms_hot * 1e3, 3)
     want = set() if args.headline_only or args.extras == "none" else (
         {"gf4", "q8", "q4k", "q6k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
 
