@@ -552,6 +552,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                 af[s][i] = *reinterpret_cast<const half8_t*>(buf + a_rd + i * 32 * kLdsRow + kk * 16);
         };
         fetch(0, 0);
+        // GF4 and F16 weights: sub-step 0's operands are issued before any
+        // MFMA, and each sub-step's scheduling region then holds its MFMAs and
+        // the next one's reads (GF4 12288x4096 M = 2048 211 -> 206 us; q8_0
+        // lost 2-3% this way, so its reads stay interleaved with sub-step 0)
+        if constexpr (!Q8W) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const int s = kk & 1;
@@ -572,6 +577,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                     if (kValuPerMfma > 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
                 }
             }
+            if constexpr (!Q8W) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
