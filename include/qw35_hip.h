@@ -31,9 +31,12 @@
  *             form for the k-quants (see qw35_hip_dequantize_f16); the GEMVs
  *             reject it
  * Shape limits of this build: k % 256 == 0 and 256 <= k <= 65536 (the
- * GEMVs take rows longer than 12288 in rounds of 32 chunks of 256 columns;
- * q8_0, whose blocks are 32 columns, needs k % 256 == 0 too, as every
- * Qwen3.5 projection has); Q6_K also needs k % 512 == 0 and rows * row bytes
+ * GEMVs take rows longer than 12288 in rounds of 32 chunks of 256 columns);
+ * q8_0, whose blocks are 32 columns, takes any k % 32 == 0 up to 65536 in the
+ * decode GEMVs (a row-wise kernel when k % 256 != 0, as the reference's
+ * n_blocks = ceil(k / 32), Qw35MetalRuntime+FFN.m:240), while its prefill
+ * matmul and greedy head need k % 256 == 0 (every Qwen3.5 projection has
+ * it); Q6_K also needs k % 512 == 0 and rows * row bytes
  * a multiple of 16 (its 210-byte super-blocks are read as the 16-byte
  * segments that cover them); rows >= 1; n_batch 1..8; a prefill call takes
  * n_tokens * k <= 2^30.

@@ -79,9 +79,12 @@ bool check_weight(const qw35_hip_weight* w, const char* what, char* err, uintptr
         set_err(err, err_len, "%s: weight data must be 16-byte aligned", what);
         return false;
     }
-    if (w->k == 0 || w->k % 256 != 0 || w->k > kMaxK) {
-        set_err(err, err_len, "%s: k=%llu must be a positive multiple of 256 and <= %llu", what,
-                (unsigned long long)w->k, (unsigned long long)kMaxK);
+    // q8_0 blocks are 32 columns (rows of k % 256 != 0 take the row-wise GEMV
+    // only); every other codec's super-block or word group spans 256
+    const uint64_t kstep = w->type_id == qw35::kTypeQ8_0 ? 32 : 256;
+    if (w->k == 0 || w->k % kstep != 0 || w->k > kMaxK) {
+        set_err(err, err_len, "%s: k=%llu must be a positive multiple of %llu and <= %llu", what,
+                (unsigned long long)w->k, (unsigned long long)kstep, (unsigned long long)kMaxK);
         return false;
     }
     if (w->rows == 0 || w->rows > 0x7fffffffull) {
@@ -104,6 +107,14 @@ bool check_weight(const qw35_hip_weight* w, const char* what, char* err, uintptr
         return false;
     }
     return true;
+}
+
+// The prefill matmul and the greedy head work in 256-column chunks.
+bool check_chunked_k(const qw35_hip_weight* w, const char* what, char* err, uintptr_t err_len) {
+    if (w->k % 256 == 0) return true;
+    set_err(err, err_len, "%s: needs k %% 256 == 0, got k=%llu (a q8_0 weight of such k runs the decode GEMV only)",
+            what, (unsigned long long)w->k);
+    return false;
 }
 
 bool check_hip(hipError_t e, const char* what, char* err, uintptr_t err_len) {
@@ -372,7 +383,9 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                 set_err(err, err_len, "%s: an ARGMAX op takes no w_up or residual", what);
                 return nullptr;
             }
-            if (!check_matvec(o.w, o.x, o.awq, o.dst, o.n_batch, what, err, err_len)) return nullptr;
+            if (!check_matvec(o.w, o.x, o.awq, o.dst, o.n_batch, what, err, err_len) ||
+                !check_chunked_k(o.w, what, err, err_len))
+                return nullptr;
             if (!o.token || ((uintptr_t)o.token & 3u)) {
                 set_err(err, err_len, "%s: an ARGMAX op needs a 4-byte aligned token output", what);
                 return nullptr;
@@ -530,8 +543,8 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight* w, void* dst, void* stream, c
 
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
     char msg[8];
-    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || n_tokens < 1 || n_tokens > 65536 ||
-        (uint64_t)n_tokens * w->k > kMaxPrefillElems)
+    if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || !check_chunked_k(w, "", msg, sizeof msg) ||
+        n_tokens < 1 || n_tokens > 65536 || (uint64_t)n_tokens * w->k > kMaxPrefillElems)
         return 0;
     if (w->type_id == qw35::kTypeF16)
         return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
@@ -544,7 +557,8 @@ uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32
 int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
                             uint32_t c_dtype, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes,
                             void* stream, char* err, uintptr_t err_len) {
-    if (!check_weight(w, "matmul_prefill", err, err_len)) return 0;
+    if (!check_weight(w, "matmul_prefill", err, err_len) || !check_chunked_k(w, "matmul_prefill", err, err_len))
+        return 0;
     if (w->type_id != qw35::kTypeGF4 && w->type_id != qw35::kTypeF16 && w->type_id != qw35::kTypeQ8_0) {
         set_err(err, err_len,
                 "matmul_prefill: GF4 (type 100), q8_0 (type 8) or F16 (type 1) weights, got %s; make the fp16 "
@@ -647,8 +661,8 @@ int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_
 
 uint64_t qw35_hip_output_argmax_workspace_size(const qw35_hip_weight* w, uint32_t n_batch) {
     char msg[8];
-    if (!check_weight(w, "output_argmax", msg, sizeof msg) || w->type_id == qw35::kTypeF16 || n_batch < 1 ||
-        n_batch > QW35_HIP_MAX_BATCH)
+    if (!check_weight(w, "output_argmax", msg, sizeof msg) || !check_chunked_k(w, "", msg, sizeof msg) ||
+        w->type_id == qw35::kTypeF16 || n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH)
         return 0;
     return 2 * argmax_ws_part(w, n_batch);
 }
@@ -656,7 +670,8 @@ uint64_t qw35_hip_output_argmax_workspace_size(const qw35_hip_weight* w, uint32_
 int qw35_hip_output_argmax(const qw35_hip_weight* w, const float* x, const float* awq, uint32_t n_batch,
                            uint32_t* token, float* logit, void* workspace, uint64_t workspace_bytes, void* stream,
                            char* err, uintptr_t err_len) {
-    if (!check_weight(w, "output_argmax", err, err_len) || !check_gemv_type(w, "output_argmax", err, err_len))
+    if (!check_weight(w, "output_argmax", err, err_len) || !check_gemv_type(w, "output_argmax", err, err_len) ||
+        !check_chunked_k(w, "output_argmax", err, err_len))
         return 0;
     if (!x || !token || !logit || !workspace) {
         set_err(err, err_len, "output_argmax: null input, output or workspace");
@@ -730,7 +745,8 @@ extern "C" {
 int qw35_hip_output_argmax_noalloc(const qw35_hip_weight* w, const float* x, const float* awq, uint32_t n_batch,
                                    uint32_t* token, float* logit, void* stream, char* err, uintptr_t err_len) {
     if (!check_weight(w, "output_argmax_noalloc", err, err_len) ||
-        !check_gemv_type(w, "output_argmax_noalloc", err, err_len))
+        !check_gemv_type(w, "output_argmax_noalloc", err, err_len) ||
+        !check_chunked_k(w, "output_argmax_noalloc", err, err_len))
         return 0;
     if (n_batch < 1 || n_batch > QW35_HIP_MAX_BATCH) {
         set_err(err, err_len, "output_argmax_noalloc: n_batch=%u must be in 1..%u", n_batch, QW35_HIP_MAX_BATCH);

@@ -8,6 +8,7 @@ hipError_t kq_q8_0_plain(const GemvArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream) {
+    if (a.k % 256 != 0) return launch_q8_0_gemv_rows(a, stream);  // rows of 32-column blocks only
     return a.w_up ? kq_q8_0_swiglu(a, stream) : kq_q8_0_plain(a, stream);
 }
 

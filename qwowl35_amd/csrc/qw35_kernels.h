@@ -71,6 +71,8 @@ struct GemvArgs {
 // Each launcher validates nothing (the C ABI does) and returns the launch status.
 hipError_t launch_gf4_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q8_0_gemv(const GemvArgs& a, hipStream_t stream);
+// q8_0 rows of k % 256 != 0 (k % 32 == 0): one wave per row, no greedy head.
+hipError_t launch_q8_0_gemv_rows(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q4_k_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_q5_k_gemv(const GemvArgs& a, hipStream_t stream);
 hipError_t launch_gf2_gemv(const GemvArgs& a, hipStream_t stream);

@@ -293,10 +293,18 @@ def gemv_kernel(w: HipWeight, n_batch: int = 1, w_up: HipWeight | None = None, a
             "workspace_bytes": ws.value}
 
 
+def _refuse_unchunked(w: HipWeight, what: str) -> None:
+    """The C ABI's error for a q8_0 weight of k % 256 != 0 on a path that works
+    in 256-column chunks (its workspace-size queries return 0 for it)."""
+    if w.type_id == TYPE_Q8_0 and w.k % 256:
+        raise Qw35Error(f"{what}: needs k % 256 == 0, got k={w.k} (a q8_0 weight of such k runs the decode GEMV only)")
+
+
 def output_argmax_workspace(w: HipWeight, n_batch: int, device="cuda") -> torch.Tensor:
     """Device bytes for ``output_argmax`` (size from the C ABI, +256 for alignment)."""
     need = int(_ffi.load().qw35_hip_output_argmax_workspace_size(C.byref(w.view), n_batch))
     if need == 0:
+        _refuse_unchunked(w, "output_argmax")
         raise Qw35Error("output_argmax: invalid weight or batch")
     return torch.empty(need + 256, dtype=torch.uint8, device=device)
 
@@ -311,6 +319,7 @@ def output_argmax(w: HipWeight, x: torch.Tensor, awq: torch.Tensor | None = None
     _check_awq(awq, w.k, x)
     need = int(_ffi.load().qw35_hip_output_argmax_workspace_size(C.byref(w.view), nb))
     if need == 0:
+        _refuse_unchunked(w, "output_argmax")
         raise Qw35Error("output_argmax: invalid weight or batch")
     if workspace is None:
         workspace = output_argmax_workspace(w, nb, device=x.device)
@@ -329,6 +338,7 @@ def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tenso
     """Device workspace for ``matmul_prefill`` of ``n_tokens`` tokens on ``w`` (256-byte aligned uint8)."""
     n = int(_ffi.load().qw35_hip_matmul_prefill_workspace_size(C.byref(w.view), n_tokens))
     if n == 0:
+        _refuse_unchunked(w, "matmul_prefill")
         raise Qw35Error(f"prefill workspace: unsupported weight or n_tokens={n_tokens}")
     return torch.empty(n, dtype=torch.uint8, device=device)  # the caching allocator aligns to 512 B
 
@@ -380,6 +390,16 @@ def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None,
         raise Qw35Error("matvec_batch takes [n_tokens, k] activations")
     if x.shape[0] <= _ffi.MAX_BATCH and w.type_id != TYPE_F16:
         return decode_matvec(w, x, dst, residual=False, stream=stream)
+    if w.type_id == TYPE_Q8_0 and w.k % 256 != 0:
+        # q8_0 rows of k % 256 != 0: the prefill matmul works in 256-column chunks,
+        # so such a chunk runs the row-wise decode GEMV MAX_BATCH tokens at a time
+        if dst is None:
+            dst = torch.empty((x.shape[0], w.rows), dtype=torch.float32, device=x.device)
+        _check_out(dst, x.shape[0], w.rows, x, "dst")
+        for t0 in range(0, x.shape[0], _ffi.MAX_BATCH):
+            t1 = min(t0 + _ffi.MAX_BATCH, x.shape[0])
+            decode_matvec(w, x[t0:t1], dst[t0:t1], residual=False, stream=stream)
+        return dst
     return matmul_prefill(w.prefill, x, out_dtype=torch.float32, dst=dst, stream=stream)
 
 

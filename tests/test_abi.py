@@ -334,3 +334,27 @@ def test_matmul_prefill_rejects_oversized_token_rows(lib):
     with pytest.raises(_ffi.Qw35Error, match=re.escape("n_tokens * k = 1073807360 must be <= 1073741824")):
         _ffi.call("qw35_hip_matmul_prefill", C.byref(w), C.c_void_p(4096), 1, None, C.c_void_p(4096), 0, 16385,
                   C.c_void_p(4096), C.c_uint64(1 << 40), None)
+
+
+def test_q8_0_rows_of_32_column_blocks(lib):
+    """q8_0 weights take any k % 32 == 0 (the row-wise GEMV); the chunked paths
+    (prefill matmul, greedy head) still need k % 256 == 0 and say so."""
+    w = _weight(type_id=8, k=4160, rows=16)
+    assert lib.qw35_hip_matmul_prefill_workspace_size(C.byref(w), 16) == 0
+    assert lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 1) == 0
+    with pytest.raises(_ffi.Qw35Error, match=re.escape("matmul_prefill: needs k % 256 == 0, got k=4160")):
+        _ffi.call("qw35_hip_matmul_prefill", C.byref(w), C.c_void_p(4096), 1, None, C.c_void_p(4096), 0, 16,
+                  C.c_void_p(4096), C.c_uint64(1 << 30), None)
+    with pytest.raises(_ffi.Qw35Error, match=re.escape("output_argmax: needs k % 256 == 0, got k=4160")):
+        _ffi.call("qw35_hip_output_argmax", C.byref(w), C.c_void_p(4096), None, 1, C.c_void_p(4096),
+                  C.c_void_p(4096), C.c_void_p(4096), C.c_uint64(1 << 20), None)
+    with pytest.raises(_ffi.Qw35Error, match=re.escape("k=4160 must be a positive multiple of 256")):
+        _call_matvec(_weight(type_id=100, k=4160))
+    with pytest.raises(_ffi.Qw35Error, match=re.escape("k=4100 must be a positive multiple of 32")):
+        _call_matvec(_weight(type_id=8, k=4100))
+    info = _ffi.LaunchInfo() if hasattr(_ffi, "LaunchInfo") else None
+    name = C.create_string_buffer(160)
+    g, b, l, ws = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_uint64()
+    _ffi.call("qw35_hip_gemv_kernel", C.byref(w), None, 3, 1, 0, name, C.sizeof(name), C.byref(g), C.byref(b),
+              C.byref(l), C.byref(ws))
+    assert name.value.decode() == "q8_gemv_rows<4, false, true>" and g.value == 4 and b.value == 256
