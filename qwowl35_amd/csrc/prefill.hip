@@ -551,6 +551,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             for (int i = 0; i < FM; ++i)
                 af[s][i] = *reinterpret_cast<const half8_t*>(buf + a_rd + i * 32 * kLdsRow + kk * 16);
         };
+        if constexpr (Q8W) {
+            // The span uses 9 of the 12 loaded dwords.  Keep all 12 live up to
+            // here: a dword left dead would be reallocated while its load is
+            // in flight, and that write-after-write makes the compiler wait
+            // for every outstanding load, the prefetches of the next two
+            // steps included (two full waits per four steps).
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int c = 0; c < WCH; ++c) asm volatile("" ::"v"(w[j][c]));
+        }
         fetch(0, 0);
         // GF4 and F16 weights: sub-step 0's operands are issued before any
         // MFMA, and each sub-step's scheduling region then holds its MFMAs and
