@@ -563,11 +563,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                 for (int c = 0; c < WCH; ++c) asm volatile("" ::"v"(w[j][c]));
         }
         fetch(0, 0);
-        // GF4 and F16 weights: sub-step 0's operands are issued before any
-        // MFMA, and each sub-step's scheduling region then holds its MFMAs and
-        // the next one's reads (GF4 12288x4096 M = 2048 211 -> 206 us; q8_0
-        // lost 2-3% this way, so its reads stay interleaved with sub-step 0)
-        if constexpr (!Q8W) __builtin_amdgcn_sched_barrier(0);
+        // Sub-step 0's operands are issued before any MFMA, and each
+        // sub-step's scheduling region then holds its MFMAs and the next one's
+        // reads (GF4 12288x4096 M = 2048 211 -> 206 us; q8_0 8192x4096
+        // M = 2048 174 -> 168 us)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const int s = kk & 1;
@@ -588,7 +588,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                     if (kValuPerMfma > 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
                 }
             }
-            if constexpr (!Q8W) __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
