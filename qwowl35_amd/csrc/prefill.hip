@@ -418,15 +418,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   the range is read) and realigns with v_perm.  B = fp16(d * q): the int8
 //   to exact fp16 of the decode GEMVs, then one v_pk_mul_f16 by (d, d) -- the
 //   same bits as the F16 prefill image, fp16_rne(d * q).
-template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false>
+template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false, int KH = 1>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
-    constexpr int NT = 64 * NW;
-    constexpr int BN = 32 * FN * NW;
+    constexpr int NWG = NW / KH;            // waves per K half
+    constexpr int NTG = 64 * NWG;           // threads per K half
+    constexpr int BN = 32 * FN * NWG;
     constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave; FN: 32-row weight tiles per wave
-    constexpr int A_CHUNKS = BM * 8 / NT;   // 16-byte token chunks per thread per step
+    constexpr int A_CHUNKS = BM * 8 / NTG;  // 16-byte token chunks per thread per step
     constexpr int BUF = BM * kLdsRow;
-    static_assert(BM % 32 == 0 && BM * 8 % NT == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
+    static_assert(BM % 32 == 0 && BM * 8 % NTG == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
+    static_assert((KH == 1 || KH == 2) && NW % KH == 0, "one or two K halves of equal wave counts");
+    static_assert(KH == 1 || NWG * FM * FN * 16 * 64 * 4 <= 2 * KH * BUF, "K-half partial sums fit the token buffers");
     typedef float float16_t __attribute__((ext_vector_type(16)));
     typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -446,9 +449,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const int split = t / tiles;
     t -= split * tiles;
     const int m0 = (t % p.tiles_m) * BM;
-    const int n0 = (t / p.tiles_m) * BN + wave * 32 * FN;
+    // KH = 2: waves [0, NWG) take the first half of the block's K range and
+    // waves [NWG, 2 NWG) the second, over the same rows, each half with its
+    // own token tile; the halves are summed in LDS at the end.
+    const int kh = KH > 1 ? wave / NWG : 0;
+    const int tg = tid - kh * NTG;
+    const int n0 = (t / p.tiles_m) * BN + (wave - kh * NWG) * 32 * FN;
     const int K = p.k;
-    const int k_begin = split * p.k_len;
+    const int k_len = p.k_len / KH;
+    const int k_begin = split * p.k_len + kh * k_len;
     const int words_per_row = K >> 3;
     const Gf4Consts gc = gf4_consts();
 
@@ -456,7 +465,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     int a_lds[A_CHUNKS];
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-        const int c = tid + i * NT;
+        const int c = tg + i * NTG;
         const int row = c >> 3;
         const int col = c & 7;
         const int gm = min(m0 + row, p.m - 1);
@@ -603,9 +612,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // load).  Each split covers a multiple of 4 * kBK columns (the host checks
     // k_len % 256 == 0); the prefetches past the last step re-read it instead
     // of branching.
-    const int KT = p.k_len / kBK;
-    uint8_t* buf0 = smem;
-    uint8_t* buf1 = smem + BUF;
+    const int KT = k_len / kBK;
+    uint8_t* buf0 = smem + kh * 2 * BUF;
+    uint8_t* buf1 = buf0 + BUF;
     Tokens t0, t1;
     Words w0, w1, w2, w3;
     load_tokens(0, t0);
@@ -629,6 +638,29 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         step(kt + 1, t1, w3, w1, buf1, t0, buf0, std::integral_constant<int, 1>{});
         step(kt + 2, t0, w0, w2, buf0, t1, buf1, std::integral_constant<int, 2>{});
         step(kt + 3, t1, w1, w3, buf1, t0, buf0, std::integral_constant<int, 3>{});
+    }
+
+    if constexpr (KH > 1) {
+        // The second half's partial sums pass through LDS (free after the last
+        // step's barrier) and the first half adds them: (first + second), the
+        // same order for every launch.
+        float* xch = reinterpret_cast<float*>(smem) + (size_t)(wave - kh * NWG) * FM * FN * 16 * 64 + lane;
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) xch[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += xch[((i * FN + j) * 16 + r) * 64];
     }
 
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
@@ -723,19 +755,21 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     }
 }
 
-template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false>
+template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, int KH = 1>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
-    constexpr int BN = 32 * FN * NW;
-    const size_t lds = 2 * (size_t)BM * kLdsRow;
+    constexpr int BN = 32 * FN * NW / KH;
+    const size_t lds = 2 * (size_t)KH * BM * kLdsRow;
+    if ((a.k_len / KH) % 256 != 0) return hipErrorInvalidValue;  // whole four-step loop bodies per half
     PrefillArgs p = a;
     p.tiles_m = (a.m + BM - 1) / BM;
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (out_f32)
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W>), grid, dim3(64 * NW), lds, s, p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W, KH>), grid, dim3(64 * NW), lds,
+                           s, p);
     else
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W, Q8W>), grid, dim3(64 * NW), lds, s,
-                           p);
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W, Q8W, KH>), grid, dim3(64 * NW), lds,
+                           s, p);
     return hipGetLastError();
 }
 
@@ -871,6 +905,20 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
     // (96 VGPRs at two tiles per wave), so a 256-row tile of 64 or more
     // tokens always runs on 8 waves of one tile each.
     if (q8w && best.bm >= 64 && best.bm <= 128) best.waves = 8;
+    // A 256-row tile on 8 one-tile waves with an even K split does the same
+    // work as a 128-row tile whose two K halves run on four waves each and are
+    // summed in LDS, with half the splits: half the fp32 partial sums, and no
+    // reduction launch where the split was two, for twice the token-tile
+    // reads.  Same-box A/B (us, without -> with): GF4 12288x4096 M = 128
+    // 35.0 -> 31.9, 4096x12288 M = 128 37.1 -> 35.5; q8_0 8192x4096 M = 128 /
+    // 512 57.3 -> 54.3 / 95.1 -> 83.4, 4096x4096 38.2 -> 35.1 / 60.1 -> 55.4.
+    // GF4 tiles of 128 tokens keep a split of more than two (4096x12288
+    // M = 512: 69.4 -> 74.0 with the halves).
+    if (!f16w && best.waves == 8 && best.fn == 2 && best.splits % 2 == 0 &&
+        (q8w || best.bm <= 64 || best.splits == 2)) {
+        best.kh = 2;
+        best.splits /= 2;
+    }
     return best;
 }
 
@@ -892,6 +940,21 @@ size_t gf4_prefill_workspace_bytes(int m, int rows, int k) {
     return gf4_prefill_workspace_bytes(m, rows, k, plan_gf4_prefill(m, rows, k));
 }
 
+namespace {
+
+// A workspace sized for another token count may not hold this call's partial
+// sums: split less (ultimately not at all) rather than fail; K halves need
+// each half to stay a multiple of 256 columns.
+void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t workspace_bytes) {
+    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
+        do --cfg.splits;
+        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % (256 * cfg.kh) != 0));
+    }
+    if ((k / cfg.splits) % (256 * cfg.kh) != 0) cfg.kh = 1;
+}
+
+}  // namespace
+
 // wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks (1 and 2 take column-order tokens and a workspace).
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
@@ -910,7 +973,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     bool af = a_f32 != 0, aw = awq != nullptr;
     const bool of = out_f32 != 0;
     if (workspace) {
-        if (cfg.splits < 1 || k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0) return hipErrorInvalidValue;
+        if (cfg.splits < 1 || (cfg.kh != 1 && cfg.kh != 2) || k % cfg.splits != 0 ||
+            (k / cfg.splits) % (256 * cfg.kh) != 0)
+            return hipErrorInvalidValue;
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
         float* rs = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2));
@@ -945,8 +1010,14 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         if (q8w) {
             switch (cfg.bm * 10 + cfg.fn) {
                 case 2562: e = launch_f16_tile<256, 4, 2, 1, false, true>(p, kf32, stream); break;
-                case 1282: e = launch_f16_tile<128, 8, 1, 2, false, true>(p, kf32, stream); break;
-                case 642: e = launch_f16_tile<64, 8, 1, 2, false, true>(p, kf32, stream); break;
+                case 1282:
+                    e = cfg.kh == 2 ? launch_f16_tile<128, 8, 1, 2, false, true, 2>(p, kf32, stream)
+                                    : launch_f16_tile<128, 8, 1, 2, false, true>(p, kf32, stream);
+                    break;
+                case 642:
+                    e = cfg.kh == 2 ? launch_f16_tile<64, 8, 1, 2, false, true, 2>(p, kf32, stream)
+                                    : launch_f16_tile<64, 8, 1, 2, false, true>(p, kf32, stream);
+                    break;
                 case 322: e = launch_f16_tile<32, 4, 2, 2, false, true>(p, kf32, stream); break;
                 default: return hipErrorInvalidValue;
             }
@@ -960,13 +1031,15 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
             }
         } else switch (cfg.bm * 10 + cfg.fn) {
             case 1282:
-                e = cfg.waves == 8 ? launch_f16_tile<128, 8, 1, 2>(p, kf32, stream)
-                                   : launch_f16_tile<128, 4, 2, 2>(p, kf32, stream);
+                e = cfg.kh == 2      ? launch_f16_tile<128, 8, 1, 2, false, false, 2>(p, kf32, stream)
+                    : cfg.waves == 8 ? launch_f16_tile<128, 8, 1, 2>(p, kf32, stream)
+                                     : launch_f16_tile<128, 4, 2, 2>(p, kf32, stream);
                 break;
             case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
             case 642:
-                e = cfg.waves == 8 ? launch_f16_tile<64, 8, 1, 2>(p, kf32, stream)
-                                   : launch_f16_tile<64, 4, 2, 2>(p, kf32, stream);
+                e = cfg.kh == 2      ? launch_f16_tile<64, 8, 1, 2, false, false, 2>(p, kf32, stream)
+                    : cfg.waves == 8 ? launch_f16_tile<64, 8, 1, 2>(p, kf32, stream)
+                                     : launch_f16_tile<64, 4, 2, 2>(p, kf32, stream);
                 break;
             case 644: e = launch_f16_tile<64, 4, 4, 2>(p, kf32, stream); break;
             case 322: e = launch_f16_tile<32, 4, 2, 2>(p, kf32, stream); break;
@@ -999,10 +1072,7 @@ hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, in
                                int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (!workspace) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_prefill(m, rows, k, true);
-    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
-        do --cfg.splits;
-        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
-    }
+    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes);
     return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 1);
 }
 
@@ -1010,10 +1080,7 @@ hipError_t launch_q8_prefill(const void* w, int rows, int k, const void* a, int 
                              int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (!workspace) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_q8_prefill(m, rows, k);
-    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
-        do --cfg.splits;
-        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
-    }
+    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes);
     return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 2);
 }
 
@@ -1025,12 +1092,7 @@ hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, h
 hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     PrefillCfg cfg = plan_gf4_prefill(m, rows, k);
-    // A workspace sized for another token count may not hold this call's
-    // partial sums: split less (ultimately not at all) rather than fail.
-    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
-        do --cfg.splits;
-        while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % 256 != 0));
-    }
+    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes);
     return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 0);
 }
 

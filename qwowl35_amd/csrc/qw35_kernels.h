@@ -123,6 +123,9 @@ struct PrefillCfg {
     // 8: the same bm x 256 tile on 8 waves of one 32-row weight tile each
     // (GF4, fn 2 only), two waves per SIMD where a CU gets only one block.
     int waves = 4;
+    // 2 (8-wave tiles only): the 8 waves form two K halves of four waves over
+    // a 128-row tile, summed in LDS; splits then counts blocks per K range.
+    int kh = 1;
 };
 PrefillCfg plan_gf4_prefill(int m, int rows, int k);
 size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg);
