@@ -914,7 +914,7 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
     // 512 57.3 -> 54.3 / 95.1 -> 83.4, 4096x4096 38.2 -> 35.1 / 60.1 -> 55.4.
     // GF4 tiles of 128 tokens keep a split of more than two (4096x12288
     // M = 512: 69.4 -> 74.0 with the halves).
-    if (!f16w && best.waves == 8 && best.fn == 2 && best.splits % 2 == 0 &&
+    if (!f16w && best.waves == 8 && best.fn == 2 && best.bm <= 128 && best.splits % 2 == 0 &&
         (q8w || best.bm <= 64 || best.splits == 2)) {
         best.kh = 2;
         best.splits /= 2;
@@ -975,6 +975,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     if (workspace) {
         if (cfg.splits < 1 || (cfg.kh != 1 && cfg.kh != 2) || k % cfg.splits != 0 ||
             (k / cfg.splits) % (256 * cfg.kh) != 0)
+            return hipErrorInvalidValue;
+        // K halves exist for the 8-wave 64- and 128-token tiles of GF4 and q8_0 weights only
+        if (cfg.kh == 2 && (f16w || cfg.waves != 8 || cfg.fn != 2 || (cfg.bm != 64 && cfg.bm != 128)))
             return hipErrorInvalidValue;
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);

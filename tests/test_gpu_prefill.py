@@ -182,6 +182,36 @@ def test_prefill_config4_shapes(cuda, m, n, k):
         assert ok, msg
 
 
+@pytest.mark.parametrize("n,k", [(12288, 4096), (4096, 12288)])
+def test_prefill_workspace_without_room_for_a_split(cuda, n, k):
+    """A workspace of only the staging bytes (room for no K split) runs the
+    planned tiles unsplit, the two in-block K halves included; the result
+    matches the planned call within fp32 rounding and the oracle on sampled
+    rows."""
+    import torch
+
+    rt = _rt()
+    m = 128
+    g = torch.Generator(device=cuda)
+    g.manual_seed(n + 3)
+    w32 = (torch.randn((n, k), generator=g, device=cuda) * 0.02).to(torch.bfloat16).float()
+    hw = rt.quantize_weight(w32, om.TYPE_GF4)
+    del w32
+    a = torch.randn((m, k), generator=g, device=cuda).to(torch.bfloat16)
+    staged_only = (m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256
+    small = torch.empty(staged_only, dtype=torch.uint8, device=cuda)
+    out = rt.matmul_prefill(hw, a, out_dtype=torch.float32, workspace=small).cpu().numpy().astype(np.float64)
+    planned = rt.matmul_prefill(hw, a, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+    assert om.rel_l2(out, planned) <= 1e-6
+    rows = np.sort(np.random.default_rng(n).choice(m, size=32, replace=False))
+    words = hw.storage.cpu().numpy().view("<u4").reshape(n, k // 8)
+    wdq = ogf4.gf4_dequant(words).astype(np.float64)
+    a_eff = om.prefill_operand(a.view(torch.int16).cpu().numpy().view(np.uint16)[rows], None).astype(np.float64)
+    want = a_eff @ wdq.T
+    assert om.rel_l2(out[rows], want) <= F32_REL_L2
+    assert np.all(np.abs(out[rows] - want) <= (np.abs(a_eff) @ np.abs(wdq).T) * 2.0 ** -16 + 1e-30)
+
+
 def test_matvec_batch_long_chunk_uses_prefill(cuda):
     """encodeMatvecBatch semantics: > 8 fp32 tokens on a GF4 weight -> fp32 [tokens, rows]."""
     rng = np.random.default_rng(2)

@@ -103,8 +103,8 @@ def test_q8_prefill_fp32_input_and_extreme_scales(cuda):
     assert np.all(np.abs(out - want) <= (np.abs(a_eff) @ np.abs(img).T) * 2.0 ** -16 + 1e-30)
 
 
-@pytest.mark.parametrize("rows,k,m", [(8192, 4096, 2048), (4096, 4096, 128), (12352, 4096, 512), (4096, 12288, 512),
-                                      (4096, 4096, 1200)])
+@pytest.mark.parametrize("rows,k,m", [(8192, 4096, 2048), (8192, 4096, 512), (8192, 4096, 128), (4096, 4096, 128),
+                                      (12352, 4096, 512), (4096, 12288, 512), (4096, 4096, 1200)])
 def test_q8_prefill_full_shapes(cuda, rows, k, m):
     """The 9B's q8_0 projections at full size: against the F16-image path on
     the GPU and against the oracle on 48 sampled weight rows."""
