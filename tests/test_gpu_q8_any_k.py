@@ -59,6 +59,23 @@ def test_q8_0_any_k_gemv(cuda, k, nb):
     assert om.rel_l2(dst.cpu().numpy(), want) <= GEMV_REL_L2
 
 
+@pytest.mark.parametrize("nb", [1, 8])
+def test_q8_0_any_k_longest_row(cuda, nb):
+    """k = 65504 (2047 blocks, the longest such row under the ABI's 65536):
+    each lane walks 32 blocks, the last lanes 31."""
+    rt = _rt()
+    rows, k = 9, 65504
+    print(f"q8_0 rows {rows}x{k} nb={nb}", flush=True)
+    rng = np.random.default_rng(nb)
+    raw, deq = make_weight(T, rows, k, seed=5)
+    w = rt.HipWeight.upload(raw, T, rows, k)
+    assert rt.gemv_kernel(w, nb)["name"].startswith("q8_gemv_rows<")
+    x = activations(rng, nb, k)
+    a = awq_scales(rng, k)
+    y = rt.decode_matvec(w, _t(x, cuda), awq=_t(a, cuda)).cpu().numpy()
+    assert om.rel_l2(y, om.matvec_f64(deq, x, a)) <= GEMV_REL_L2
+
+
 @pytest.mark.parametrize("k", [96, 4160])
 @pytest.mark.parametrize("nb", [1, 8])
 def test_q8_0_any_k_swiglu(cuda, k, nb):
