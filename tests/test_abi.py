@@ -357,4 +357,7 @@ def test_q8_0_rows_of_32_column_blocks(lib):
     g, b, l, ws = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_uint64()
     _ffi.call("qw35_hip_gemv_kernel", C.byref(w), None, 3, 1, 0, name, C.sizeof(name), C.byref(g), C.byref(b),
               C.byref(l), C.byref(ws))
-    assert name.value.decode() == "q8_gemv_rows<4, false, true>" and g.value == 4 and b.value == 256
+    # 16 rows at batch 3 (the 4-row instantiation): one workgroup of 8 waves, two rows each,
+    # activations of 4 batch rows x 64 blocks x 36 floats in LDS
+    assert name.value.decode() == "q8_gemv_rows<4, false, true>"
+    assert (g.value, b.value, l.value, ws.value) == (1, 512, 4 * 64 * 36 * 4, 0)
