@@ -337,11 +337,18 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                     if constexpr (FMT == kFmtQ6K) {
                         // Rows of k % 2048 != 0 start 4, 8 or 12 bytes past a 16-byte
                         // boundary (the low bits of loff): the 16-byte segment holding
-                        // the chunk's first byte may then be the next one.
+                        // the chunk's first byte may then be the next one.  Cached like
+                        // Q4_K's below: 210-byte chunks share lines across waves.
                         const uint32_t q15 = (uint32_t)(chunk * 210) & 15u;
-                        wv[sl][t * NM + m][i] = load_stream16(wbase + ((loff[t][i] + q15) & ~15u));
+                        wv[sl][t * NM + m][i] = load_cached16(wbase + ((loff[t][i] + q15) & ~15u));
                     } else {
-                        wv[sl][t * NM + m][i] = load_stream16(wbase + loff[t][i]);
+                        // Q4_K's 144-byte chunks share a 128-byte line with the next
+                        // chunk (another wave's): cached loads keep it for that reader
+                        // (LM head 248320x4096 b1 136-149 -> 122-127 us, 1.40x the
+                        // weight bytes fetched before); whole-line GF4 chunks and q8_0
+                        // measured no better or slower cached, so they stream
+                        wv[sl][t * NM + m][i] = FMT == kFmtQ4K ? load_cached16(wbase + loff[t][i])
+                                                               : load_stream16(wbase + loff[t][i]);
                     }
                 }
         }

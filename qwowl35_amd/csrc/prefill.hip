@@ -253,7 +253,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         }
         const uint32_t* bs = b_src + (k0 >> 3);
         if constexpr (WPT == 4) {
-            const uint4_t v = load_stream16(bs);
+            const uint4_t v = load_cached16(bs);
             r.b[0] = v.x; r.b[1] = v.y; r.b[2] = v.z; r.b[3] = v.w;
         } else if constexpr (WPT == 2) {
             typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int c = 0; c < WCH; ++c)
-                w[j][c] = load_stream16(w_src[j] + (Q8W  ? (k0 / 64) * 68 - 4 * ((k0 / 64) & 3) + 16 * c
+                w[j][c] = load_cached16(w_src[j] + (Q8W  ? (k0 / 64) * 68 - 4 * ((k0 / 64) & 3) + 16 * c
                                                     : F16W ? k0 * 2 + 16 * c
                                                            : k0 / 2));
     };

@@ -142,6 +142,15 @@ __device__ __forceinline__ uint4_t load_stream16(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint4_t*>(p));
 }
 
+// Cached 16-byte load of weights whose 128-byte lines are read again soon by
+// other waves: prefill weight tiles (every token tile of the launch reads
+// them) and k-quant chunks that do not end on a line boundary (the next
+// chunk's wave reads the rest of the line).  A streaming load lets L2 drop
+// such a line before its second reader arrives.
+__device__ __forceinline__ uint4_t load_cached16(const void* p) {
+    return *reinterpret_cast<const uint4_t*>(p);
+}
+
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
 // Power-of-two factor 2^e that brings max_abs into [2^13, 2^14), so that every
