@@ -403,8 +403,7 @@ const void *qw35_hip_runtime_store(void *runtime);
  * through an F16 weight (the prefill image of qw35_hip_dequantize_f16), for
  * the GF2 / Q4_K / Q5_K / Q6_K projections
  * (qw35_mul_mm_{gf2,q4_k,q5_k,q6_k}_f32, qw35_tiled_mm.metal:208-254); a
- * q8_0 weight's image gives the same products (faster, at 2 bytes per weight
- * of HBM).
+ * q8_0 weight's image gives the same products, at 2 bytes per weight of HBM.
  * 1 <= n_tokens <= 65536, rows <= 2^24. */
 #define QW35_HIP_DTYPE_F32 0u
 #define QW35_HIP_DTYPE_BF16 1u
