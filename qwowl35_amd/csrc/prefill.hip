@@ -905,6 +905,12 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
     // (96 VGPRs at two tiles per wave), so a 256-row tile of 64 or more
     // tokens always runs on 8 waves of one tile each.
     if (q8w && best.bm >= 64 && best.bm <= 128) best.waves = 8;
+    // 256-token tiles (F16 and q8_0 weights): 8 one-tile waves, two per SIMD
+    // (128 accumulator registers each) in place of 4 two-tile waves.  Sweep
+    // after the cached weight loads (us, 4 -> 8 waves): F16 12352x4096 M =
+    // 1024 / 2048 147.7 -> 131.9 / 275.4 -> 243.2, 8192x4096 M = 2048 149.6 ->
+    // 140.1; q8_0 12352x4096 M = 2048 275.9 -> 261.6, 8192x4096 156.4 -> 148.8.
+    if ((f16w || q8w) && best.bm == 256) best.waves = 8;
     // A 256-row tile on 8 one-tile waves with an even K split does the same
     // work as a 128-row tile whose two K halves run on four waves each and are
     // summed in LDS, with half the splits: half the fp32 partial sums, and no
@@ -1012,7 +1018,10 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const bool kf32 = of || split;
         if (q8w) {
             switch (cfg.bm * 10 + cfg.fn) {
-                case 2562: e = launch_f16_tile<256, 4, 2, 1, false, true>(p, kf32, stream); break;
+                case 2562:
+                    e = cfg.waves == 8 ? launch_f16_tile<256, 8, 1, 2, false, true>(p, kf32, stream)
+                                       : launch_f16_tile<256, 4, 2, 1, false, true>(p, kf32, stream);
+                    break;
                 case 1282:
                     e = cfg.kh == 2 ? launch_f16_tile<128, 8, 1, 2, false, true, 2>(p, kf32, stream)
                                     : launch_f16_tile<128, 8, 1, 2, false, true>(p, kf32, stream);
@@ -1026,7 +1035,10 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
             }
         } else if (f16w) {
             switch (cfg.bm * 10 + cfg.fn) {
-                case 2562: e = launch_f16_tile<256, 4, 2, 1, true>(p, kf32, stream); break;
+                case 2562:
+                    e = cfg.waves == 8 ? launch_f16_tile<256, 8, 1, 2, true>(p, kf32, stream)
+                                       : launch_f16_tile<256, 4, 2, 1, true>(p, kf32, stream);
+                    break;
                 case 1282: e = launch_f16_tile<128, 4, 2, 1, true>(p, kf32, stream); break;
                 case 642: e = launch_f16_tile<64, 4, 2, 2, true>(p, kf32, stream); break;
                 case 322: e = launch_f16_tile<32, 4, 2, 2, true>(p, kf32, stream); break;
