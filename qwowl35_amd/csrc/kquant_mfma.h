@@ -852,8 +852,9 @@ struct KqPlan {
 // q8_0 4096 x 4096 b1 {1, 16, 1, 1} 6.2 us ({1, 8, 2, 2} 7.2 us); Q4_K
 // 248320 x 4096 b8 {2, 4, 4, 2} 264 us ({4, 8, 2, 1} 275 us).  Batch-1 heads,
 // one sweep on one box: Q4_K {3, 8, 2, 2} 134-136 us ({2, 16, 1, 1} 142 us),
-// Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us), GF2 {3, 8, 2, 2} 113 us
-// ({2, 16, 1, 1} 119 us); Q5_K keeps {2, 16, 1, 1} 157 us ({3, 8, 2, 2} 160 us).
+// Q6_K {1, 8, 2, 2} 175 us ({2, 16, 1, 1} 183 us; now two tiles, below), GF2
+// {3, 8, 2, 2} 113 us ({2, 16, 1, 1} 119 us); Q5_K keeps {2, 16, 1, 1} 157 us
+// ({3, 8, 2, 2} 160 us).
 inline KqPlan plan_kq(int fmt, int rows, int k, int nb, bool split_ok = false) {
     const int chunks = k >> 8;
     const int tiles = (rows + 15) / 16;
@@ -874,7 +875,10 @@ inline KqPlan plan_kq(int fmt, int rows, int k, int nb, bool split_ok = false) {
                 if (fmt != kFmtQ8 && fmt != kFmtGF4) {
                     // LM-head sized: at batch 8 four tiles per 4-wave workgroup
                     // (head b8 Q4_K 199 us, Q6_K 278, Q5_K 249, GF2 176; with
-                    // {2, 4, 4, 2} 234 / 322 / 261 / 210 us)
+                    // {2, 4, 4, 2} 234 / 322 / 261 / 210 us); Q4_K eight tiles
+                    // (one sweep on one box: 170.3 us against 173.5 with four,
+                    // 175.9 with six; Q6_K 258.7 with eight, 240.3 with four)
+                    if (tiles >= 4096 && nb >= 8 && fmt == kFmtQ4K) return {8, 4, 4, 1};
                     if (tiles >= 4096) return nb >= 8 ? KqPlan{4, 4, 4, 1} : KqPlan{2, 4, 4, 2};
                     return {4, 8, 2, 1};
                 }
@@ -886,6 +890,9 @@ inline KqPlan plan_kq(int fmt, int rows, int k, int nb, bool split_ok = false) {
         if (tiles >= 4096) {  // LM-head sized
             if (fmt == kFmtQ4K || fmt == kFmtGF2) return {3, 8, 2, 2};
             if (fmt == kFmtQ5K) return {2, 16, 1, 1};
+            // Q6_K: two tiles (one sweep on one box: 170.9 us, against 176.7
+            // with one, 176.9 with {3, 4, 4, 2}, 183.6 with {4, 8, 2, 1})
+            if (fmt == kFmtQ6K) return {2, 8, 2, 2};
         }
         if (fmt == kFmtQ8 && tiles < 512) return {1, 16, 1, 1};
         return {1, 8, 2, 2};
@@ -1019,6 +1026,12 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
     }
     if constexpr (NB == 8 && (FMT == kFmtQ4K || FMT == kFmtQ6K || FMT == kFmtQ5K || FMT == kFmtGF2)) {
         QW35_KQ_PLAN(4, 4, 4, 1)
+    }
+    if constexpr (NB == 8 && FMT == kFmtQ4K) {
+        QW35_KQ_PLAN(8, 4, 4, 1)
+    }
+    if constexpr (NB <= 2 && FMT == kFmtQ6K) {
+        QW35_KQ_PLAN(2, 8, 2, 2)
     }
     if constexpr (NB == 8 && FMT == kFmtGF4) {
         QW35_KQ_PLAN(1, 12, 4, 2)

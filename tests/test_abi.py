@@ -301,6 +301,30 @@ def test_swiglu_rejects_q6k(lib):
                   None)
 
 
+@pytest.mark.parametrize("type_id", [8, 12, 13, 14, 101])
+@pytest.mark.parametrize("rows", [65549, 248320])
+def test_argmax_partials_match_the_launched_grid(lib, type_id, rows):
+    """The greedy head sizes its partials from the launch planner (one (token,
+    logit) pair per workgroup and batch row, tokens and logits each rounded up to
+    256 bytes), and its GEMV launch refuses any other grid. So every shape the
+    planner picks for a head must be compiled at every batch: a plan without an
+    instantiation falls back to one row tile per workgroup, a different grid. The
+    decode GEMV of these types launches the same kernel and plan, so its grid
+    (queried without a GPU) must match the partial count at batch 1..8."""
+    from qwowl35_amd import runtime as rt
+
+    k = 4096
+    w = _weight(type_id=type_id, k=k, rows=rows, nbytes=rows * rt.row_bytes(type_id, k))
+    name = C.create_string_buffer(160)
+    g, b, l, ws = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_uint64()
+    for nb in range(1, 9):
+        part = lib.qw35_hip_output_argmax_workspace_size(C.byref(w), nb) // 2
+        _ffi.call("qw35_hip_gemv_kernel", C.byref(w), None, nb, 0, 0, name, C.sizeof(name), C.byref(g), C.byref(b),
+                  C.byref(l), C.byref(ws))
+        assert name.value.startswith(b"kq_mfma_gemv<"), name.value
+        assert part == (g.value * nb * 4 + 255) // 256 * 256, (nb, name.value, g.value, part)
+
+
 def test_output_argmax_workspace_and_validation(lib):
     w = _weight(type_id=14, k=4096, rows=248320)
     n1 = lib.qw35_hip_output_argmax_workspace_size(C.byref(w), 1)
