@@ -428,8 +428,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     constexpr int A_CHUNKS = BM * 8 / NTG;  // 16-byte token chunks per thread per step
     constexpr int BUF = BM * kLdsRow;
     static_assert(BM % 32 == 0 && BM * 8 % NTG == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
-    static_assert((KH == 1 || KH == 2) && NW % KH == 0, "one or two K halves of equal wave counts");
-    static_assert(KH == 1 || NWG * FM * FN * 16 * 64 * 4 <= 2 * KH * BUF, "K-half partial sums fit the token buffers");
+    static_assert((KH == 1 || KH == 2 || KH == 4) && NW % KH == 0, "one, two or four K parts of equal wave counts");
+    static_assert(KH == 1 || (KH / 2) * NWG * FM * FN * 16 * 64 * 4 <= 2 * KH * BUF,
+                  "K-part partial sums fit the token buffers");
     typedef float float16_t __attribute__((ext_vector_type(16)));
     typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -449,9 +450,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const int split = t / tiles;
     t -= split * tiles;
     const int m0 = (t % p.tiles_m) * BM;
-    // KH = 2: waves [0, NWG) take the first half of the block's K range and
-    // waves [NWG, 2 NWG) the second, over the same rows, each half with its
-    // own token tile; the halves are summed in LDS at the end.
+    // KH = 2 (4): waves [kh NWG, (kh + 1) NWG) take part kh of the block's K
+    // range, two halves (four quarters), over the same rows, each part with its
+    // own token tile; the parts are summed in LDS at the end.
     const int kh = KH > 1 ? wave / NWG : 0;
     const int tg = tid - kh * NTG;
     const int n0 = (t / p.tiles_m) * BN + (wave - kh * NWG) * 32 * FN;
@@ -641,26 +642,42 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     }
 
     if constexpr (KH > 1) {
-        // The second half's partial sums pass through LDS (free after the last
-        // step's barrier) and the first half adds them: (first + second), the
-        // same order for every launch.
+        // Partial sums pass through LDS (free after the last step's barrier):
+        // halves as (first + second); quarters as (q0 + q1) + (q2 + q3), the
+        // odd quarters handing over to the even ones, then q2 to q0.  The same
+        // order for every launch.
+        constexpr int kPart = NWG * FM * FN * 16 * 64;  // floats of one part's sums
         float* xch = reinterpret_cast<float*>(smem) + (size_t)(wave - kh * NWG) * FM * FN * 16 * 64 + lane;
-        if (kh == 1) {
+        auto put = [&](float* x) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) xch[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+                    for (int r = 0; r < 16; ++r) x[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+        };
+        auto add = [&](const float* x) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += x[((i * FN + j) * 16 + r) * 64];
+        };
+        if constexpr (KH == 4) {
+            if (kh & 1) put(xch + (kh >> 1) * kPart);
+            __syncthreads();
+            if (!(kh & 1)) add(xch + (kh >> 1) * kPart);
+            __syncthreads();
+            if (kh == 2) put(xch);
+            __syncthreads();
+            if (kh != 0) return;
+        } else {
+            if (kh == 1) put(xch);
+            __syncthreads();
+            if (kh == 1) return;
         }
-        __syncthreads();
-        if (kh == 1) return;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] += xch[((i * FN + j) * 16 + r) * 64];
+        add(xch);
     }
 
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
@@ -925,6 +942,26 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
         best.kh = 2;
         best.splits /= 2;
     }
+    // K quarters for GF4 at 33..128 tokens and k <= 4096: each 64-token block
+    // runs four parts of its K range (16 steps each at k = 4096, summed in
+    // LDS) instead of two of 32, with no K split and so no reduction launch,
+    // on 8 waves over 64 rows or 16 over 128, whichever fills half the CUs to
+    // all of them in one round.
+    // Same-box A/B at M = 128 (us, plan -> quarters): 8192x4096 28.3 -> 22.0
+    // (8 waves), 4096x4096 21.5 -> 19.9 (8), 12288x4096 29.5 -> 28.0 (16
+    // waves); 4096x12288 (48-step quarters) was not faster, 30.5 -> 30.5-36.4.
+    if (!f16w && !q8w && m > 32 && m <= 128 && k <= 4096 && k % 1024 == 0) {
+        const long tm = (m + 63) / 64;
+        const long b64 = tm * ((rows + 63) / 64), b128 = tm * ((rows + 127) / 128);
+        const int waves = 2 * b64 >= cus && b64 <= cus ? 8 : 2 * b128 >= cus && b128 <= cus ? 16 : 0;
+        if (waves) {
+            best.bm = 64;
+            best.fn = 2;
+            best.splits = 1;
+            best.waves = waves;
+            best.kh = 4;
+        }
+    }
     return best;
 }
 
@@ -979,11 +1016,14 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     bool af = a_f32 != 0, aw = awq != nullptr;
     const bool of = out_f32 != 0;
     if (workspace) {
-        if (cfg.splits < 1 || (cfg.kh != 1 && cfg.kh != 2) || k % cfg.splits != 0 ||
+        if (cfg.splits < 1 || (cfg.kh != 1 && cfg.kh != 2 && cfg.kh != 4) || k % cfg.splits != 0 ||
             (k / cfg.splits) % (256 * cfg.kh) != 0)
             return hipErrorInvalidValue;
         // K halves exist for the 8-wave 64- and 128-token tiles of GF4 and q8_0 weights only
         if (cfg.kh == 2 && (f16w || cfg.waves != 8 || cfg.fn != 2 || (cfg.bm != 64 && cfg.bm != 128)))
+            return hipErrorInvalidValue;
+        // K quarters: the 64-token GF4 tile on 16 waves (128 rows) or 8 (64 rows)
+        if (cfg.kh == 4 && (f16w || q8w || (cfg.waves != 16 && cfg.waves != 8) || cfg.fn != 2 || cfg.bm != 64))
             return hipErrorInvalidValue;
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
@@ -1052,7 +1092,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
                 break;
             case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
             case 642:
-                e = cfg.kh == 2      ? launch_f16_tile<64, 8, 1, 2, false, false, 2>(p, kf32, stream)
+                e = cfg.kh == 4      ? (cfg.waves == 16 ? launch_f16_tile<64, 16, 1, 4, false, false, 4>(p, kf32, stream)
+                                                        : launch_f16_tile<64, 8, 1, 4, false, false, 4>(p, kf32, stream))
+                    : cfg.kh == 2    ? launch_f16_tile<64, 8, 1, 2, false, false, 2>(p, kf32, stream)
                     : cfg.waves == 8 ? launch_f16_tile<64, 8, 1, 2>(p, kf32, stream)
                                      : launch_f16_tile<64, 4, 2, 2>(p, kf32, stream);
                 break;

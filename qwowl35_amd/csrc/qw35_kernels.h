@@ -122,9 +122,12 @@ struct PrefillCfg {
     int splits;  // K splits; k / splits must be a multiple of 256
     // 8: the same bm x 256 tile on 8 waves of one 32-row weight tile each
     // (GF4, fn 2 only), two waves per SIMD where a CU gets only one block.
+    // 16: only with kh 4 (below).
     int waves = 4;
     // 2 (8-wave tiles only): the 8 waves form two K halves of four waves over
     // a 128-row tile, summed in LDS; splits then counts blocks per K range.
+    // 4 (GF4, bm 64, fn 2): four K quarters, of two waves over a 64-row tile
+    // (waves 8) or of four over a 128-row tile (waves 16).
     int kh = 1;
 };
 PrefillCfg plan_gf4_prefill(int m, int rows, int k);

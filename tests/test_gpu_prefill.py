@@ -182,6 +182,41 @@ def test_prefill_config4_shapes(cuda, m, n, k):
         assert ok, msg
 
 
+@pytest.mark.parametrize("m,n,k", [(128, 8192, 4096), (100, 4096, 4096), (128, 6000, 4096), (64, 12288, 4096),
+                                   (128, 12288, 4096), (128, 8192, 1024)])
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_prefill_k_quarters(cuda, m, n, k, out_f32):
+    """Shapes the planner gives four in-block K parts (64-token tiles, k <= 4096,
+    one block per CU or fewer): 8 waves over 64 rows, or 16 over 128 rows
+    (12288 rows at M = 128); ragged tokens (100) and rows (6000); quarters of
+    256 columns (k = 1024).  GPU-packed GF4 weights, AWQ; 32 sampled token rows
+    against the oracle, to the same bars as every prefill output."""
+    import torch
+
+    rt = _rt()
+    g = torch.Generator(device=cuda)
+    g.manual_seed(m + n + k)
+    w32 = (torch.randn((n, k), generator=g, device=cuda) * 0.02).to(torch.bfloat16).float()
+    hw = rt.quantize_weight(w32, om.TYPE_GF4)
+    del w32
+    a = torch.randn((m, k), generator=g, device=cuda).to(torch.bfloat16)
+    awq = torch.rand((k,), generator=g, device=cuda) * 1.5 + 0.5
+    out = rt.matmul_prefill(hw, a, awq=awq, out_dtype=torch.float32 if out_f32 else torch.bfloat16)
+    rows = np.sort(np.random.default_rng(n + m).choice(m, size=32, replace=False))
+    words = hw.storage.cpu().numpy().view("<u4").reshape(n, k // 8)
+    wdq = ogf4.gf4_dequant(words)
+    a_eff = om.prefill_operand(a.view(torch.int16).cpu().numpy().view(np.uint16)[rows], awq.cpu().numpy())
+    want = a_eff.astype(np.float64) @ wdq.astype(np.float64).T
+    if out_f32:
+        got = out.cpu().numpy()[rows].astype(np.float64)
+        assert om.rel_l2(got, want) <= F32_REL_L2
+        assert np.all(np.abs(got - want) <= (np.abs(a_eff) @ np.abs(wdq).T) * 2.0 ** -16 + 1e-30)
+    else:
+        got_bits = out.view(torch.int16).cpu().numpy().view(np.uint16)[rows]
+        ok, msg = _bf16_out_ok(got_bits, want, a_eff, wdq)
+        assert ok, msg
+
+
 @pytest.mark.parametrize("n,k", [(12288, 4096), (4096, 12288)])
 def test_prefill_workspace_without_room_for_a_split(cuda, n, k):
     """A workspace of only the staging bytes (room for no K split) runs the
