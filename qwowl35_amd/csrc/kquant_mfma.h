@@ -348,13 +348,17 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                         const uint32_t q15 = (uint32_t)(chunk * 210) & 15u;
                         wv[sl][t * NM + m][i] = load_cached16(wbase + ((loff[t][i] + q15) & ~15u));
                     } else {
-                        // Q4_K's 144-byte chunks share a 128-byte line with the next
-                        // chunk (another wave's): cached loads keep it for that reader
-                        // (LM head 248320x4096 b1 136-149 -> 122-127 us, 1.40x the
-                        // weight bytes fetched before); whole-line GF4 chunks and q8_0
-                        // measured no better or slower cached, so they stream
-                        wv[sl][t * NM + m][i] = FMT == kFmtQ4K ? load_cached16(wbase + loff[t][i])
-                                                               : load_stream16(wbase + loff[t][i]);
+                        // Q4_K's 144-byte chunks (Q5_K's 176, GF2's) share a 128-byte
+                        // line with the next chunk (another wave's): cached loads keep
+                        // it for that reader (LM head 248320x4096 b1: Q4_K 136-149 ->
+                        // 122-127 us, 1.40x the weight bytes fetched before; Q5_K
+                        // 161 -> 152, GF2 116 -> 108, b8 216 -> 207 and 154 -> 143).
+                        // Whole-line GF4 chunks stream; so does q8_0, which measured
+                        // 3-6% faster cached on 4096x4096 but 2-6% slower on
+                        // 4096x12288 and the same on 12352x4096.
+                        constexpr bool kCached = FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtGF2;
+                        wv[sl][t * NM + m][i] = kCached ? load_cached16(wbase + loff[t][i])
+                                                        : load_stream16(wbase + loff[t][i]);
                     }
                 }
         }
