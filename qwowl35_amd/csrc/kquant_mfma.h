@@ -892,7 +892,10 @@ inline KqPlan plan_kq(int fmt, int rows, int k, int nb, bool split_ok = false) {
             return fmt == kFmtQ8 ? KqPlan{1, 8, 2, 1} : KqPlan{1, 8, 2, 2};
         }
         if (tiles >= 4096) {  // LM-head sized
-            if (fmt == kFmtQ4K || fmt == kFmtGF2) return {3, 8, 2, 2};
+            if (fmt == kFmtQ4K) return {3, 8, 2, 2};
+            // GF2 (cached loads): four tiles per 4-wave workgroup, one sweep on
+            // one box: 99.3-100.0 us against 106-113 with {3, 8, 2, 2}
+            if (fmt == kFmtGF2) return {4, 4, 4, 1};
             if (fmt == kFmtQ5K) return {2, 16, 1, 1};
             // Q6_K: two tiles (one sweep on one box: 170.9 us, against 176.7
             // with one, 176.9 with {3, 4, 4, 2}, 183.6 with {4, 8, 2, 1})
@@ -1036,6 +1039,9 @@ hipError_t kq_launch_nb(const GemvArgs& a, hipStream_t stream) {
     }
     if constexpr (NB <= 2 && FMT == kFmtQ6K) {
         QW35_KQ_PLAN(2, 8, 2, 2)
+    }
+    if constexpr (NB <= 2 && FMT == kFmtGF2) {
+        QW35_KQ_PLAN(4, 4, 4, 1)
     }
     if constexpr (NB == 8 && FMT == kFmtGF4) {
         QW35_KQ_PLAN(1, 12, 4, 2)
