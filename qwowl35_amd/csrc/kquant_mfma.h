@@ -353,10 +353,12 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                         // it for that reader (LM head 248320x4096 b1: Q4_K 136-149 ->
                         // 122-127 us, 1.40x the weight bytes fetched before; Q5_K
                         // 161 -> 152, GF2 116 -> 108, b8 216 -> 207 and 154 -> 143).
-                        // Whole-line GF4 chunks stream; so does q8_0, which measured
-                        // 3-6% faster cached on 4096x4096 but 2-6% slower on
-                        // 4096x12288 and the same on 12352x4096.
-                        constexpr bool kCached = FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtGF2;
+                        // Whole-line GF4 chunks stream.  q8_0 loads cached only in the
+                        // one-tile shapes with one chunk in flight (4096x4096 b1 / b8
+                        // 6.47 / 9.13 -> 6.28 / 8.62 us); its other shapes measured
+                        // the same (12352x4096) or 2-6% slower (4096x12288) cached.
+                        constexpr bool kCached = FMT == kFmtQ4K || FMT == kFmtQ5K || FMT == kFmtGF2 ||
+                                                 (FMT == kFmtQ8 && RT == 1 && P == 1);
                         wv[sl][t * NM + m][i] = kCached ? load_cached16(wbase + loff[t][i])
                                                         : load_stream16(wbase + loff[t][i]);
                     }
