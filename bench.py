@@ -120,7 +120,13 @@ class Bench:
 
     def time_launches(self, calls, launches: int, warmup: int):
         """Time exactly ``launches`` launches, rotating over ``calls`` (one launch
-        each), replayed from graphs; returns (ms per launch, launches)."""
+        each), replayed from graphs; returns (ms per launch, launches).
+
+        Both graphs (the full rotation and the remainder) are replayed before
+        the timed window, and the window's start event is queued behind
+        warm-up replays still running on the GPU: the window then holds the
+        kernels back to back, not the latency of a first or an idle-GPU graph
+        launch (which a short window, e.g. 20 launches, would otherwise carry)."""
         torch = self.torch
         n = len(calls)
         launches = max(1, int(launches))
@@ -131,13 +137,15 @@ class Bench:
         full = self._graph(calls)
         reps, rem = divmod(launches, n)
         part = self._graph(calls[:rem]) if rem else None
-        with torch.cuda.stream(self.stream):
-            for _ in range(max(1, -(-warmup // n))):
-                full.replay()
-        torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(self.stream):  # replays and events on the same stream
+            if part is not None:
+                part.replay()
+            full.replay()
+            torch.cuda.synchronize()
+            for _ in range(max(2, -(-warmup // n))):  # keeps the GPU busy while the window is queued
+                full.replay()
             ev0.record(self.stream)
             for _ in range(reps):
                 full.replay()
@@ -452,12 +460,16 @@ def bench_codecs(b: Bench, steps: int, warmup: int) -> dict:
 
 def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
     """Config 4: GF4 prefill dequant-matmul, W 12288x4096 and 4096x12288 (12
-    rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out; the staged
-    path (workspace, fp16 MFMA; the time includes the staging pass) and the
-    direct path (bf16 MFMA).  Then the q8_0 projections (6 rotated copies),
-    dequantised inside the staged kernel and, for comparison, through their
-    fp16 prefill image.  Utilisation is against the nominal 2.5 PFLOP/s and
-    against the MFMA probe's sustained rate on this box."""
+    rotated copies), A bf16 N(0,1) [M][k], AWQ U(0.5,2), bf16 out, on the
+    staged path (workspace, fp16 MFMA; the time includes the staging pass).
+    Each shape also at M = 128 with fp32 activations and fp32 out (the
+    runtime's multi-token chunks: an fp16 hi/lo pair per activation, twice the
+    MFMA work).  Then the q8_0 projections (6 rotated copies), dequantised
+    inside the staged kernel and, for comparison, through their fp16 prefill
+    image.  Utilisation is against the nominal 2.5 PFLOP/s and against the
+    MFMA probe's sustained rate on this box.  Every line of this library's
+    kernels carries the CPU baseline of the same shape and M (numpy
+    dequantisation + fp32 BLAS)."""
     rt, torch = b.rt, b.torch
     ceiling = mfma_ceiling(b)
     out = {"mfma_probe_TFLOP/s": round(ceiling, 1)}
@@ -468,24 +480,28 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
         r["frac_of_probe"] = round(flops / (ms * 1e-3) / 1e12 / ceiling, 4)
         return r
 
+    def with_cpu(r, type_id, w, rows, k, m, what):
+        if cpu is not None:
+            t_dq, t_mm = cpu.matmul(type_id, host_bytes(w), rows, k, m)
+            r["cpu_baseline"] = cpu.record(
+                round(2.0 * m * rows * k / (t_dq + t_mm) / 1e12, 4), "TFLOP/s",
+                f"{what} {rows}x{k}, M={m}: dequant {t_dq * 1e3:.1f} ms + fp32 W@A^T {t_mm * 1e3:.1f} ms")
+        return r
+
     for rows, k in ((12288, 4096), (4096, 12288)):
         ws = [b.weight(rt.TYPE_GF4, rows, k) for _ in range(12)]
         awq = torch.rand((k,), generator=b.gen, device=b.dev) * 1.5 + 0.5
-        for m in (128, 512, 2048):
-            a = b.normal((m, k)).to(torch.bfloat16)
-            c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
+        for m, a_dt, c_dt, tag in ((128, torch.bfloat16, torch.bfloat16, ""), (512, torch.bfloat16, torch.bfloat16, ""),
+                                   (2048, torch.bfloat16, torch.bfloat16, ""), (128, torch.float32, torch.float32, "_f32")):
+            a = b.normal((m, k)).to(a_dt)
+            c = torch.empty((m, rows), dtype=c_dt, device=b.dev)
             wsp = rt.prefill_workspace(ws[0], m, device=b.dev)
-            for path, work, kern in (("", wsp, "gf4_prefill_f16_kernel"), ("_direct", None, "gf4_prefill_kernel")):
-                calls = [lambda s, w=w, work=work: rt.matmul_prefill(w, a, awq=awq, dst=c, workspace=work, stream=s)
-                         for w in ws]
-                ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
-                r = line(ms, m, rows, k, kern)
-                if cpu is not None and path == "" and rows == 12288:
-                    t_dq, t_mm = cpu.matmul(rt.TYPE_GF4, host_bytes(ws[0]), rows, k, m)
-                    r["cpu_baseline"] = cpu.record(
-                        round(2.0 * m * rows * k / (t_dq + t_mm) / 1e12, 4), "TFLOP/s",
-                        f"GF4 {rows}x{k}, M={m}: dequant {t_dq * 1e3:.1f} ms + fp32 W@A^T {t_mm * 1e3:.1f} ms")
-                out[f"prefill_gf4_m{m}_{rows}x{k}{path}"] = r
+            calls = [lambda s, w=w: rt.matmul_prefill(w, a, awq=awq, out_dtype=c_dt, dst=c, workspace=wsp, stream=s)
+                     for w in ws]
+            ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
+            kern = "gf4_prefill_f16_kernel" + (" (fp32 activations, hi/lo)" if tag else "")
+            out[f"prefill_gf4{tag}_m{m}_{rows}x{k}"] = with_cpu(line(ms, m, rows, k, kern), rt.TYPE_GF4, ws[0],
+                                                                rows, k, m, "GF4")
         del ws
     for rows, k in ((8192, 4096), (4096, 4096)):
         q8 = [b.weight(rt.TYPE_Q8_0, rows, k) for _ in range(6)]
@@ -502,8 +518,10 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
                 wsp = rt.prefill_workspace(wl[0], m, device=b.dev)
                 calls = [lambda s, w=w, wsp=wsp: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in wl]
                 ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
-                out[f"prefill_q8_0{tag}_m{m}_{rows}x{k}"] = line(
-                    ms, m, rows, k, "gf4_prefill_f16_kernel" + (" (F16 weights)" if tag else " (q8_0 weights)"))
+                r = line(ms, m, rows, k, "gf4_prefill_f16_kernel" + (" (F16 weights)" if tag else " (q8_0 weights)"))
+                if not tag:
+                    r = with_cpu(r, rt.TYPE_Q8_0, q8[0], rows, k, m, "q8_0")
+                out[f"prefill_q8_0{tag}_m{m}_{rows}x{k}"] = r
         del q8, imgs
     # Reference point, not this library: the vendor's dense fp16 GEMM (torch.mm,
     # served by hipBLASLt) on the same shapes with fp16 weights in HBM (4 rotated

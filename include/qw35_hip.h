@@ -392,11 +392,10 @@ void *qw35_hip_runtime_stream(void *runtime);
 const void *qw35_hip_runtime_store(void *runtime);
 
 /* Multi-token (prefill) matmul of a GF4, q8_0 or F16 weight on MFMA:
- *   c[t][r] = sum_k bf16_rne(awq[k] * a[t][k]) * W[r][k]    (awq == NULL: a[t][k] as bf16)
- * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32
- * (fp32 input is rounded to bf16 after the AWQ multiply); c: device
- * [n_tokens][rows], c_dtype QW35_HIP_DTYPE_BF16 (round-to-nearest-even) or
- * QW35_HIP_DTYPE_F32; fp32 accumulation.  Replaces encodeMatvecBatch /
+ *   c[t][r] = sum_k W[r][k] * v[t][k],  v = awq[k] * a[t][k]   (awq == NULL: v = a)
+ * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32;
+ * c: device [n_tokens][rows], c_dtype QW35_HIP_DTYPE_BF16 (round-to-nearest-
+ * even) or QW35_HIP_DTYPE_F32; fp32 accumulation.  Replaces encodeMatvecBatch /
  * encodeTiledKMatmul for type 100 (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366,
  * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255), for q8_0
  * dequantised in the kernel to fp16(d * q) (qw35_mul_mm_q8_0_f32), and,
@@ -404,27 +403,36 @@ const void *qw35_hip_runtime_store(void *runtime);
  * the GF2 / Q4_K / Q5_K / Q6_K projections
  * (qw35_mul_mm_{gf2,q4_k,q5_k,q6_k}_f32, qw35_tiled_mm.metal:208-254); a
  * q8_0 weight's image gives the same products, at 2 bytes per weight of HBM.
- * 1 <= n_tokens <= 65536, rows <= 2^24. */
+ * 1 <= n_tokens <= 65536, rows <= 2^24; n_tokens * k <= 2^30 for bf16
+ * activations, 2^29 for fp32. */
 #define QW35_HIP_DTYPE_F32 0u
 #define QW35_HIP_DTYPE_BF16 1u
 /* workspace: NULL, or device memory of
  * qw35_hip_matmul_prefill_workspace_size(w, n_tokens) bytes (256-byte
- * aligned, owned by the caller, not shared by concurrent calls).  With a
- * workspace the activations are first staged as fp16 with a per-token
- * power-of-two scale (exact for every value above 2^-28 of the token's
- * largest) and contracted on fp16 MFMA; shapes with too few output tiles for
- * the device also split K, with fp32 partial sums in the workspace reduced in
- * a fixed order.  Without a workspace the loader converts the activations and
- * contracts on bf16 MFMA.  Both compute the products of bf16_rne(awq * a) and
- * the weights exactly for every activation of at least 2^-28 of its token
- * row's largest magnitude (the fp16 staging holds every such bf16 value
- * exactly); smaller activations are rounded by the staging, at most 2^-39 of
- * the row's largest.  The size depends
- * on the weight's shape and n_tokens (0: invalid weight or n_tokens); a
- * smaller workspace that still holds the staged activations (2 bytes per
- * activation plus 4 per token, each part rounded up to 256 bytes) is
- * accepted and splits K less.  F16 and q8_0 weights always take the staged
- * path (the workspace is required). */
+ * aligned, owned by the caller, not shared by concurrent calls).
+ * With a workspace (the staged path) v is computed in fp32 and staged as
+ * fp16 with a per-token power of two 2^e that puts the token's max |v| in
+ * [2^14, 2^15), and contracted on fp16 MFMA:
+ *   - bf16 activations: fp16_rne(2^e v).  Without AWQ every activation of at
+ *     least 2^-28 of its token's largest is carried exactly (smaller ones
+ *     round at 2^-39 of the largest); with AWQ the product is rounded once,
+ *     to fp16;
+ *   - fp32 activations: an fp16 hi/lo pair, hi = fp16_rne(2^e v) and
+ *     lo = fp16_rne((2^e v - hi) * 2^11), contracted as hi + 2^-11 lo: about
+ *     22 significant bits of every activation, the fp32 activations of the
+ *     reference's tiled matmul (qw35_tiled_mm.metal:200-224), at twice the
+ *     MFMA work of bf16 input.
+ * Shapes with too few output tiles for the device also split K, with fp32
+ * partial sums in the workspace reduced in a fixed order.  Without a
+ * workspace (GF4 only) the loader converts the activations to bf16 and
+ * contracts on bf16 MFMA; that path takes bf16 activations without AWQ only
+ * (the operands it represents exactly).  The size depends on the weight's
+ * shape and n_tokens and covers both activation types (0: invalid weight or
+ * n_tokens); a smaller workspace that still holds the staged activations (2
+ * bytes per staged activation, 4 per token, each part rounded up to 256
+ * bytes; fp32 activations stage two rows per token in groups of 32 tokens:
+ * 64 * ceil(n_tokens / 32) rows) is accepted and splits K less.  F16 and q8_0
+ * weights always take the staged path (the workspace is required). */
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight *w, uint32_t n_tokens);
 int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
                             uint32_t c_dtype, uint32_t n_tokens, void *workspace, uint64_t workspace_bytes,

@@ -10,10 +10,16 @@ oracle-dequantised weights with the activations the kernel was given:
   ``silu(gate . x) * (up . x)`` with ``silu(v) = v / (1 + exp(-v))``
   (``qw35_types.metal:40-42``);
 * prefill dequant-matmul (``qw35_tiled_mm.metal:36-198``; output layout
-  ``dst[token * rows + row]`` at ``:157-165``): the kernel consumes
-  ``A' = bf16_rne(a * A)`` (fp32 product, one rounding) and returns
-  ``bf16_rne(sum_k A'[m, k] * W[n, k])``; the oracle accumulates the same bf16
-  operands in fp64.
+  ``dst[token * rows + row]`` at ``:157-165``): ``C[m, n] = sum_k W[n, k] *
+  (a[k] * A[m, k])`` in fp64 on the unrounded activations, which the
+  reference's tiled matmul keeps in fp32 (src1 staged as float,
+  ``qw35_tiled_mm.metal:200-224``).  ``prefill_f64`` is that reference.  Two
+  more functions restate the activation rounding of this library's two
+  prefill paths (not the reference's arithmetic), so that tests can bound the
+  kernel's own accumulation error tightly: ``prefill_staged_operand`` (fp16
+  staging with a per-token power of two; an fp16 hi/lo pair for fp32 input)
+  and ``prefill_direct_operand`` (bf16 operands of the path without a
+  workspace).
 """
 from __future__ import annotations
 
@@ -135,18 +141,66 @@ def bf16_round(v: np.ndarray) -> np.ndarray:
     return bf16_bits_to_f32(f32_to_bf16_bits(v))
 
 
-def prefill_operand(a_bits: np.ndarray, awq: np.ndarray | None) -> np.ndarray:
-    """The activation tile the prefill kernel contracts: ``bf16_rne(fp32(A) * a)`` as fp32."""
-    a32 = bf16_bits_to_f32(a_bits)
-    if awq is None:
-        return a32
-    return bf16_round(a32 * np.asarray(awq, dtype=np.float32)[None, :])
+def prefill_input(a: np.ndarray, awq: np.ndarray | None = None) -> np.ndarray:
+    """fp64 ``awq * A`` of prefill activations ``a``: bf16 bit patterns (uint16)
+    or fp32 values, taken exactly."""
+    a = np.asarray(a)
+    a64 = (bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)).astype(np.float64)
+    if awq is not None:
+        a64 = a64 * np.asarray(awq, dtype=np.float32).astype(np.float64)[None, :]
+    return a64
 
 
-def prefill_f64(w: np.ndarray, a_bits: np.ndarray, awq: np.ndarray | None = None) -> np.ndarray:
-    """fp64 C[M, rows] = A' @ W^T on the exact bf16 operands the kernel consumes."""
-    a_eff = prefill_operand(a_bits, awq).astype(np.float64)
-    return a_eff @ np.asarray(w, dtype=np.float64).T
+def prefill_f64(w: np.ndarray, a: np.ndarray, awq: np.ndarray | None = None) -> np.ndarray:
+    """fp64 ``C[M, rows] = (awq * A) @ W^T`` on the unrounded activations (bf16
+    bits or fp32 values), the reference product the prefill paths are measured against."""
+    return prefill_input(a, awq) @ np.asarray(w, dtype=np.float64).T
+
+
+def _f16(v: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 round-to-nearest-even (numpy's cast), back to fp32."""
+    return np.asarray(v, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def _pow2_scale(max_abs: np.ndarray) -> np.ndarray:
+    """2^e with max_abs * 2^e in [2^14, 2^15), e clamped to [-124, 126]; 1 for a
+    zero or non-finite maximum (the staging's power-of-two factor)."""
+    out = np.ones(max_abs.shape, dtype=np.float64)
+    ok = (max_abs > 0) & np.isfinite(max_abs)
+    _, e = np.frexp(max_abs[ok].astype(np.float64))  # max in [2^(e-1), 2^e)
+    out[ok] = np.exp2(np.clip(15 - e, -124, 126).astype(np.float64))
+    return out
+
+
+def prefill_staged_operand(a: np.ndarray, awq: np.ndarray | None, a_f32: bool) -> np.ndarray:
+    """The activations the staged prefill path (a workspace given) contracts, in
+    fp64: v = fp32(awq * A), one power of two 2^e per token row putting max |v|
+    in [2^14, 2^15), hi = fp16_rne(2^e v); fp32 input adds lo =
+    fp16_rne((2^e v - hi) 2^11) and contracts hi + 2^-11 lo.  The operand is
+    that sum times 2^-e.  This library's own staging, restated so a test can
+    separate the staging's rounding from the kernel's accumulation."""
+    a = np.asarray(a)
+    v = bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+    if awq is not None:
+        v = (v * np.asarray(awq, dtype=np.float32)[None, :]).astype(np.float32)
+    sc = _pow2_scale(np.max(np.abs(v), axis=1))[:, None]
+    s = (v.astype(np.float64) * sc).astype(np.float32)  # exact: a power of two
+    hi = _f16(s).astype(np.float64)
+    op = hi
+    if a_f32:
+        lo = _f16(((s.astype(np.float64) - hi) * 2048.0).astype(np.float32)).astype(np.float64)
+        op = hi + lo / 2048.0
+    return op / sc
+
+
+def prefill_direct_operand(a: np.ndarray, awq: np.ndarray | None) -> np.ndarray:
+    """The activations the prefill path without a workspace contracts on bf16
+    MFMA: bf16_rne(fp32(awq * A)), in fp64 (this library's direct path)."""
+    a = np.asarray(a)
+    v = bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+    if awq is not None:
+        v = (v * np.asarray(awq, dtype=np.float32)[None, :]).astype(np.float32)
+    return bf16_round(v).astype(np.float64)
 
 
 def argmax_rule(logits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:

@@ -541,17 +541,23 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight* w, void* dst, void* stream, c
                : 0;
 }
 
+namespace {
+// Weight form of the prefill kernel: 0 GF4 words, 1 F16, 2 q8_0 blocks; -1 none.
+int prefill_wkind(uint32_t type_id) {
+    return type_id == qw35::kTypeGF4 ? 0 : type_id == qw35::kTypeF16 ? 1 : type_id == qw35::kTypeQ8_0 ? 2 : -1;
+}
+}  // namespace
+
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
     char msg[8];
     if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || !check_chunked_k(w, "", msg, sizeof msg) ||
         n_tokens < 1 || n_tokens > 65536 || (uint64_t)n_tokens * w->k > kMaxPrefillElems)
         return 0;
-    if (w->type_id == qw35::kTypeF16)
-        return (uint64_t)qw35::f16w_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
-    if (w->type_id == qw35::kTypeQ8_0)
-        return (uint64_t)qw35::q8_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
-    if (w->type_id != qw35::kTypeGF4) return 0;
-    return (uint64_t)qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k);
+    const int wkind = prefill_wkind(w->type_id);
+    if (wkind < 0) return 0;
+    // fp32 activations (two staged rows per token) are accepted up to half the elements
+    return (uint64_t)qw35::prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, wkind,
+                                                   (uint64_t)n_tokens * w->k <= kMaxPrefillElems / 2);
 }
 
 int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
@@ -574,9 +580,12 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         set_err(err, err_len, "matmul_prefill: n_tokens=%u must be in 1..65536", n_tokens);
         return 0;
     }
-    if ((uint64_t)n_tokens * w->k > kMaxPrefillElems) {  // staged token offsets are 32-bit byte offsets
-        set_err(err, err_len, "matmul_prefill: n_tokens * k = %llu must be <= %llu",
-                (unsigned long long)n_tokens * w->k, (unsigned long long)kMaxPrefillElems);
+    // staged token offsets are 32-bit byte offsets; fp32 input stages two rows per token
+    const uint64_t max_elems = a_dtype == QW35_HIP_DTYPE_F32 ? kMaxPrefillElems / 2 : kMaxPrefillElems;
+    if ((uint64_t)n_tokens * w->k > max_elems) {
+        set_err(err, err_len, "matmul_prefill: n_tokens * k = %llu must be <= %llu for %s activations",
+                (unsigned long long)n_tokens * w->k, (unsigned long long)max_elems,
+                a_dtype == QW35_HIP_DTYPE_F32 ? "fp32" : "bf16");
         return 0;
     }
     if (w->rows > (1ull << 24)) {  // keeps every launch grid within 2^31 blocks
@@ -591,36 +600,28 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
         set_err(err, err_len, "matmul_prefill: a/awq must be 16-byte aligned and c 4-byte aligned");
         return 0;
     }
-    if (w->type_id == qw35::kTypeF16 || w->type_id == qw35::kTypeQ8_0) {
-        const bool q8 = w->type_id == qw35::kTypeQ8_0;
-        const uint64_t need =
-            qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, qw35::PrefillCfg{32, 2, 1});
+    const int wkind = prefill_wkind(w->type_id);
+    const bool a_f32 = a_dtype == QW35_HIP_DTYPE_F32;
+    if (!workspace && wkind == 0 && (a_f32 || awq)) {
+        set_err(err, err_len,
+                "matmul_prefill: fp32 activations and AWQ need a workspace (the staged path); the path without one "
+                "contracts bf16 operands and takes bf16 activations without AWQ only");
+        return 0;
+    }
+    if (workspace || wkind != 0) {
+        const uint64_t need = qw35::prefill_min_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, a_f32);
         if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
-            set_err(err, err_len, "matmul_prefill: %s weights need a 256-byte aligned workspace of >= %llu bytes",
-                    q8 ? "q8_0" : "f16", (unsigned long long)need);
-            return 0;
-        }
-        const hipError_t e =
-            q8 ? qw35::launch_q8_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32, awq, c,
-                                         (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace_bytes,
-                                         static_cast<hipStream_t>(stream))
-               : qw35::launch_f16w_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32, awq, c,
-                                           (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace_bytes,
-                                           static_cast<hipStream_t>(stream));
-        return check_hip(e, "matmul_prefill", err, err_len) ? 1 : 0;
-    }
-    if (workspace) {
-        const uint64_t need =
-            qw35::gf4_prefill_workspace_bytes((int)n_tokens, (int)w->rows, (int)w->k, qw35::PrefillCfg{32, 2, 1});
-        if (workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
-            set_err(err, err_len, "matmul_prefill: workspace must be 256-byte aligned and >= %llu bytes, got %llu",
-                    (unsigned long long)need, (unsigned long long)workspace_bytes);
+            set_err(err, err_len,
+                    "matmul_prefill: %s a 256-byte aligned workspace of >= %llu bytes for %u %s tokens, got %llu",
+                    wkind == 0 ? "the staged path needs" : wkind == 1 ? "f16 weights need" : "q8_0 weights need",
+                    (unsigned long long)need, n_tokens, a_f32 ? "fp32" : "bf16",
+                    (unsigned long long)(workspace ? workspace_bytes : 0));
             return 0;
         }
     }
-    return check_hip(qw35::launch_gf4_prefill(w->data, (int)w->rows, (int)w->k, a, a_dtype == QW35_HIP_DTYPE_F32,
-                                              awq, c, (int)n_tokens, c_dtype == QW35_HIP_DTYPE_F32, workspace,
-                                              workspace ? workspace_bytes : 0, static_cast<hipStream_t>(stream)),
+    return check_hip(qw35::launch_prefill(wkind, w->data, (int)w->rows, (int)w->k, a, a_f32, awq, c, (int)n_tokens,
+                                          c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace ? workspace_bytes : 0,
+                                          static_cast<hipStream_t>(stream)),
                      "matmul_prefill", err, err_len)
                ? 1
                : 0;

@@ -51,8 +51,10 @@ struct PrefillArgs {
     const void* a;           // [M][K] bf16 or fp32 (staged path: fp16, see below)
     const float* awq;        // [K] or nullptr
     void* c;                 // [M][N] bf16 or fp32
-    const float* row_scale;  // staged path: per token row, the inverse of its fp16 scale
-    int m, n, k;
+    const float* row_scale;  // staged path: per token, the inverse of its fp16 scale
+    int m, n, k;             // m: rows of a (staged path: staged rows)
+    int m_out;               // rows of c (tokens)
+    int hilo;                // staged fp32 input: MFMA tiles 2i, 2i + 1 are one token tile's hi, lo rows
     int tiles_m, tiles_n;
     int splits;              // staged path: K split this many ways (1: none)
     int k_len;               // columns per split
@@ -74,28 +76,52 @@ __device__ __forceinline__ uint4_t gf4_word_to_bf16x8(uint32_t w) {
     return uint4_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
 }
 
-// Staged activations (the path taken when the caller provides a workspace):
-// one workgroup per token row writes A'' = fp16(2^e * bf16_rne(awq * A)) with
-// 2^e the power of two that puts the row's max |A'| in [2^14, 2^15), and
-// row_scale = 2^-e.  Every bf16 value of at least 2^-28 of the row maximum is
-// exact in fp16 (smaller ones round at 2^-39 of the maximum), so the matmul
-// can contract on fp16 MFMA with the GF4 weights decoded by the 15-op fp16
-// decode of gf4_decode.h.  Each group of 8 columns is stored in the decode's
-// column order 0,4,1,5,2,6,3,7 (GF4_ORDER), or in column order for the F16
-// weight kernel.
+// Staged activations (the path taken when the caller provides a workspace).
+// v = awq * A in fp32 (A read exactly from bf16 or fp32; awq == nullptr:
+// v = A), and 2^e the power of two that puts the token row's max |v| in
+// [2^14, 2^15); row_scale = 2^-e.
+// * bf16 input: one staged fp16 row per token, fp16_rne(2^e v).  Without AWQ
+//   every bf16 value of at least 2^-28 of the row maximum is exact (smaller
+//   ones round at 2^-39 of the maximum); with AWQ the product is rounded once,
+//   to fp16 (11 significant bits).
+// * fp32 input (HILO): two staged fp16 rows per token, hi = fp16_rne(2^e v)
+//   and lo = fp16_rne((2^e v - hi) 2^11) (the difference is exact in fp32), so
+//   hi + 2^-11 lo carries about 22 significant bits of v: the activations
+//   keep fp32 precision, as the reference's tiled matmul keeps src1 in fp32
+//   (qw35-server/src/metal/qw35_tiled_mm.metal:200-224).  Token t's rows are
+//   64 (t / 32) + t % 32 (hi) and that + 32 (lo): in a block of staged rows
+//   the 32-row MFMA tiles 2i and 2i + 1 hold the same 32 tokens' hi and lo
+//   halves, and the matmul adds their accumulators (hi + 2^-11 lo) before the
+//   row scale.  The grid covers tokens 0 .. 32 ceil(M / 32) - 1; the padding
+//   tokens' rows are written as zeros.
+// The fp16 values feed fp16 MFMA with the weights decoded by the 15-op fp16
+// GF4 decode of gf4_decode.h (or fp16 q8_0 / F16 weights).  Each group of 8
+// columns is stored in the decode's column order 0,4,1,5,2,6,3,7 (GF4_ORDER),
+// or in column order for the F16 and q8_0 weight kernels.
 constexpr int kStageThreads = 256;
 
 template <bool A_F32, bool HAS_AWQ, bool GF4_ORDER = true>
 __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void* __restrict__ a,
-                                                                      const float* __restrict__ awq, int k,
+                                                                      const float* __restrict__ awq, int m, int k,
                                                                       uint16_t* __restrict__ a16,
                                                                       float* __restrict__ row_scale) {
     // Up to 12288 columns stay in registers between the two passes; longer rows
     // are read again for the second.
     constexpr int kMaxGroups = 12288 / 8 / kStageThreads;  // resident groups of 8 columns per thread
+    constexpr bool HILO = A_F32;
     const int row = blockIdx.x;
     const int groups = k >> 3;
-    // A' = bf16_rne(awq * A) of columns 8g..8g+7, as fp32
+    const size_t hi_row = HILO ? (size_t)64 * (row >> 5) + (row & 31) : (size_t)row;
+    uint16_t* const dst_hi = a16 + hi_row * k;
+    uint16_t* const dst_lo = dst_hi + (size_t)32 * k;
+    if (HILO && row >= m) {  // padding token: zero rows, never stored by the matmul
+        for (int g = threadIdx.x; g < groups; g += kStageThreads) {
+            *reinterpret_cast<uint4_t*>(dst_hi + 8 * g) = uint4_t{0u, 0u, 0u, 0u};
+            *reinterpret_cast<uint4_t*>(dst_lo + 8 * g) = uint4_t{0u, 0u, 0u, 0u};
+        }
+        return;
+    }
+    // v = awq * A of columns 8g..8g+7, fp32
     auto load8 = [&](int g, float (&o)[8]) {
         const size_t e0 = (size_t)row * k + 8 * g;
         if constexpr (A_F32) {
@@ -115,22 +141,13 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
                 o[2 * q + 1] = bf16_hi(w4[q]);
             }
         }
-        if constexpr (HAS_AWQ || A_F32) {
-            float s8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-            if constexpr (HAS_AWQ) {
-                const float4_t s0 = *reinterpret_cast<const float4_t*>(awq + 8 * g);
-                const float4_t s1 = *reinterpret_cast<const float4_t*>(awq + 8 * g + 4);
+        if constexpr (HAS_AWQ) {
+            const float4_t s0 = *reinterpret_cast<const float4_t*>(awq + 8 * g);
+            const float4_t s1 = *reinterpret_cast<const float4_t*>(awq + 8 * g + 4);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    s8[q] = s0[q];
-                    s8[4 + q] = s1[q];
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < 8; q += 2) {
-                const uint32_t pk = pack_bf16(o[q] * s8[q], o[q + 1] * s8[q + 1]);
-                o[q] = bf16_lo(pk);
-                o[q + 1] = bf16_hi(pk);
+            for (int q = 0; q < 4; ++q) {
+                o[q] *= s0[q];
+                o[4 + q] *= s1[q];
             }
         }
     };
@@ -157,12 +174,24 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float sc = 2.0f * fp16_range_scale(mx);  // max in [2^14, 2^15)
     if (threadIdx.x == 0) row_scale[row] = pow2_inverse(sc);
+    // the 8 values of a group in storage order, as 4 packed pairs
+    auto pack = [&](const float (&x)[8]) -> uint4_t {
+        return GF4_ORDER ? uint4_t{as_u32(h2(x[0], x[4])), as_u32(h2(x[1], x[5])), as_u32(h2(x[2], x[6])),
+                                   as_u32(h2(x[3], x[7]))}
+                         : uint4_t{as_u32(h2(x[0], x[1])), as_u32(h2(x[2], x[3])), as_u32(h2(x[4], x[5])),
+                                   as_u32(h2(x[6], x[7]))};
+    };
     auto store8 = [&](int g, const float (&x)[8]) {
-        const uint4_t out = GF4_ORDER ? uint4_t{as_u32(h2(x[0] * sc, x[4] * sc)), as_u32(h2(x[1] * sc, x[5] * sc)),
-                                                as_u32(h2(x[2] * sc, x[6] * sc)), as_u32(h2(x[3] * sc, x[7] * sc))}
-                                      : uint4_t{as_u32(h2(x[0] * sc, x[1] * sc)), as_u32(h2(x[2] * sc, x[3] * sc)),
-                                                as_u32(h2(x[4] * sc, x[5] * sc)), as_u32(h2(x[6] * sc, x[7] * sc))};
-        *reinterpret_cast<uint4_t*>(a16 + (size_t)row * k + 8 * g) = out;
+        float s[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s[q] = x[q] * sc;
+        *reinterpret_cast<uint4_t*>(dst_hi + 8 * g) = pack(s);
+        if constexpr (HILO) {
+            float r[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) r[q] = (s[q] - (float)(_Float16)s[q]) * 2048.0f;
+            *reinterpret_cast<uint4_t*>(dst_lo + 8 * g) = pack(r);
+        }
     };
 #pragma unroll
     for (int j = 0; j < kMaxGroups; ++j) {
@@ -176,6 +205,10 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
         store8(g, t);
     }
 }
+
+// Staged rows for m tokens: one per token, or (fp32 input) a hi and a lo row
+// per token padded to whole 32-token groups.
+inline int staged_rows(int m, bool a_f32) { return a_f32 ? 64 * ((m + 31) / 32) : m; }
 
 template <int BM, int BN, int NT, bool A_F32>
 struct StepRegs {
@@ -682,41 +715,59 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
     // Split launches write unscaled fp32 partial sums, split s at
-    // c + s * m * n (OUT_F32 is then true); prefill_split_reduce finishes.
-    void* const c = OUT_F32 ? static_cast<void*>(static_cast<float*>(p.c) + (size_t)split * p.m * p.n) : p.c;
+    // c + s * m_out * n (OUT_F32 is then true); prefill_split_reduce finishes.
+    void* const c = OUT_F32 ? static_cast<void*>(static_cast<float*>(p.c) + (size_t)split * p.m_out * p.n) : p.c;
     const bool vec_ok = (p.n & 3) == 0 && ((uintptr_t)p.c & 15) == 0;
+    // token gm's 4 x 4 outputs of weight tile j: d(g, r) is row n0 + 32 j + 8 g + 4 half + r
+    auto emit = [&](int gm, int j, float rs, auto d_of) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int gm = m0 + 32 * i + l32;
-        if (gm >= p.m) continue;
-        const float rs = p.splits > 1 ? 1.0f : p.row_scale[gm];
+        for (int g = 0; g < 4; ++g) {
+            const int gn = n0 + 32 * j + 8 * g + 4 * half;
+            const size_t o = (size_t)gm * p.n + gn;
+            const float d[4] = {d_of(g, 0) * rs, d_of(g, 1) * rs, d_of(g, 2) * rs, d_of(g, 3) * rs};
+            if (vec_ok && gn + 3 < p.n) {
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<float4_t*>(static_cast<float*>(c) + o) = float4_t{d[0], d[1], d[2], d[3]};
+                else
+                    *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
+                        uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
+            } else {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int gn = n0 + 32 * j + 8 * g + 4 * half;
-                const size_t o = (size_t)gm * p.n + gn;
-                const float d[4] = {acc[i][j][4 * g] * rs, acc[i][j][4 * g + 1] * rs, acc[i][j][4 * g + 2] * rs,
-                                    acc[i][j][4 * g + 3] * rs};
-                if (vec_ok && gn + 3 < p.n) {
-                    if constexpr (OUT_F32)
-                        *reinterpret_cast<float4_t*>(static_cast<float*>(c) + o) = float4_t{d[0], d[1], d[2], d[3]};
-                    else
-                        *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
-                            uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (gn + r < p.n) {
-                            if constexpr (OUT_F32)
-                                static_cast<float*>(c)[o + r] = d[r];
-                            else
-                                static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
-                        }
+                for (int r = 0; r < 4; ++r) {
+                    if (gn + r < p.n) {
+                        if constexpr (OUT_F32)
+                            static_cast<float*>(c)[o + r] = d[r];
+                        else
+                            static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
                     }
                 }
             }
         }
+    };
+    if constexpr (FM % 2 == 0) {
+        if (p.hilo) {
+            // staged rows m0 + 64 i' .. + 63 are tokens m0 / 2 + 32 i' .. + 31: hi (tile 2 i'), lo (2 i' + 1)
+#pragma unroll
+            for (int i = 0; i < FM / 2; ++i) {
+                const int gm = m0 / 2 + 32 * i + l32;
+                if (gm >= p.m_out) continue;
+                const float rs = p.splits > 1 ? 1.0f : p.row_scale[gm];
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    emit(gm, j, rs, [&](int g, int r) {
+                        return acc[2 * i][j][4 * g + r] + acc[2 * i + 1][j][4 * g + r] * 0x1p-11f;
+                    });
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int gm = m0 + 32 * i + l32;
+        if (gm >= p.m_out) continue;
+        const float rs = p.splits > 1 ? 1.0f : p.row_scale[gm];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) emit(gm, j, rs, [&](int g, int r) { return acc[i][j][4 * g + r]; });
     }
 }
 
@@ -873,7 +924,11 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // pick is the fastest or within 5% of it.
 // F16 weights (2 bytes per weight against GF4's half byte) use FN = 2 only:
 // their four-slot register ring of 16-byte loads is four times GF4's.
-PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
+// fp32 input (hilo) stages two rows per token in 32-token groups: the tiles
+// are planned over the staged rows, of at least 64 (one hi and one lo MFMA
+// tile per wave), and the K-split partial sums stay one row per token.
+PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool hilo) {
+    const int m = staged_rows(m_tokens, hilo);
     constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9;
     // K-split partial sums cost less relative to fp16 weight tiles than to GF4
     // ones: with 0.5 the F16 plan for 8192x4096 M=128 was {64,2,4} 57.1 us,
@@ -890,13 +945,14 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
     // 128 tokens, F16 172 against 244; GF4 was slower with them (236-260 us
     // against 210 at 12288x4096).
     static constexpr int kShapes[][2] = {{256, 2}, {128, 4}, {128, 2}, {64, 4}, {64, 2}, {32, 2}};
-    PrefillCfg best{32, 2, 1};
+    PrefillCfg best{hilo ? 64 : 32, 2, 1};
     double best_us = 0;
     for (const auto& sh : kShapes) {
         const int bm = sh[0], fn = sh[1], bn = 128 * fn;
         if ((f16w || q8w) && fn != 2) continue;
         if (bm == 256 && !(f16w || q8w)) continue;
         if (bm > 32 && m <= bm / 2) continue;  // half the token tile or more would be padding
+        if (hilo && bm < 64) continue;
         const long tiles = (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn);
         for (int sp = 1; sp <= 16 && sp <= chunks; ++sp) {
             if (chunks % sp != 0 || (sp > 1 && k / sp < 512)) continue;
@@ -904,7 +960,7 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
             const double rounds = (double)((blocks + cus - 1) / cus);
             const double k_len = (double)k / sp;
             double us = rounds * (kUsPerMflop * 2.0 * bm * bn * k_len * 1e-6 + kUsPerMB * k_len * (2.0 * bm + w_bytes * bn) * 1e-6);
-            if (sp > 1) us += kUsPerPartialMB * 4.0 * sp * m * rows * 1e-6;
+            if (sp > 1) us += kUsPerPartialMB * 4.0 * sp * m_tokens * rows * 1e-6;
             if (best_us == 0 || us < best_us) {
                 best_us = us;
                 best = {bm, fn, sp};
@@ -965,22 +1021,29 @@ PrefillCfg plan_prefill(int m, int rows, int k, bool f16w, bool q8w = false) {
     return best;
 }
 
-PrefillCfg plan_q8_prefill(int m, int rows, int k) { return plan_prefill(m, rows, k, false, true); }
-
-size_t q8_prefill_workspace_bytes(int m, int rows, int k) {
-    return gf4_prefill_workspace_bytes(m, rows, k, plan_q8_prefill(m, rows, k));
+PrefillCfg plan_prefill_kind(int m, int rows, int k, int wkind, bool a_f32) {
+    return plan_prefill(m, rows, k, wkind == 1, wkind == 2, a_f32);
 }
 
-PrefillCfg plan_gf4_prefill(int m, int rows, int k) { return plan_prefill(m, rows, k, false); }
+PrefillCfg plan_gf4_prefill(int m, int rows, int k, bool a_f32) { return plan_prefill_kind(m, rows, k, 0, a_f32); }
 
-size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg) {
-    size_t b = round256((size_t)m * k * 2) + round256((size_t)m * 4);
+// Staged tokens (2 bytes per staged activation), one fp32 scale per token,
+// then the K-split partial sums (fp32, one row per token and split).
+size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg, bool a_f32) {
+    size_t b = round256((size_t)staged_rows(m, a_f32) * k * 2) + round256((size_t)m * 4);
     if (cfg.splits > 1) b += (size_t)cfg.splits * m * rows * 4;
     return b;
 }
 
-size_t gf4_prefill_workspace_bytes(int m, int rows, int k) {
-    return gf4_prefill_workspace_bytes(m, rows, k, plan_gf4_prefill(m, rows, k));
+size_t prefill_workspace_bytes(int m, int rows, int k, int wkind, bool with_f32) {
+    const size_t b16 = gf4_prefill_workspace_bytes(m, rows, k, plan_prefill_kind(m, rows, k, wkind, false), false);
+    if (!with_f32) return b16;
+    const size_t b32 = gf4_prefill_workspace_bytes(m, rows, k, plan_prefill_kind(m, rows, k, wkind, true), true);
+    return b16 > b32 ? b16 : b32;
+}
+
+size_t prefill_min_workspace_bytes(int m, int rows, int k, bool a_f32) {
+    return gf4_prefill_workspace_bytes(m, rows, k, PrefillCfg{64, 2, 1}, a_f32);
 }
 
 namespace {
@@ -988,8 +1051,8 @@ namespace {
 // A workspace sized for another token count may not hold this call's partial
 // sums: split less (ultimately not at all) rather than fail; K halves need
 // each half to stay a multiple of 256 columns.
-void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t workspace_bytes) {
-    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg) > workspace_bytes) {
+void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t workspace_bytes, bool a_f32) {
+    while (cfg.splits > 1 && gf4_prefill_workspace_bytes(m, rows, k, cfg, a_f32) > workspace_bytes) {
         do --cfg.splits;
         while (cfg.splits > 1 && (k % cfg.splits != 0 || (k / cfg.splits) % (256 * cfg.kh) != 0));
     }
@@ -1009,6 +1072,8 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     p.awq = awq;
     p.c = c;
     p.m = m;
+    p.m_out = m;
+    p.hilo = 0;
     p.n = rows;
     p.k = k;
     p.splits = 1;
@@ -1019,19 +1084,23 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         if (cfg.splits < 1 || (cfg.kh != 1 && cfg.kh != 2 && cfg.kh != 4) || k % cfg.splits != 0 ||
             (k / cfg.splits) % (256 * cfg.kh) != 0)
             return hipErrorInvalidValue;
+        // fp32 input: hi and lo tiles pair up inside a wave's token tiles
+        if (af && cfg.bm < 64) return hipErrorInvalidValue;
         // K halves exist for the 8-wave 64- and 128-token tiles of GF4 and q8_0 weights only
         if (cfg.kh == 2 && (f16w || cfg.waves != 8 || cfg.fn != 2 || (cfg.bm != 64 && cfg.bm != 128)))
             return hipErrorInvalidValue;
         // K quarters: the 64-token GF4 tile on 16 waves (128 rows) or 8 (64 rows)
         if (cfg.kh == 4 && (f16w || q8w || (cfg.waves != 16 && cfg.waves != 8) || cfg.fn != 2 || cfg.bm != 64))
             return hipErrorInvalidValue;
+        const int ms = staged_rows(m, af);
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         uint16_t* a16 = reinterpret_cast<uint16_t*>(ws);
-        float* rs = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2));
-        float* partial = reinterpret_cast<float*>(ws + round256((size_t)m * k * 2) + round256((size_t)m * 4));
-#define QW35_STAGE(AF, AW, ORD)                                                                          \
-    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, ORD>), dim3(m), dim3(kStageThreads), 0, stream, a, awq, k, \
-                       a16, rs)
+        float* rs = reinterpret_cast<float*>(ws + round256((size_t)ms * k * 2));
+        float* partial = reinterpret_cast<float*>(ws + round256((size_t)ms * k * 2) + round256((size_t)m * 4));
+        const unsigned stage_grid = af ? (unsigned)(ms / 2) : (unsigned)m;
+#define QW35_STAGE(AF, AW, ORD)                                                                                   \
+    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, ORD>), dim3(stage_grid), dim3(kStageThreads), 0, stream, a, \
+                       awq, m, k, a16, rs)
         if (f16w || q8w) {
             if (af) {
                 if (aw) QW35_STAGE(true, true, false); else QW35_STAGE(true, false, false);
@@ -1051,6 +1120,8 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         p.a = a16;
         p.awq = nullptr;
         p.row_scale = rs;
+        p.m = ms;
+        p.hilo = af ? 1 : 0;
         p.splits = cfg.splits;
         p.k_len = k / cfg.splits;
         const bool split = cfg.splits > 1;
@@ -1121,24 +1192,12 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     return launch_tile<64, 64, 2, 2>(p, af, aw, of, stream);
 }
 
-size_t f16w_prefill_workspace_bytes(int m, int rows, int k) {
-    return gf4_prefill_workspace_bytes(m, rows, k, plan_prefill(m, rows, k, true));
-}
-
-hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (!workspace) return hipErrorInvalidValue;
-    PrefillCfg cfg = plan_prefill(m, rows, k, true);
-    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes);
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 1);
-}
-
-hipError_t launch_q8_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                             int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (!workspace) return hipErrorInvalidValue;
-    PrefillCfg cfg = plan_q8_prefill(m, rows, k);
-    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes);
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 2);
+hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
+                          void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!workspace && wkind != 0) return hipErrorInvalidValue;
+    PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
+    if (workspace) fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {
@@ -1146,11 +1205,5 @@ hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, h
     return hipGetLastError();
 }
 
-hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                              int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    PrefillCfg cfg = plan_gf4_prefill(m, rows, k);
-    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes);
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, 0);
-}
 
 }  // namespace qw35

@@ -104,18 +104,20 @@ hipError_t launch_quantize(uint32_t type_id, const float* src, int rows, int k, 
 unsigned stream_read_blocks(uint64_t bytes);
 hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 
-// GF4 prefill dequant-matmul:
-//   C[m][n] = sum_k bf16_rne(awq[k] * A[m][k]) * W[n][k],  fp32 accumulation.
-// a: [m][k] bf16 (a_f32 == 0) or fp32; c: [m][rows] bf16 RNE (out_f32 == 0) or fp32.
-// workspace (nullable, 256-byte aligned, at least the unsplit size
-// gf4_prefill_workspace_bytes(m, rows, k, {.., 1})): stage A as fp16 with
-// per-row power-of-two scales and contract on fp16 MFMA, split over K (fp32
-// partials in the workspace) when the tiles alone would leave CUs idle and
-// workspace_bytes holds the partials.  Without a workspace: bf16 MFMA, no split.
 // MFMA throughput probe: workgroups x 4 waves x iters x 8 v_mfma_f32_32x32x16_f16
 // (32768 flops each); sink holds workgroups * 256 floats.
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream);
 
+// Prefill dequant-matmul of GF4 words, F16 weights or q8_0 blocks (wkind 0, 1, 2):
+//   C[m][n] = sum_k v[m][k] * W[n][k],  v = awq[k] * A[m][k] (fp32 product), fp32 accumulation.
+// a: [m][k] bf16 (a_f32 == 0) or fp32; c: [m][rows] bf16 RNE (out_f32 == 0) or fp32.
+// workspace (nullable for GF4 only; 256-byte aligned, at least
+// prefill_min_workspace_bytes(m, rows, k, a_f32)): stage v as fp16 with
+// per-token power-of-two scales (fp32 input: an fp16 hi and lo row per token,
+// about 22 significant bits) and contract on fp16 MFMA, split over K (fp32
+// partials in the workspace) when the tiles alone would leave CUs idle and
+// workspace_bytes holds the partials.  Without a workspace (GF4): bf16 MFMA on
+// bf16_rne(v), no split.
 struct PrefillCfg {
     int bm;      // tokens per block: 256 (F16 / q8_0 weights), 128, 64 or 32
     int fn;      // 32-row weight tiles per wave (4 waves per block): 2 or 4 (4 needs bm >= 64)
@@ -130,27 +132,19 @@ struct PrefillCfg {
     // (waves 8) or of four over a 128-row tile (waves 16).
     int kh = 1;
 };
-PrefillCfg plan_gf4_prefill(int m, int rows, int k);
-size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg);
-size_t gf4_prefill_workspace_bytes(int m, int rows, int k);
+PrefillCfg plan_prefill_kind(int m, int rows, int k, int wkind, bool a_f32);
+PrefillCfg plan_gf4_prefill(int m, int rows, int k, bool a_f32);
+size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg, bool a_f32);
+// Workspace of the planned launch for bf16 activations, or (with_f32) the
+// larger of the bf16 and fp32 ones.
+size_t prefill_workspace_bytes(int m, int rows, int k, int wkind, bool with_f32);
+// Smallest workspace the staged path accepts (no K split).
+size_t prefill_min_workspace_bytes(int m, int rows, int k, bool a_f32);
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
                                   int wkind = 0);  // 0 GF4, 1 F16, 2 q8_0
-hipError_t launch_gf4_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                              int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
-
-// F16-weight prefill (GGUF type 1, e.g. the fp16 prefill image of a q8_0 /
-// Q4_K / Q6_K projection): the staged GF4 path with w fp16 [rows][k]; the
-// workspace is required (at least the staged tokens and scales; its full
-// size, f16w_prefill_workspace_bytes, also holds the K-split partials).
-size_t f16w_prefill_workspace_bytes(int m, int rows, int k);
-// q8_0 weights dequantised inside the staged kernel (no image); a workspace of
-// at least gf4_prefill_workspace_bytes(m, rows, k, {.., 1}) is required.
-PrefillCfg plan_q8_prefill(int m, int rows, int k);
-size_t q8_prefill_workspace_bytes(int m, int rows, int k);
-hipError_t launch_q8_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                             int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
-hipError_t launch_f16w_prefill(const void* w, int rows, int k, const void* a, int a_f32, const float* awq, void* c,
-                               int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
+// Planned launch; the workspace is required for F16 and q8_0 weights.
+hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
+                          void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace qw35

@@ -346,14 +346,17 @@ def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tenso
 def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = None,
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
                    workspace: torch.Tensor | None | bool = True, stream=None) -> torch.Tensor:
-    """``C[t] = bf16(awq * a[t]) @ W^T`` for a GF4, q8_0 or F16 weight
+    """``C[t] = (awq * a[t]) @ W^T`` for a GF4, q8_0 or F16 weight
     (``encodeTiledKMatmul``; the other k-quants enter as their fp16 image,
     ``w.prefill``).  q8_0 and F16 need a workspace.
 
     ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
     ``out_dtype`` (bfloat16, rounded to nearest even, or float32).
     ``workspace``: True (allocate one), a tensor from ``prefill_workspace``, or
-    None/False for the path without staging (bf16 MFMA).
+    None/False for the path without staging (bf16 MFMA; GF4 weights, bf16
+    activations, no AWQ).  With a workspace fp32 activations keep fp32
+    precision (an fp16 hi/lo pair per activation) and bf16 ones are carried
+    exactly (with AWQ: the product rounded once to fp16).
     """
     if a.dim() != 2 or not a.is_cuda or not a.is_contiguous() or a.dtype not in (torch.bfloat16, torch.float32):
         raise Qw35Error("matmul_prefill: a must be a contiguous 2-D bf16/fp32 device tensor")
@@ -384,7 +387,9 @@ def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None,
     1..8 tokens run the decode GEMV (fp32 activations); longer chunks run the
     prefill matmul with fp32 output (GF4 and q8_0 directly, the other
     k-quants through their fp16 prefill image), as the reference switches to
-    its tiled matmul for multi-token chunks.
+    its tiled matmul for multi-token chunks.  Both keep the activations at fp32
+    precision (fp16 hi/lo pairs on MFMA), as the reference's tiled matmul
+    keeps src1 in fp32 (qw35_tiled_mm.metal:200-224).
     """
     if x.dim() != 2:
         raise Qw35Error("matvec_batch takes [n_tokens, k] activations")

@@ -39,3 +39,64 @@ def activations(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
 
 def awq_scales(rng: np.random.Generator, k: int) -> np.ndarray:
     return rng.uniform(0.5, 2.0, size=k).astype(np.float32)
+
+
+def prefill_rel_l2_bar(a_f32: bool, awq_on: bool) -> float:
+    """rel-L2 bar of a prefill's fp32 output against oracle.matvec.prefill_f64
+    (unrounded activations) on the weights the kernel contracts: 1e-5 where the
+    staged operand carries the activations exactly (bf16 without AWQ) or to
+    ~22 bits (fp32 as an fp16 hi/lo pair); 4e-4 for bf16 with AWQ (the product
+    rounded once to fp16)."""
+    return 4e-4 if (awq_on and not a_f32) else 1e-5
+
+
+def bf16_out_ok(got_bf16_bits: np.ndarray, want: np.ndarray, a_eff: np.ndarray, w: np.ndarray) -> tuple[bool, str]:
+    """bf16 output within one bf16 ulp of the fp64 value plus the
+    fp32-accumulation allowance 2^-16 * sum_k |A'_k W_k|, per element."""
+    got = om.bf16_bits_to_f32(got_bf16_bits).astype(np.float64)
+    mag = np.abs(want)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 2.0 ** -126))) - 7)
+    abs_sum = np.abs(a_eff.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    bound = ulp + abs_sum * 2.0 ** -16
+    err = np.abs(got - want)
+    worst = float(np.max(err / bound))
+    return bool(np.all(err <= bound)), f"worst err/bound {worst:.3f}"
+
+
+def check_prefill(out, a_host: np.ndarray, awq: np.ndarray | None, w_op: np.ndarray, staged: bool = True,
+                  w_exact: np.ndarray | None = None) -> float:
+    """Bars on a prefill result.  ``out``: the device result (token rows
+    matching ``a_host``); ``a_host``: bf16 bit patterns (uint16) or fp32
+    activations; ``w_op``: the weights the kernel contracts (exact GF4
+    dequantisation, or the fp16 image of a q8_0 / k-quant weight);
+    ``w_exact``: the exact dequantisation when ``w_op`` is an fp16 image.
+
+    * accumulation: against the fp64 product of the operand the path contracts
+      (prefill_staged_operand / prefill_direct_operand): fp32 output within
+      2^-16 * sum_k |A'_k W_k| per element, bf16 output within one ulp more;
+    * fp32 output: rel-L2 against prefill_f64 on the unrounded activations
+      within prefill_rel_l2_bar, and against the exact weights within 1e-3.
+
+    Returns the rel-L2 against prefill_f64 on ``w_exact`` (else ``w_op``), or 0
+    for bf16 output."""
+    import torch
+
+    a_f32 = a_host.dtype == np.float32
+    w64 = np.asarray(w_op).astype(np.float64)
+    op = om.prefill_staged_operand(a_host, awq, a_f32) if staged else om.prefill_direct_operand(a_host, awq)
+    want_op = op @ w64.T
+    if out.dtype == torch.float32:
+        got = out.cpu().numpy().astype(np.float64)
+        bound = (np.abs(op) @ np.abs(w64).T) * 2.0 ** -16 + 1e-30
+        worst = float(np.max(np.abs(got - want_op) / bound))
+        assert worst <= 1.0, f"accumulation: worst err/bound {worst:.3f}"
+        err = om.rel_l2(got, om.prefill_f64(w64, a_host, awq))
+        assert err <= prefill_rel_l2_bar(a_f32, awq is not None), f"rel-L2 {err:.3e} against the unrounded product"
+        if w_exact is not None:
+            err = om.rel_l2(got, om.prefill_f64(w_exact, a_host, awq))
+            assert err <= GEMV_REL_L2, f"rel-L2 {err:.3e} against the exact weights"
+        return err
+    got_bits = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    ok, msg = bf16_out_ok(got_bits, want_op, op, w64)
+    assert ok, msg
+    return 0.0

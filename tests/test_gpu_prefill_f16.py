@@ -4,11 +4,14 @@
 
 Oracle: oracle.matvec.prefill_image (fp16_rne of the exact dequantised weight,
 the half dequantisation of the reference's tiled matmul,
-qw35_tiled_mm.metal:199-255) and an fp64 product of the exact operands the
-kernel contracts, A' = bf16_rne(awq * A) and the fp16 weights.  Bars: the image
-bit-exact; fp32 output within 1e-3 relative L2 and, per element, within the
-fp32-accumulation allowance 2^-16 * sum_k |A'_k W_k|; bf16 output within one
-bf16 ulp plus that allowance (the GF4 prefill bars of test_gpu_prefill.py)."""
+qw35_tiled_mm.metal:199-255) and oracle.matvec.prefill_f64, the fp64 product
+of the unrounded activations (the reference keeps them fp32,
+qw35_tiled_mm.metal:200-224).  Bars: the image bit-exact; the bars of
+tests/helpers.py:check_prefill (the GF4 prefill bars): fp32 output within
+prefill_rel_l2_bar of the product with the image and within 1e-3 of the
+product with the exact weights, per element within the fp32-accumulation
+allowance of the staged operand; bf16 output within one bf16 ulp plus that
+allowance."""
 from __future__ import annotations
 
 import numpy as np
@@ -16,7 +19,7 @@ import pytest
 
 from oracle import matvec as om
 from oracle import q6_k as oq6
-from tests.helpers import activations, awq_scales, bf16_normal, make_weight
+from tests.helpers import activations, awq_scales, bf16_normal, check_prefill, make_weight
 
 pytestmark = pytest.mark.gpu
 
@@ -68,32 +71,24 @@ def _bf16_tensor(bits, cuda):
 @pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (37, 1000, 4096), (128, 4096, 4096), (300, 640, 12288)])
 @pytest.mark.parametrize("awq_on", [False, True])
 @pytest.mark.parametrize("out_f32", [True, False])
-def test_f16_prefill_matches_oracle(cuda, m, n, k, awq_on, out_f32):
+@pytest.mark.parametrize("a_f32", [False, True])
+def test_f16_prefill_matches_oracle(cuda, m, n, k, awq_on, out_f32, a_f32):
     import torch
 
     rng = np.random.default_rng(m * 7 + n + k + awq_on)
     w16 = bf16_normal(rng, (n, k), 0.02).astype(np.float16)
     a32 = activations(rng, m, k)
     awq = awq_scales(rng, k) if awq_on else None
-    bits = om.f32_to_bf16_bits(a32)
-    a_eff = om.prefill_operand(bits, awq)
+    a_host = a32 if a_f32 else om.f32_to_bf16_bits(a32)
+    a_dev = _t(a32, cuda) if a_f32 else _bf16_tensor(a_host, cuda)
     hw = _rt().HipWeight.upload(w16.view(np.uint8), om.TYPE_F16, n, k)
-    out = _rt().matmul_prefill(hw, _bf16_tensor(bits, cuda), awq=_t(awq, cuda) if awq is not None else None,
+    out = _rt().matmul_prefill(hw, a_dev, awq=_t(awq, cuda) if awq is not None else None,
                                out_dtype=torch.float32 if out_f32 else torch.bfloat16)
-    w64 = w16.astype(np.float64)
-    want = a_eff.astype(np.float64) @ w64.T
-    allow = (np.abs(a_eff.astype(np.float64)) @ np.abs(w64).T) * 2.0 ** -16
-    if out_f32:
-        got = out.cpu().numpy().astype(np.float64)
-        assert om.rel_l2(got, want) <= 1e-3
-        assert np.all(np.abs(got - want) <= allow + 1e-30)
-    else:
-        got = om.bf16_bits_to_f32(out.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
-        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
-        assert np.all(np.abs(got - want) <= ulp + allow)
+    check_prefill(out, a_host, awq, w16.astype(np.float32))
 
 
 def test_f16_prefill_fp32_input(cuda):
+    """fp32 activations of larger magnitude with AWQ: fp32 precision (hi/lo staging)."""
     import torch
 
     rng = np.random.default_rng(5)
@@ -102,25 +97,24 @@ def test_f16_prefill_fp32_input(cuda):
     a32 = activations(rng, m, k) * np.float32(100.0)
     awq = awq_scales(rng, k)
     hw = _rt().HipWeight.upload(w16.view(np.uint8), om.TYPE_F16, n, k)
-    out = _rt().matmul_prefill(hw, _t(a32, cuda), awq=_t(awq, cuda), out_dtype=torch.float32).cpu().numpy()
-    a_eff = om.bf16_round(a32 * awq[None, :]).astype(np.float64)
-    want = a_eff @ w16.astype(np.float64).T
-    assert om.rel_l2(out, want) <= 1e-3
+    out = _rt().matmul_prefill(hw, _t(a32, cuda), awq=_t(awq, cuda), out_dtype=torch.float32)
+    check_prefill(out, a32, awq, w16.astype(np.float32))
 
 
 @pytest.mark.parametrize("name", ["gf2", "q8_0", "q4_k", "q5_k", "q6_k"])
 def test_matvec_batch_long_kquant_chunk(cuda, name):
+    """More than 8 fp32 tokens on a k-quant weight: the prefill matmul on its
+    fp16 image (q8_0: decoded in the kernel to the same values) with fp32
+    activation precision; against the exact weights the fp16 weights cost
+    ~2^-12 per weight, under the 1e-3 bar."""
     rows, k, m = 700, 4096, 64
     raw, deq = _weight(name, rows, k, seed=9)
     rng = np.random.default_rng(10)
     x = activations(rng, m, k)
     w = _rt().HipWeight.upload(raw, NAMES[name], rows, k)
-    got = _rt().matvec_batch(w, _t(x, cuda)).cpu().numpy()
-    img = om.prefill_image(NAMES[name], raw, rows, k).astype(np.float64)
-    assert om.rel_l2(got, om.bf16_round(x).astype(np.float64) @ img.T) <= 1e-3
-    # against the exact weights and fp32 activations: fp16 weights and bf16
-    # activations (the reference tiled matmul's half weights) cost ~2^-9
-    assert om.rel_l2(got, om.matvec_f64(deq, x)) <= 5e-3
+    got = _rt().matvec_batch(w, _t(x, cuda))
+    img = om.prefill_image(NAMES[name], raw, rows, k)
+    check_prefill(got, x, None, img.astype(np.float32), w_exact=deq)
     assert w.prefill is w.prefill  # the image is made once and kept
 
 
