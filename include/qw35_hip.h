@@ -59,6 +59,8 @@ extern "C" {
 #define QW35_HIP_TYPE_GF4 100u
 #define QW35_HIP_TYPE_GF2 101u
 #define QW35_HIP_MAX_BATCH 8u
+/* Largest prefill chunk of a projection runtime (qw35_hip_runtime_create). */
+#define QW35_HIP_MAX_PREFILL_CHUNK 4096u
 
 /* GGUF tensor descriptor; field-for-field the reference's
  * qw35_metal_tensor_desc (qw35-server/src/metal/bridge/Qw35MetalTypes.h:18-27),
@@ -252,20 +254,28 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight *w, void *dst, void *stream, c
 #define QW35_HIP_OP_MATVEC 0u /* dst (+)= W (awq * x), see qw35_hip_decode_matvec */
 #define QW35_HIP_OP_SWIGLU 1u /* dst = silu(gate (awq*x)) * (up (awq*x)) */
 #define QW35_HIP_OP_ARGMAX 2u /* greedy head, see qw35_hip_output_argmax: token[b], dst[b] = logit */
+/* Multi-token ops (a prefill chunk): the prefill matmul of fp32 activations
+ * into fp32 dst, n_batch = the chunk's tokens (1..65536), through the op's
+ * workspace (qw35_hip_matmul_prefill_epilogue). */
+#define QW35_HIP_OP_MATMUL 3u        /* dst (+)= W (awq * x): STORE, or ADD with residual */
+#define QW35_HIP_OP_MATMUL_SWIGLU 4u /* dst = silu(gate (awq*x)) * (up (awq*x)): two launches (STORE, SWIGLU) */
 typedef struct {
     uint32_t kind;               /* QW35_HIP_OP_* */
-    uint32_t n_batch;            /* 1..8 */
-    int32_t residual;            /* MATVEC only: nonzero adds into dst */
+    uint32_t n_batch;            /* 1..8; MATMUL / MATMUL_SWIGLU: tokens, 1..65536 */
+    int32_t residual;            /* MATVEC / MATMUL: nonzero adds into dst */
     uint32_t reserved;
-    const qw35_hip_weight *w;    /* MATVEC / ARGMAX weight or SWIGLU gate */
-    const qw35_hip_weight *w_up; /* SWIGLU up, else NULL */
+    const qw35_hip_weight *w;    /* MATVEC / MATMUL / ARGMAX weight or SWIGLU / MATMUL_SWIGLU gate */
+    const qw35_hip_weight *w_up; /* SWIGLU / MATMUL_SWIGLU up, else NULL */
     const float *x;              /* device [n_batch][k] */
     const float *awq;            /* device [k] or NULL */
     float *dst;                  /* device [n_batch][rows]; ARGMAX: the chosen logits [n_batch] */
-    /* ARGMAX only (NULL / 0 otherwise): the chosen rows [n_batch], and a workspace
-     * of qw35_hip_output_argmax_workspace_size(w, n_batch) bytes, 256-byte
-     * aligned, used by this op alone. */
+    /* ARGMAX only (NULL otherwise): the chosen rows [n_batch]. */
     uint32_t *token;
+    /* ARGMAX: a workspace of qw35_hip_output_argmax_workspace_size(w, n_batch)
+     * bytes used by this op alone.  MATMUL / MATMUL_SWIGLU: a prefill
+     * workspace (qw35_hip_matmul_prefill_workspace_size), which ops that run
+     * one after the other may share.  256-byte aligned; NULL / 0 for the
+     * other kinds. */
     void *workspace;
     uint64_t workspace_bytes;
 } qw35_hip_plan_op;
@@ -339,12 +349,20 @@ typedef enum {
     QW35_HIP_LOGITS_FULL = 2,   /* the full logits vector */
 } qw35_hip_logits_mode;
 
-/* Runtime-owned fp32 device buffers, [n_batch][width] with row stride width
- * (the reference runtime's buffers, Qw35MetalRuntime.m:374-460). */
+/* Runtime-owned fp32 device buffers (the reference runtime's buffers,
+ * Qw35MetalRuntime.m:374-460): max(max_batch, prefill_chunk) rows of `width`
+ * floats each (the logits: max_batch rows), width being the largest row any
+ * op reads or writes there.  Like the reference's max-sized scratch, a
+ * buffer holds the n rows of one op packed at that op's own row length: an op
+ * of k input columns reads row t at offset t * k, an op of `rows` output rows
+ * writes row t at offset t * rows.  So where a buffer serves ops of
+ * different lengths (QKV: attn_q and attn_qkv; CORE: attn_output and ssm_out
+ * inputs), the row stride of each op is its own length, not `width`. */
 #define QW35_HIP_RT_NORM 0u   /* [emb] input of the mixer input projections, the FFN and the head (_norm) */
-#define QW35_HIP_RT_CORE 1u   /* [max(heads*value_length, ssm_inner)] input of attn_output / ssm_out (_core) */
+#define QW35_HIP_RT_CORE 1u   /* input of attn_output [heads*value_length] or ssm_out [ssm_inner] (_core) */
 #define QW35_HIP_RT_ACT 2u    /* [emb] residual stream; attn_output, ssm_out and ffn_down add into it (_act_a) */
-#define QW35_HIP_RT_QKV 3u    /* attn_q (heads*key_length*(attn_gate?2:1)) or attn_qkv output (_qkv) */
+#define QW35_HIP_RT_QKV 3u    /* output of attn_q [heads*key_length*(attn_gate?2:1)] or attn_qkv
+                               * [ssm_inner + 2*groups*state] (_qkv) */
 #define QW35_HIP_RT_K 4u      /* [kv_heads*key_length] attn_k output */
 #define QW35_HIP_RT_V 5u      /* [kv_heads*value_length] attn_v output */
 #define QW35_HIP_RT_Z 6u      /* [ssm_inner] attn_gate output (_z_gate) */
@@ -359,12 +377,18 @@ typedef enum {
  * store of model_map (qw35_hip_store_create), resolve and validate every
  * projection (blk.N.attn_q/k/v/output or blk.N.attn_qkv/attn_gate/ssm_beta/
  * ssm_alpha/ssm_out by layer kind, blk.N.ffn_gate/up/down, output.weight with
- * vocab_size rows), and allocate the buffers above for max_batch (1..8) batch
- * rows.  NULL on error (missing tensor, shape that does not match hparams,
- * type the GEMVs do not take, gate/up of different types). */
+ * vocab_size rows), and allocate the buffers above.  max_batch (1..8): rows
+ * of a decode step; prefill_chunk (0..QW35_HIP_MAX_PREFILL_CHUNK): most
+ * tokens of a prefill chunk (the reference's prefill_chunk argument of
+ * qw35_metal_runtime_create, Qw35FFI.h:37-50; its server's default is 128,
+ * its maximum 256, qw35-server/src/model.rs:30-31).  Above 8, the runtime
+ * also holds one prefill matmul workspace and, for each projection that is
+ * not GF4 or q8_0, its fp16 prefill image (qw35_hip_dequantize_f16: 2 bytes
+ * per weight).  NULL on error (missing tensor, shape that does not match
+ * hparams, type the GEMVs do not take, gate/up of different types). */
 void *qw35_hip_runtime_create(const void *model_map, uint64_t model_size, const qw35_hip_tensor_desc *tensors,
                               uintptr_t tensor_count, const qw35_hip_hparams *hparams, uint32_t vocab_size,
-                              uint32_t max_batch, char *err, uintptr_t err_len);
+                              uint32_t max_batch, uint32_t prefill_chunk, char *err, uintptr_t err_len);
 /* Waits for the runtime's work, then frees it (the store when its last user goes). */
 void qw35_hip_runtime_destroy(void *runtime);
 /* One decode step's projections for n_batch rows of the buffers, replayed from
@@ -373,6 +397,19 @@ void qw35_hip_runtime_destroy(void *runtime);
  * copy_logits, as in the reference (Qw35FFI.h:87-88).  Replaces the projection
  * part of qw35_metal_runtime_eval_token (Qw35FFI.h:92-97). */
 int qw35_hip_runtime_eval_step(void *runtime, uint32_t n_batch, int logits_mode, char *err, uintptr_t err_len);
+/* One prefill chunk's projections for n_tokens rows of the buffers (1 ..
+ * max(max_batch, prefill_chunk)), in evalTokens' order (Qw35MetalRuntime.m:
+ * 1227-1333): per layer the mixer input projections over NORM, the mixer
+ * output projection over CORE added into ACT, ffn_gate / ffn_up / SwiGLU over
+ * NORM into FFN, ffn_down over FFN added into ACT; then the head (logits_mode)
+ * on the chunk's last NORM row only, as evalTokens runs encodeOutputHead on
+ * the last token.  More than 8 tokens run the prefill matmul with fp32
+ * activations (qw35_hip_matmul_prefill_epilogue: ADD for the output
+ * projections, SWIGLU for ffn_up), up to 8 the decode GEMVs.  Recorded as a
+ * hipGraph on first use of (n_tokens, logits_mode) and replayed; asynchronous
+ * like eval_step.  A following argmax / copy_logits reads one row.  Replaces
+ * the projection part of qw35_metal_runtime_eval_tokens (Qw35FFI.h:97-105). */
+int qw35_hip_runtime_eval_chunk(void *runtime, uint32_t n_tokens, int logits_mode, char *err, uintptr_t err_len);
 /* Wait for the last eval; then the greedy head's rows and logits of its n_batch
  * batch rows (that eval must have used QW35_HIP_LOGITS_ARGMAX).  Replaces
  * qw35_metal_runtime_argmax (Qw35FFI.h:106-111). */
@@ -437,6 +474,26 @@ uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight *w, uint32
 int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
                             uint32_t c_dtype, uint32_t n_tokens, void *workspace, uint64_t workspace_bytes,
                             void *stream, char *err, uintptr_t err_len);
+/* The prefill matmul with the result r = W v written through an epilogue
+ * (fp32 c and a workspace; the other arguments as qw35_hip_matmul_prefill):
+ *   QW35_HIP_EPILOGUE_STORE   c = r                (qw35_hip_matmul_prefill)
+ *   QW35_HIP_EPILOGUE_ADD     c += r               (the residual add of the decode GEMVs, for
+ *                                                   attn_output / ssm_out / ffn_down over a chunk)
+ *   QW35_HIP_EPILOGUE_SWIGLU  c = silu(c) * r      (c holds the ffn_gate product, r is ffn_up's:
+ *                                                   encodeSwiGLU, Qw35MetalRuntime+FFN.m:369-383,
+ *                                                   kernel qw35_swiglu_f32 of qw35_core.metal:149,
+ *                                                   fused into the up projection)
+ * silu(v) = v / (1 + exp(-v)) (qw35_types.metal:40-42).  With a K split the
+ * epilogue is applied once, to the sum of the splits.  The reference runs
+ * ffn_gate and ffn_up as two tiled matmuls and SwiGLU as a third dispatch
+ * (Qw35MetalRuntime.m:1298-1301); here the third is the up matmul's epilogue. */
+#define QW35_HIP_EPILOGUE_STORE 0u
+#define QW35_HIP_EPILOGUE_ADD 1u
+#define QW35_HIP_EPILOGUE_SWIGLU 2u
+int qw35_hip_matmul_prefill_epilogue(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq,
+                                     void *c, uint32_t c_dtype, uint32_t epilogue, uint32_t n_tokens,
+                                     void *workspace, uint64_t workspace_bytes, void *stream, char *err,
+                                     uintptr_t err_len);
 
 /* Weight producer: fp32 src [rows][k] (device, 16-byte aligned) -> raw tensor
  * bytes of type_id in dst (device, 16-byte aligned, rows * row_bytes(type, k)

@@ -76,6 +76,14 @@ class PlanOp(C.Structure):
 
 
 OP_ARGMAX = 2
+OP_MATMUL = 3
+OP_MATMUL_SWIGLU = 4
+
+# Prefill matmul epilogues (QW35_HIP_EPILOGUE_*).
+EPILOGUE_STORE = 0
+EPILOGUE_ADD = 1
+EPILOGUE_SWIGLU = 2
+MAX_PREFILL_CHUNK = 4096
 
 LOGITS_NONE = 0
 LOGITS_ARGMAX = 1
@@ -171,10 +179,11 @@ PROTOTYPES: dict[str, tuple] = {
     "qw35_hip_runtime_create": (
         C.c_void_p,
         [C.c_void_p, C.c_uint64, C.POINTER(TensorDesc), C.c_size_t, C.POINTER(Hparams), C.c_uint32, C.c_uint32,
-         C.c_char_p, C.c_size_t],
+         C.c_uint32, C.c_char_p, C.c_size_t],
     ),
     "qw35_hip_runtime_destroy": (None, [C.c_void_p]),
     "qw35_hip_runtime_eval_step": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, C.c_char_p, C.c_size_t]),
+    "qw35_hip_runtime_eval_chunk": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, C.c_char_p, C.c_size_t]),
     "qw35_hip_runtime_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]),
     "qw35_hip_runtime_copy_logits": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
     "qw35_hip_runtime_sync": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
@@ -191,6 +200,11 @@ PROTOTYPES: dict[str, tuple] = {
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
          C.c_uint64, C.c_void_p, C.c_char_p, C.c_size_t],
+    ),
+    "qw35_hip_matmul_prefill_epilogue": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
+         C.c_void_p, C.c_uint64, C.c_void_p, C.c_char_p, C.c_size_t],
     ),
     "qw35_hip_quantize": (
         C.c_int,

@@ -210,6 +210,54 @@ bool mergeable(const qw35_hip_plan_op& a, const qw35_hip_plan_op& b) {
     return !overlaps(a.dst, da, b.dst, db) && !overlaps(a.x, xa, a.dst, da) && !overlaps(a.x, xa, b.dst, db);
 }
 
+// Weight form of the prefill kernel: 0 GF4 words, 1 F16, 2 q8_0 blocks; -1 none.
+int prefill_wkind(uint32_t type_id) {
+    return type_id == qw35::kTypeGF4 ? 0 : type_id == qw35::kTypeF16 ? 1 : type_id == qw35::kTypeQ8_0 ? 2 : -1;
+}
+
+// A MATMUL / MATMUL_SWIGLU plan op: the rules of qw35_hip_matmul_prefill(_epilogue)
+// with fp32 activations and output and the op's workspace.
+bool check_matmul_op(const qw35_hip_plan_op& o, const char* what, char* err, uintptr_t err_len) {
+    const bool sw = o.kind == QW35_HIP_OP_MATMUL_SWIGLU;
+    if (!check_weight(o.w, what, err, err_len) || !check_chunked_k(o.w, what, err, err_len)) return false;
+    if (prefill_wkind(o.w->type_id) < 0) {
+        set_err(err, err_len, "%s: the prefill matmul takes GF4, q8_0 or F16 weights, got type %u", what,
+                o.w->type_id);
+        return false;
+    }
+    if (sw) {
+        if (o.residual) {
+            set_err(err, err_len, "%s: a MATMUL_SWIGLU op has no residual form", what);
+            return false;
+        }
+        if (!check_weight(o.w_up, what, err, err_len)) return false;
+        if (o.w_up->type_id != o.w->type_id || o.w_up->k != o.w->k || o.w_up->rows != o.w->rows) {
+            set_err(err, err_len, "%s: gate and up must share type and shape", what);
+            return false;
+        }
+    } else if (o.w_up) {
+        set_err(err, err_len, "%s: a MATMUL op takes no w_up", what);
+        return false;
+    }
+    if (!o.x || !o.dst || ((uintptr_t)o.x & 15u) || (o.awq && ((uintptr_t)o.awq & 15u)) || ((uintptr_t)o.dst & 3u)) {
+        set_err(err, err_len, "%s: x/awq must be non-null 16-byte aligned and dst non-null 4-byte aligned", what);
+        return false;
+    }
+    if (o.n_batch < 1 || o.n_batch > 65536 || (uint64_t)o.n_batch * o.w->k > kMaxPrefillElems / 2 ||
+        o.w->rows > (1ull << 24)) {
+        set_err(err, err_len, "%s: n_batch=%u tokens must be in 1..65536 with n_batch * k <= %llu", what, o.n_batch,
+                (unsigned long long)(kMaxPrefillElems / 2));
+        return false;
+    }
+    const uint64_t need = qw35::prefill_min_workspace_bytes((int)o.n_batch, (int)o.w->rows, (int)o.w->k, true);
+    if (!o.workspace || ((uintptr_t)o.workspace & 255u) || o.workspace_bytes < need) {
+        set_err(err, err_len, "%s: a MATMUL op needs a 256-byte aligned workspace of >= %llu bytes", what,
+                (unsigned long long)need);
+        return false;
+    }
+    return true;
+}
+
 // Greedy head workspace: per batch row, one (token, logit) partial per
 // workgroup of the GEMV launch; tokens first, logits at a 256-byte boundary.
 uint64_t argmax_ws_part(const qw35_hip_weight* w, uint32_t n_batch) {
@@ -396,6 +444,8 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                         (unsigned long long)(2 * part));
                 return nullptr;
             }
+        } else if (o.kind == QW35_HIP_OP_MATMUL || o.kind == QW35_HIP_OP_MATMUL_SWIGLU) {
+            if (!check_matmul_op(o, what, err, err_len)) return nullptr;
         } else {
             set_err(err, err_len, "%s: unknown kind %u", what, o.kind);
             return nullptr;
@@ -415,6 +465,8 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
             if (ws_bytes) {
                 e = hipMalloc(&plan->ws, ws_bytes);
                 if (e == hipSuccess) e = hipMemset(plan->ws, 0, ws_bytes);
+                // the counters must be zero before the first replay, on whatever stream it runs
+                if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
             }
             if (e == hipSuccess) e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
             if (e == hipSuccess) e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
@@ -428,6 +480,22 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
         qw35::LaunchInfo info{};
         for (uint32_t i = 0; i < n_ops && launch == hipSuccess;) {
             const qw35_hip_plan_op& o = ops[i];
+            if (o.kind == QW35_HIP_OP_MATMUL || o.kind == QW35_HIP_OP_MATMUL_SWIGLU) {
+                if (pass == 1) {
+                    const bool sw = o.kind == QW35_HIP_OP_MATMUL_SWIGLU;
+                    auto mm = [&](const qw35_hip_weight* w, uint32_t epi) {
+                        return qw35::launch_prefill(prefill_wkind(w->type_id), w->data, (int)w->rows, (int)w->k, o.x,
+                                                    1, o.awq, o.dst, (int)o.n_batch, 1, o.workspace,
+                                                    o.workspace_bytes, s, (int)epi);
+                    };
+                    launch = mm(o.w, sw          ? QW35_HIP_EPILOGUE_STORE
+                                     : o.residual ? QW35_HIP_EPILOGUE_ADD
+                                                  : QW35_HIP_EPILOGUE_STORE);
+                    if (launch == hipSuccess && sw) launch = mm(o.w_up, QW35_HIP_EPILOGUE_SWIGLU);
+                }
+                ++i;
+                continue;
+            }
             if (o.kind == QW35_HIP_OP_ARGMAX) {
                 qw35::GemvArgs a = gemv_args(o.w, nullptr, o.x, o.awq, nullptr, o.n_batch, 0);
                 a.am_token = static_cast<uint32_t*>(o.workspace);
@@ -541,13 +609,6 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight* w, void* dst, void* stream, c
                : 0;
 }
 
-namespace {
-// Weight form of the prefill kernel: 0 GF4 words, 1 F16, 2 q8_0 blocks; -1 none.
-int prefill_wkind(uint32_t type_id) {
-    return type_id == qw35::kTypeGF4 ? 0 : type_id == qw35::kTypeF16 ? 1 : type_id == qw35::kTypeQ8_0 ? 2 : -1;
-}
-}  // namespace
-
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32_t n_tokens) {
     char msg[8];
     if (!check_weight(w, "matmul_prefill", msg, sizeof msg) || !check_chunked_k(w, "", msg, sizeof msg) ||
@@ -563,8 +624,23 @@ uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight* w, uint32
 int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
                             uint32_t c_dtype, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes,
                             void* stream, char* err, uintptr_t err_len) {
+    return qw35_hip_matmul_prefill_epilogue(w, a, a_dtype, awq, c, c_dtype, QW35_HIP_EPILOGUE_STORE, n_tokens,
+                                            workspace, workspace_bytes, stream, err, err_len);
+}
+
+int qw35_hip_matmul_prefill_epilogue(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq,
+                                     void* c, uint32_t c_dtype, uint32_t epilogue, uint32_t n_tokens, void* workspace,
+                                     uint64_t workspace_bytes, void* stream, char* err, uintptr_t err_len) {
     if (!check_weight(w, "matmul_prefill", err, err_len) || !check_chunked_k(w, "matmul_prefill", err, err_len))
         return 0;
+    if (epilogue > QW35_HIP_EPILOGUE_SWIGLU) {
+        set_err(err, err_len, "matmul_prefill: unknown epilogue %u", epilogue);
+        return 0;
+    }
+    if (epilogue != QW35_HIP_EPILOGUE_STORE && (c_dtype != QW35_HIP_DTYPE_F32 || !workspace)) {
+        set_err(err, err_len, "matmul_prefill: the add and SwiGLU epilogues take fp32 c and a workspace");
+        return 0;
+    }
     if (w->type_id != qw35::kTypeGF4 && w->type_id != qw35::kTypeF16 && w->type_id != qw35::kTypeQ8_0) {
         set_err(err, err_len,
                 "matmul_prefill: GF4 (type 100), q8_0 (type 8) or F16 (type 1) weights, got %s; make the fp16 "
@@ -621,7 +697,7 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
     }
     return check_hip(qw35::launch_prefill(wkind, w->data, (int)w->rows, (int)w->k, a, a_f32, awq, c, (int)n_tokens,
                                           c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace ? workspace_bytes : 0,
-                                          static_cast<hipStream_t>(stream)),
+                                          static_cast<hipStream_t>(stream), (int)epilogue),
                      "matmul_prefill", err, err_len)
                ? 1
                : 0;

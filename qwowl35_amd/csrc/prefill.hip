@@ -55,10 +55,18 @@ struct PrefillArgs {
     int m, n, k;             // m: rows of a (staged path: staged rows)
     int m_out;               // rows of c (tokens)
     int hilo;                // staged fp32 input: MFMA tiles 2i, 2i + 1 are one token tile's hi, lo rows
+    int epi;                 // fp32 c: kEpiStore c = r, kEpiAdd c += r, kEpiSwiglu c = silu(c) * r
     int tiles_m, tiles_n;
     int splits;              // staged path: K split this many ways (1: none)
     int k_len;               // columns per split
 };
+
+// How a result r is written to fp32 c.
+constexpr int kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2;
+
+__device__ __forceinline__ float epilogue(int epi, float old, float r) {
+    return epi == kEpiAdd ? old + r : epi == kEpiSwiglu ? silu(old) * r : r;
+}
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{lo, hi}, bf16x2_t));
@@ -718,27 +726,38 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // c + s * m_out * n (OUT_F32 is then true); prefill_split_reduce finishes.
     void* const c = OUT_F32 ? static_cast<void*>(static_cast<float*>(p.c) + (size_t)split * p.m_out * p.n) : p.c;
     const bool vec_ok = (p.n & 3) == 0 && ((uintptr_t)p.c & 15) == 0;
+    // split launches write partial sums; the reduction applies the epilogue
+    const int epi = OUT_F32 && p.splits == 1 ? p.epi : kEpiStore;
     // token gm's 4 x 4 outputs of weight tile j: d(g, r) is row n0 + 32 j + 8 g + 4 half + r
     auto emit = [&](int gm, int j, float rs, auto d_of) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int gn = n0 + 32 * j + 8 * g + 4 * half;
             const size_t o = (size_t)gm * p.n + gn;
-            const float d[4] = {d_of(g, 0) * rs, d_of(g, 1) * rs, d_of(g, 2) * rs, d_of(g, 3) * rs};
+            float d[4] = {d_of(g, 0) * rs, d_of(g, 1) * rs, d_of(g, 2) * rs, d_of(g, 3) * rs};
             if (vec_ok && gn + 3 < p.n) {
-                if constexpr (OUT_F32)
-                    *reinterpret_cast<float4_t*>(static_cast<float*>(c) + o) = float4_t{d[0], d[1], d[2], d[3]};
-                else
+                if constexpr (OUT_F32) {
+                    float4_t* const dst = reinterpret_cast<float4_t*>(static_cast<float*>(c) + o);
+                    if (epi != kEpiStore) {
+                        const float4_t old = *dst;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) d[r] = epilogue(epi, old[r], d[r]);
+                    }
+                    *dst = float4_t{d[0], d[1], d[2], d[3]};
+                } else {
                     *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
                         uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
+                }
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if (gn + r < p.n) {
-                        if constexpr (OUT_F32)
-                            static_cast<float*>(c)[o + r] = d[r];
-                        else
+                        if constexpr (OUT_F32) {
+                            float* const dst = static_cast<float*>(c) + o + r;
+                            *dst = epi != kEpiStore ? epilogue(epi, *dst, d[r]) : d[r];
+                        } else {
                             static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+                        }
                     }
                 }
             }
@@ -771,15 +790,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     }
 }
 
-// C[m][n] = row_scale[m] * sum_s partial[s][m][n], splits summed in order.
-// One thread per 4 consecutive outputs of a row.
+// C[m][n] = row_scale[m] * sum_s partial[s][m][n], splits summed in order,
+// written through the epilogue (fp32 C).  One thread per 4 consecutive
+// outputs of a row.
 constexpr int kReduceThreads = 256;
 
 template <bool OUT_F32>
 __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const float* __restrict__ partial,
                                                                        int splits, int m, int n,
                                                                        const float* __restrict__ row_scale,
-                                                                       void* __restrict__ c) {
+                                                                       void* __restrict__ c, int epi) {
     const int n4 = (n + 3) >> 2;
     const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
     if (idx >= (size_t)m * n4) return;
@@ -807,7 +827,13 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     for (int r = 0; r < 4; ++r) d[r] *= rs;
     if (vec) {
         if constexpr (OUT_F32) {
-            *reinterpret_cast<float4_t*>(static_cast<float*>(c) + o) = float4_t{d[0], d[1], d[2], d[3]};
+            float4_t* const dst = reinterpret_cast<float4_t*>(static_cast<float*>(c) + o);
+            if (epi != kEpiStore) {
+                const float4_t old = *dst;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) d[r] = epilogue(epi, old[r], d[r]);
+            }
+            *dst = float4_t{d[0], d[1], d[2], d[3]};
         } else {
             typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
             *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
@@ -815,10 +841,12 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
         }
     } else {
         for (int r = 0; r < cnt; ++r) {
-            if constexpr (OUT_F32)
-                static_cast<float*>(c)[o + r] = d[r];
-            else
+            if constexpr (OUT_F32) {
+                float* const dst = static_cast<float*>(c) + o + r;
+                *dst = epi != kEpiStore ? epilogue(epi, *dst, d[r]) : d[r];
+            } else {
                 static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+            }
         }
     }
 }
@@ -1064,7 +1092,7 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 // wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks (1 and 2 take column-order tokens and a workspace).
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
-                                  hipStream_t stream, int wkind) {
+                                  hipStream_t stream, int wkind, int epi) {
     const bool f16w = wkind == 1, q8w = wkind == 2;
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
@@ -1074,6 +1102,10 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     p.m = m;
     p.m_out = m;
     p.hilo = 0;
+    p.epi = epi;
+    // epilogues read fp32 c; the path without a workspace has none
+    if (epi != kEpiStore && (!out_f32 || !workspace)) return hipErrorInvalidValue;
+    if (epi < kEpiStore || epi > kEpiSwiglu) return hipErrorInvalidValue;
     p.n = rows;
     p.k = k;
     p.splits = 1;
@@ -1178,10 +1210,10 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const dim3 grid((unsigned)((threads + kReduceThreads - 1) / kReduceThreads));
         if (of)
             hipLaunchKernelGGL((prefill_split_reduce<true>), grid, dim3(kReduceThreads), 0, stream, partial,
-                               cfg.splits, m, rows, rs, c);
+                               cfg.splits, m, rows, rs, c, epi);
         else
             hipLaunchKernelGGL((prefill_split_reduce<false>), grid, dim3(kReduceThreads), 0, stream, partial,
-                               cfg.splits, m, rows, rs, c);
+                               cfg.splits, m, rows, rs, c, kEpiStore);
         return hipGetLastError();
     }
     // Direct path: largest tile that still gives every CU a block.
@@ -1193,11 +1225,12 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
 }
 
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
-                          void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                          void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                          int epi) {
     if (!workspace && wkind != 0) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
     if (workspace) fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind);
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind, epi);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {

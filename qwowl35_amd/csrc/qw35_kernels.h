@@ -140,11 +140,13 @@ size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg, bool 
 size_t prefill_workspace_bytes(int m, int rows, int k, int wkind, bool with_f32);
 // Smallest workspace the staged path accepts (no K split).
 size_t prefill_min_workspace_bytes(int m, int rows, int k, bool a_f32);
+// epi (fp32 c with a workspace only): 0 c = r, 1 c += r, 2 c = silu(c) * r.
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
-                                  int wkind = 0);  // 0 GF4, 1 F16, 2 q8_0
+                                  int wkind = 0, int epi = 0);  // wkind 0 GF4, 1 F16, 2 q8_0
 // Planned launch; the workspace is required for F16 and q8_0 weights.
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
-                          void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                          void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                          int epi = 0);
 
 }  // namespace qw35

@@ -13,6 +13,15 @@
 //     fused gate/up/SwiGLU and the down projection added into the residual
 //     stream; then the head of encodeOutputHead, +Output.m:11-65), recorded
 //     once per (batch, logits mode) as a decode plan (hipGraph) and replayed;
+//   * eval_chunk: the projections of one prefill chunk in evalTokens' order
+//     (Qw35MetalRuntime.m:1227-1333: per layer the mixer input projections,
+//     the mixer output projection, ffn_gate / ffn_up / SwiGLU and ffn_down
+//     over the chunk's tokens through encodeMatvecBatch, +FFN.m:260-306; the
+//     head on the chunk's last token), recorded once per (tokens, logits
+//     mode).  Chunks of more than 8 tokens run the prefill matmul with fp32
+//     activations, the output projections adding into the residual stream and
+//     the up projection applying SwiGLU in its epilogue; up to 8 tokens run
+//     the decode GEMVs;
 //   * argmax / copy_logits / sync: wait for the last step and read back, as
 //     readArgmaxToken / copyLogits (+Output.m:71-92).
 // The runtime owns one non-blocking stream at default priority; it is a
@@ -61,7 +70,8 @@ struct DeviceScope {
 
 struct MixProj {
     qw35_hip_weight w;
-    uint32_t out;  // QW35_HIP_RT_* buffer it writes
+    qw35_hip_weight pf;  // the weight the prefill matmul takes (w, or its fp16 image)
+    uint32_t out;        // QW35_HIP_RT_* buffer it writes
 };
 
 struct Layer {
@@ -69,6 +79,7 @@ struct Layer {
     std::vector<MixProj> mix;  // attention: q, k, v; delta: qkv, gate, beta, alpha
     qw35_hip_weight out{};      // attn_output / ssm_out
     qw35_hip_weight gate{}, up{}, down{};
+    qw35_hip_weight out_pf{}, gate_pf{}, up_pf{}, down_pf{};  // prefill forms
 };
 
 struct Runtime {
@@ -77,6 +88,8 @@ struct Runtime {
     void* store = nullptr;
     qw35_hip_hparams h{};
     uint32_t vocab = 0, max_batch = 0;
+    uint32_t chunk = 0;     // most tokens of a prefill chunk (0: decode batches only)
+    uint32_t rows_cap = 0;  // rows of the activation buffers: max(max_batch, chunk)
     std::vector<Layer> layers;
     qw35_hip_weight head{};
     float* buf[QW35_HIP_RT_NBUF] = {};
@@ -85,7 +98,11 @@ struct Runtime {
     float* logit = nullptr;     // [max_batch] greedy-head logits
     void* am_ws = nullptr;      // greedy-head partials
     uint64_t am_ws_bytes = 0;
-    std::map<std::pair<uint32_t, int>, void*> plans;  // (n_batch, logits mode) -> decode plan
+    std::map<std::pair<uint32_t, int>, void*> plans;        // (n_batch, logits mode) -> decode plan
+    std::map<std::pair<uint32_t, int>, void*> chunk_plans;  // (tokens, logits mode) -> prefill chunk plan
+    std::vector<void*> images;  // fp16 prefill images of the k-quant projections
+    void* pf_ws = nullptr;      // prefill matmul workspace, shared by a chunk's launches
+    uint64_t pf_ws_bytes = 0;
     uint32_t last_batch = 0;
     int last_mode = -1;
 };
@@ -95,6 +112,9 @@ void runtime_free(Runtime* r) {
     DeviceScope dev(r->device);
     if (r->stream) (void)hipStreamSynchronize(r->stream);
     for (auto& kv : r->plans) qw35_hip_plan_destroy(kv.second);
+    for (auto& kv : r->chunk_plans) qw35_hip_plan_destroy(kv.second);
+    for (void* p : r->images) (void)hipFree(p);
+    if (r->pf_ws) (void)hipFree(r->pf_ws);
     for (float* p : r->buf)
         if (p) (void)hipFree(p);
     if (r->token) (void)hipFree(r->token);
@@ -136,7 +156,8 @@ bool resolve(Runtime* r, int il, const char* suffix, uint64_t rows, uint64_t k, 
     return true;
 }
 
-bool check_hparams(const qw35_hip_hparams& h, uint32_t vocab, uint32_t max_batch, char* err, uintptr_t err_len) {
+bool check_hparams(const qw35_hip_hparams& h, uint32_t vocab, uint32_t max_batch, uint32_t chunk, char* err,
+                   uintptr_t err_len) {
     if (h.transformer_layers == 0 || h.transformer_layers > 4096 || h.embedding_length == 0 ||
         h.feed_forward_length == 0) {
         rt_err(err, err_len, "runtime_create: transformer_layers, embedding_length and feed_forward_length must be "
@@ -154,6 +175,10 @@ bool check_hparams(const qw35_hip_hparams& h, uint32_t vocab, uint32_t max_batch
     }
     if (max_batch < 1 || max_batch > QW35_HIP_MAX_BATCH) {
         rt_err(err, err_len, "runtime_create: max_batch=%u must be in 1..%u", max_batch, QW35_HIP_MAX_BATCH);
+        return false;
+    }
+    if (chunk > QW35_HIP_MAX_PREFILL_CHUNK) {
+        rt_err(err, err_len, "runtime_create: prefill_chunk=%u must be in 0..%u", chunk, QW35_HIP_MAX_PREFILL_CHUNK);
         return false;
     }
     return true;
@@ -196,6 +221,83 @@ std::vector<qw35_hip_plan_op> step_ops(const Runtime& r, uint32_t nb, int mode) 
     return ops;
 }
 
+// The head on the chunk's last token: one row of NORM.
+void head_op(const Runtime& r, std::vector<qw35_hip_plan_op>& ops, const float* x, int mode) {
+    qw35_hip_plan_op o{};
+    o.n_batch = 1;
+    o.w = &r.head;
+    o.x = x;
+    if (mode == QW35_HIP_LOGITS_FULL) {
+        o.kind = QW35_HIP_OP_MATVEC;
+        o.dst = r.buf[QW35_HIP_RT_LOGITS];
+        ops.push_back(o);
+    } else if (mode == QW35_HIP_LOGITS_ARGMAX) {
+        o.kind = QW35_HIP_OP_ARGMAX;
+        o.dst = r.logit;
+        o.token = r.token;
+        o.workspace = r.am_ws;
+        o.workspace_bytes = r.am_ws_bytes;
+        ops.push_back(o);
+    }
+}
+
+// A prefill chunk's ops for n tokens, in evalTokens' order: more than 8 tokens
+// on the prefill matmul (fp32 activations), else on the decode GEMVs.
+std::vector<qw35_hip_plan_op> chunk_ops(const Runtime& r, uint32_t n, int mode) {
+    std::vector<qw35_hip_plan_op> ops;
+    if (n <= QW35_HIP_MAX_BATCH) {
+        ops = step_ops(r, n, QW35_HIP_LOGITS_NONE);
+    } else {
+        auto op = [&](uint32_t kind, const qw35_hip_weight* w, const qw35_hip_weight* up, uint32_t in, uint32_t out,
+                      int residual) {
+            qw35_hip_plan_op o{};
+            o.kind = kind;
+            o.n_batch = n;
+            o.residual = residual;
+            o.w = w;
+            o.w_up = up;
+            o.x = r.buf[in];
+            o.dst = r.buf[out];
+            o.workspace = r.pf_ws;
+            o.workspace_bytes = r.pf_ws_bytes;
+            ops.push_back(o);
+        };
+        for (const Layer& l : r.layers) {
+            for (const MixProj& m : l.mix) op(QW35_HIP_OP_MATMUL, &m.pf, nullptr, QW35_HIP_RT_NORM, m.out, 0);
+            op(QW35_HIP_OP_MATMUL, &l.out_pf, nullptr, QW35_HIP_RT_CORE, QW35_HIP_RT_ACT, 1);
+            op(QW35_HIP_OP_MATMUL_SWIGLU, &l.gate_pf, &l.up_pf, QW35_HIP_RT_NORM, QW35_HIP_RT_FFN, 0);
+            op(QW35_HIP_OP_MATMUL, &l.down_pf, nullptr, QW35_HIP_RT_FFN, QW35_HIP_RT_ACT, 1);
+        }
+    }
+    head_op(r, ops, r.buf[QW35_HIP_RT_NORM] + (size_t)(n - 1) * r.h.embedding_length, mode);
+    return ops;
+}
+
+// The prefill matmul's weight for w: w itself (GF4, q8_0), else its fp16
+// image, made on the runtime's stream and owned by the runtime.
+bool prefill_form(Runtime* r, const qw35_hip_weight& w, qw35_hip_weight* pf, char* err, uintptr_t err_len) {
+    if (w.type_id == QW35_HIP_TYPE_GF4 || w.type_id == QW35_HIP_TYPE_Q8_0) {
+        *pf = w;
+        return true;
+    }
+    void* img = nullptr;
+    if (!rt_hip(hipMalloc(&img, (size_t)w.rows * w.k * 2), "runtime_create: prefill image", err, err_len))
+        return false;
+    try {
+        r->images.push_back(img);
+    } catch (...) {
+        (void)hipFree(img);
+        rt_err(err, err_len, "runtime_create: out of host memory");
+        return false;
+    }
+    if (!qw35_hip_dequantize_f16(&w, img, r->stream, err, err_len)) return false;
+    *pf = w;
+    pf->type_id = QW35_HIP_TYPE_F16;
+    pf->data = img;
+    pf->bytes = w.rows * w.k * 2;
+    return true;
+}
+
 bool wait(Runtime* r, const char* what, char* err, uintptr_t err_len) {
     hipError_t e = hipStreamSynchronize(r->stream);
     if (e == hipSuccess) e = hipGetLastError();
@@ -208,7 +310,7 @@ extern "C" {
 
 void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const qw35_hip_tensor_desc* tensors,
                               uintptr_t tensor_count, const qw35_hip_hparams* hparams, uint32_t vocab_size,
-                              uint32_t max_batch, char* err, uintptr_t err_len) {
+                              uint32_t max_batch, uint32_t prefill_chunk, char* err, uintptr_t err_len) {
     if (!model_map || !model_size || !tensors || !tensor_count || !hparams) {
         rt_err(err, err_len, "runtime_create: invalid runtime creation inputs");
         return nullptr;
@@ -218,7 +320,7 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
         return nullptr;
     }
     const qw35_hip_hparams& h = *hparams;
-    if (!check_hparams(h, vocab_size, max_batch, err, err_len)) return nullptr;
+    if (!check_hparams(h, vocab_size, max_batch, prefill_chunk, err, err_len)) return nullptr;
     Runtime* r = new (std::nothrow) Runtime();
     if (!r) {
         rt_err(err, err_len, "runtime_create: out of host memory");
@@ -227,6 +329,8 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
     r->h = h;
     r->vocab = vocab_size;
     r->max_batch = max_batch;
+    r->chunk = prefill_chunk;
+    r->rows_cap = std::max(max_batch, prefill_chunk);
     if (!rt_hip(hipGetDevice(&r->device), "runtime_create: device", err, err_len) ||
         !rt_hip(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking), "runtime_create: stream", err, err_len)) {
         runtime_free(r);
@@ -304,7 +408,57 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
         return nullptr;
     }
 
-    // Buffers: [max_batch][width] fp32, zeroed.
+    // Prefill forms and the workspace of chunks of more than 8 tokens: the
+    // largest any projection's planned launch uses at any chunk length.
+    if (prefill_chunk > QW35_HIP_MAX_BATCH) {
+        std::vector<const qw35_hip_weight*> pfs;
+        try {
+            for (Layer& l : r->layers) {
+                for (MixProj& m : l.mix) {
+                    if (!prefill_form(r, m.w, &m.pf, err, err_len)) {
+                        runtime_free(r);
+                        return nullptr;
+                    }
+                    pfs.push_back(&m.pf);
+                }
+                if (!prefill_form(r, l.out, &l.out_pf, err, err_len) ||
+                    !prefill_form(r, l.gate, &l.gate_pf, err, err_len) ||
+                    !prefill_form(r, l.up, &l.up_pf, err, err_len) ||
+                    !prefill_form(r, l.down, &l.down_pf, err, err_len)) {
+                    runtime_free(r);
+                    return nullptr;
+                }
+                pfs.insert(pfs.end(), {&l.out_pf, &l.gate_pf, &l.down_pf});
+            }
+        } catch (...) {
+            rt_err(err, err_len, "runtime_create: out of host memory");
+            runtime_free(r);
+            return nullptr;
+        }
+        std::vector<std::pair<uint32_t, std::pair<uint64_t, uint64_t>>> shapes;  // distinct (type, rows, k)
+        for (const qw35_hip_weight* w : pfs) {
+            const auto key = std::make_pair(w->type_id, std::make_pair(w->rows, w->k));
+            if (std::find(shapes.begin(), shapes.end(), key) != shapes.end()) continue;
+            shapes.push_back(key);
+            for (uint32_t n = QW35_HIP_MAX_BATCH + 1; n <= prefill_chunk; ++n) {
+                const uint64_t b = qw35_hip_matmul_prefill_workspace_size(w, n);
+                if (b == 0) {
+                    rt_err(err, err_len, "runtime_create: a %llu x %llu projection of type %u has no prefill form",
+                           (unsigned long long)w->rows, (unsigned long long)w->k, w->type_id);
+                    runtime_free(r);
+                    return nullptr;
+                }
+                r->pf_ws_bytes = std::max(r->pf_ws_bytes, b);
+            }
+        }
+        if (!rt_hip(hipMalloc(&r->pf_ws, r->pf_ws_bytes), "runtime_create: prefill workspace", err, err_len) ||
+            !rt_hip(hipStreamSynchronize(r->stream), "runtime_create: prefill images", err, err_len)) {
+            runtime_free(r);
+            return nullptr;
+        }
+    }
+
+    // Buffers: rows_cap rows of fp32, zeroed (the logits: max_batch rows).
     r->width[QW35_HIP_RT_NORM] = emb;
     r->width[QW35_HIP_RT_CORE] = std::max(any_attn ? attn_out_k : 0, any_delta ? inner : 0);
     r->width[QW35_HIP_RT_ACT] = emb;
@@ -318,7 +472,8 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
     r->width[QW35_HIP_RT_LOGITS] = vocab_size;
     for (uint32_t b = 0; b < QW35_HIP_RT_NBUF; ++b) {
         if (!r->width[b]) continue;
-        const size_t bytes = (size_t)max_batch * r->width[b] * sizeof(float);
+        const size_t rows = b == QW35_HIP_RT_LOGITS ? max_batch : r->rows_cap;
+        const size_t bytes = rows * r->width[b] * sizeof(float);
         if (!rt_hip(hipMalloc(&r->buf[b], bytes), "runtime_create: buffer", err, err_len) ||
             !rt_hip(hipMemset(r->buf[b], 0, bytes), "runtime_create: buffer", err, err_len)) {
             runtime_free(r);
@@ -329,7 +484,8 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
         r->am_ws_bytes = std::max(r->am_ws_bytes, qw35_hip_output_argmax_workspace_size(&r->head, nb));
     if (!rt_hip(hipMalloc(&r->token, max_batch * sizeof(uint32_t)), "runtime_create: head", err, err_len) ||
         !rt_hip(hipMalloc(&r->logit, max_batch * sizeof(float)), "runtime_create: head", err, err_len) ||
-        !rt_hip(hipMalloc(&r->am_ws, r->am_ws_bytes), "runtime_create: head workspace", err, err_len)) {
+        !rt_hip(hipMalloc(&r->am_ws, r->am_ws_bytes), "runtime_create: head workspace", err, err_len) ||
+        !rt_hip(hipDeviceSynchronize(), "runtime_create: buffers", err, err_len)) {
         runtime_free(r);
         return nullptr;
     }
@@ -381,6 +537,54 @@ int qw35_hip_runtime_eval_step(void* runtime, uint32_t n_batch, int logits_mode,
     }
     if (!qw35_hip_plan_launch(plan, r->stream, err, err_len)) return 0;
     r->last_batch = n_batch;
+    r->last_mode = logits_mode;
+    return 1;
+}
+
+int qw35_hip_runtime_eval_chunk(void* runtime, uint32_t n_tokens, int logits_mode, char* err, uintptr_t err_len) {
+    Runtime* r = static_cast<Runtime*>(runtime);
+    if (!r) {
+        rt_err(err, err_len, "runtime_eval_chunk: invalid runtime");
+        return 0;
+    }
+    if (n_tokens < 1 || n_tokens > r->rows_cap) {
+        rt_err(err, err_len, "runtime_eval_chunk: n_tokens=%u must be in 1..%u (max(max_batch, prefill_chunk))",
+               n_tokens, r->rows_cap);
+        return 0;
+    }
+    if (logits_mode != QW35_HIP_LOGITS_NONE && logits_mode != QW35_HIP_LOGITS_ARGMAX &&
+        logits_mode != QW35_HIP_LOGITS_FULL) {
+        rt_err(err, err_len, "runtime_eval_chunk: unknown logits mode %d", logits_mode);
+        return 0;
+    }
+    DeviceScope dev(r->device);
+    if (!dev.ok) {
+        rt_err(err, err_len, "runtime_eval_chunk: cannot make device %d current", r->device);
+        return 0;
+    }
+    const auto key = std::make_pair(n_tokens, logits_mode);
+    auto it = r->chunk_plans.find(key);
+    void* plan = it == r->chunk_plans.end() ? nullptr : it->second;
+    if (!plan) {
+        std::vector<qw35_hip_plan_op> ops;
+        try {
+            ops = chunk_ops(*r, n_tokens, logits_mode);
+        } catch (...) {
+            rt_err(err, err_len, "runtime_eval_chunk: out of host memory");
+            return 0;
+        }
+        plan = qw35_hip_plan_create(ops.data(), (uint32_t)ops.size(), err, err_len);
+        if (!plan) return 0;
+        try {
+            r->chunk_plans[key] = plan;
+        } catch (...) {
+            qw35_hip_plan_destroy(plan);
+            rt_err(err, err_len, "runtime_eval_chunk: out of host memory");
+            return 0;
+        }
+    }
+    if (!qw35_hip_plan_launch(plan, r->stream, err, err_len)) return 0;
+    r->last_batch = 1;  // the head ran on the chunk's last token
     r->last_mode = logits_mode;
     return 1;
 }

@@ -345,7 +345,8 @@ def prefill_workspace(w: HipWeight, n_tokens: int, device="cuda") -> torch.Tenso
 
 def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = None,
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
-                   workspace: torch.Tensor | None | bool = True, stream=None) -> torch.Tensor:
+                   workspace: torch.Tensor | None | bool = True, stream=None,
+                   epilogue: int = _ffi.EPILOGUE_STORE) -> torch.Tensor:
     """``C[t] = (awq * a[t]) @ W^T`` for a GF4, q8_0 or F16 weight
     (``encodeTiledKMatmul``; the other k-quants enter as their fp16 image,
     ``w.prefill``).  q8_0 and F16 need a workspace.
@@ -357,6 +358,9 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
     activations, no AWQ).  With a workspace fp32 activations keep fp32
     precision (an fp16 hi/lo pair per activation) and bf16 ones are carried
     exactly (with AWQ: the product rounded once to fp16).
+    ``epilogue`` (fp32 ``dst`` given, workspace): ``_ffi.EPILOGUE_STORE``
+    (dst = r), ``EPILOGUE_ADD`` (dst += r) or ``EPILOGUE_SWIGLU``
+    (dst = silu(dst) * r), see ``qw35_hip_matmul_prefill_epilogue``.
     """
     if a.dim() != 2 or not a.is_cuda or not a.is_contiguous() or a.dtype not in (torch.bfloat16, torch.float32):
         raise Qw35Error("matmul_prefill: a must be a contiguous 2-D bf16/fp32 device tensor")
@@ -376,8 +380,8 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
     elif workspace is False:
         workspace = None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    _ffi.call("qw35_hip_matmul_prefill", C.byref(w.view), _ptr(a), a_dt, _ptr(awq), _ptr(dst), c_dt, n,
-              _ptr(workspace), ws_bytes, _stream(stream))
+    _ffi.call("qw35_hip_matmul_prefill_epilogue", C.byref(w.view), _ptr(a), a_dt, _ptr(awq), _ptr(dst), c_dt,
+              int(epilogue), n, _ptr(workspace), ws_bytes, _stream(stream))
     return dst
 
 
@@ -576,11 +580,13 @@ class ProjectionRuntime:
     Built from a GGUF image (host bytes or an mmap) and the hyper-parameters;
     ``write(which, x)`` fills an input buffer (``_ffi.RT_NORM`` / ``RT_CORE`` /
     ``RT_ACT``), ``eval_step(n_batch, mode)`` replays one decode step's
-    projections, and ``argmax()`` / ``copy_logits()`` / ``read(which, n_batch)``
-    wait and read back, as ``qw35_metal_runtime_argmax`` / ``copy_logits`` do.
+    projections, ``eval_chunk(n_tokens, mode)`` one prefill chunk's (the
+    projection part of ``qw35_metal_runtime_eval_tokens``), and ``argmax()`` /
+    ``copy_logits()`` / ``read(which, n)`` wait and read back, as
+    ``qw35_metal_runtime_argmax`` / ``copy_logits`` do.
     """
 
-    def __init__(self, image, hparams, vocab: int, max_batch: int = 1):
+    def __init__(self, image, hparams, vocab: int, max_batch: int = 1, prefill_chunk: int = 0):
         self._h = None
         tensors, _, (descs, n, keep) = gguf_parse(image)
         ptr, size, _ = _image_ptr(keep)
@@ -589,8 +595,10 @@ class ProjectionRuntime:
         self.hparams = hparams_struct(hparams)
         self.vocab = int(vocab)
         self.max_batch = int(max_batch)
+        self.prefill_chunk = int(prefill_chunk)
+        self.rows = max(self.max_batch, self.prefill_chunk)  # rows of the activation buffers
         self._h = C.c_void_p(_ffi.call("qw35_hip_runtime_create", ptr, size, descs, n, C.byref(self.hparams),
-                                       self.vocab, self.max_batch))
+                                       self.vocab, self.max_batch, self.prefill_chunk))
         self._hip = _hip_runtime()
         self.last_batch = 0
 
@@ -609,20 +617,25 @@ class ProjectionRuntime:
         if rc != 0:
             raise Qw35Error(f"hipMemcpy failed ({rc})")
 
+    def _rows_of(self, which: int) -> int:
+        return self.max_batch if which == _ffi.RT_LOGITS else self.rows
+
     def write(self, which: int, x: torch.Tensor) -> None:
-        """Copy fp32 [n_batch, width'] (contiguous, any device) into buffer ``which``."""
+        """Copy fp32 [n, width'] (contiguous, any device) into buffer ``which``:
+        n rows packed at the row length width' of the op that reads them."""
         torch.cuda.synchronize()
         self.sync()
         ptr, width = self.buffer(which)
-        if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() > width * self.max_batch or not ptr:
-            raise Qw35Error(f"write: fp32 contiguous data of at most {self.max_batch} x {width} floats")
+        cap = width * self._rows_of(which)
+        if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() > cap or not ptr:
+            raise Qw35Error(f"write: fp32 contiguous data of at most {cap} floats")
         self._copy(ptr, x.data_ptr(), x.numel() * 4)
 
     def read(self, which: int, n_floats: int) -> torch.Tensor:
         """The first ``n_floats`` of buffer ``which`` (after waiting), as a CPU tensor."""
         self.sync()
         ptr, width = self.buffer(which)
-        if n_floats > width * self.max_batch:
+        if n_floats > width * self._rows_of(which):
             raise Qw35Error("read: more floats than the buffer holds")
         out = torch.empty(n_floats, dtype=torch.float32)
         self._copy(out.data_ptr(), ptr, n_floats * 4)
@@ -631,6 +644,11 @@ class ProjectionRuntime:
     def eval_step(self, n_batch: int = 1, mode: int = _ffi.LOGITS_FULL) -> None:
         _ffi.call("qw35_hip_runtime_eval_step", self._h, n_batch, mode)
         self.last_batch = n_batch
+
+    def eval_chunk(self, n_tokens: int, mode: int = _ffi.LOGITS_FULL) -> None:
+        """One prefill chunk's projections over ``n_tokens`` rows; the head on the last token."""
+        _ffi.call("qw35_hip_runtime_eval_chunk", self._h, n_tokens, mode)
+        self.last_batch = 1
 
     def argmax(self) -> tuple[list[int], list[float]]:
         tok = (C.c_uint32 * self.last_batch)()

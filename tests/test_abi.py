@@ -94,17 +94,21 @@ def test_runtime_create_rejects_bad_inputs_without_a_device(lib):
     d = _ffi.TensorDesc()
     img = (C.c_uint8 * 64)()
     with pytest.raises(_ffi.Qw35Error, match="invalid runtime creation inputs"):
-        _ffi.call("qw35_hip_runtime_create", None, 64, C.byref(d), 1, C.byref(hp), 10, 1)
+        _ffi.call("qw35_hip_runtime_create", None, 64, C.byref(d), 1, C.byref(hp), 10, 1, 0)
     with pytest.raises(_ffi.Qw35Error, match="must be positive"):
-        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1)
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1, 0)
     hp.transformer_layers, hp.embedding_length, hp.feed_forward_length, hp.n_cls_out = 1, 256, 256, 2
     with pytest.raises(_ffi.Qw35Error, match="classification heads"):
-        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1)
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1, 0)
     hp.n_cls_out = 0
     with pytest.raises(_ffi.Qw35Error, match="max_batch=0"):
-        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 0)
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 0, 0)
+    with pytest.raises(_ffi.Qw35Error, match="prefill_chunk=4097"):
+        _ffi.call("qw35_hip_runtime_create", img, 64, C.byref(d), 1, C.byref(hp), 10, 1, _ffi.MAX_PREFILL_CHUNK + 1)
     with pytest.raises(_ffi.Qw35Error, match="invalid runtime"):
         _ffi.call("qw35_hip_runtime_eval_step", None, 1, 2)
+    with pytest.raises(_ffi.Qw35Error, match="invalid runtime"):
+        _ffi.call("qw35_hip_runtime_eval_chunk", None, 16, 2)
 
 
 def _weight(type_id=100, k=4096, rows=16, data=4096, nbytes=None):
