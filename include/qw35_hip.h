@@ -108,9 +108,10 @@ int qw35_hip_gguf_parse(const void *model_map, uint64_t model_size, qw35_hip_ten
  * image may be unmapped afterwards.  One store per model image and device is
  * shared, as the reference shares one store per mapped file between its
  * runtimes (Qw35MetalRuntime.m:42-80): a create over the same (model_map,
- * model_size, descriptor count) on the same device returns the existing
- * store with one more reference, and qw35_hip_store_destroy drops one; the
- * device copy is freed with the last.  The store is immutable after creation,
+ * model_size) on the same device with the same descriptors (every field and
+ * name equal) returns the existing store with one more reference, and
+ * qw35_hip_store_destroy drops one; the device copy is freed with the last.
+ * Other descriptors over the same image get a store of their own.  The store is immutable after creation,
  * so its users may be on different threads.  Sharing is keyed by the image's
  * address: an image must not be changed, or freed and replaced at the same
  * address, while a store over it is alive.  qw35_hip_store_weight gives the

@@ -291,6 +291,25 @@ int qw35_hip_gguf_parse(const void* model_map, uint64_t model_size, qw35_hip_ten
     return 1;
 }
 
+namespace {
+
+// The descriptors a store was made from, field for field (names by their bytes).
+bool same_descs(const Store* s, const qw35_hip_tensor_desc* descs, uint32_t count) {
+    if (s->count != count) return false;
+    for (uint32_t i = 0; i < count; ++i) {
+        const qw35_hip_tensor_desc& a = s->descs[i];
+        const qw35_hip_tensor_desc& b = descs[i];
+        const uintptr_t blen = b.name ? b.name_len : 0;
+        if (a.type_id != b.type_id || a.abs_offset != b.abs_offset || a.bytes != b.bytes ||
+            a.elements != b.elements || a.n_dims != b.n_dims || memcmp(a.dims, b.dims, sizeof a.dims) != 0 ||
+            s->names[i].size() != blen || (blen && memcmp(s->names[i].data(), b.name, blen) != 0))
+            return false;
+    }
+    return true;
+}
+
+}  // namespace
+
 void* qw35_hip_store_create(const void* model_map, uint64_t model_size, const qw35_hip_tensor_desc* descs,
                             uint32_t count, char* err, uintptr_t err_len) {
     if (!model_map || (!descs && count)) {
@@ -315,7 +334,9 @@ void* qw35_hip_store_create(const void* model_map, uint64_t model_size, const qw
     // Creation runs under the lock, so two first users of one image copy it once.
     std::lock_guard<std::mutex> lock(g_stores_mu);
     for (Store* o : g_stores) {
-        if (o->map == model_map && o->map_size == model_size && o->count == count && o->device == device) {
+        // shared only with the same image, device and descriptors; other
+        // descriptors over the same image get a store of their own
+        if (o->map == model_map && o->map_size == model_size && o->device == device && same_descs(o, descs, count)) {
             ++o->refs;
             return o;
         }

@@ -100,3 +100,28 @@ def check_prefill(out, a_host: np.ndarray, awq: np.ndarray | None, w_op: np.ndar
     ok, msg = bf16_out_ok(got_bits, want_op, op, w64)
     assert ok, msg
     return 0.0
+
+
+def pinned_rows(rows: int, edge: int = 1024, stride: int = 61) -> np.ndarray:
+    """Rows of a large weight whose dequantisation is pinned to the oracle: the
+    first and last ``edge`` rows and every ``stride``-th row."""
+    return np.unique(np.concatenate([np.arange(min(edge, rows)), np.arange(max(0, rows - edge), rows),
+                                     np.arange(0, rows, stride)])).astype(np.int64)
+
+
+def assert_dequant_pinned(w, rows: np.ndarray) -> None:
+    """The library's dequantisation of rows ``rows`` of the device weight ``w``
+    (qw35_hip_dequantize with a row gather) equals, bit for bit, the oracle's
+    dequantisation of the same rows' bytes."""
+    import torch
+
+    from qwowl35_amd import runtime as rt
+
+    dev = w.storage.device
+    ids = torch.from_numpy(rows.astype(np.int32)).to(dev)
+    got = rt.dequantize(w, ids).cpu().numpy()
+    rb = rt.row_bytes(w.type_id, w.k)
+    raw = w.storage[: w.rows * rb].view(w.rows, rb)[ids.long()].cpu().numpy().reshape(-1)
+    want = om.dequant(w.type_id, raw, len(rows), w.k)
+    bad = np.flatnonzero(np.any(got.view(np.uint32) != want.view(np.uint32), axis=1))
+    assert bad.size == 0, f"rows {rows[bad[:8]].tolist()} differ from the oracle"

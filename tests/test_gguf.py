@@ -169,3 +169,38 @@ def test_store_outlives_the_host_image(cuda, tmp_path):
     x = np.ones((1, k), np.float32)
     y = rt.decode_matvec(w, torch.from_numpy(x).to(cuda)).cpu().numpy()
     assert om.rel_l2(y, om.matvec_f64(deq, x)) <= GEMV_REL_L2
+
+
+@pytest.mark.gpu
+def test_store_shared_only_for_the_same_descriptors(cuda):
+    """Two creates over one image share a store only when every descriptor
+    matches: the same count with one tensor renamed gets a store of its own,
+    which serves the new name."""
+    import ctypes as C
+
+    from qwowl35_amd import _ffi
+
+    rt = _rt()
+    image, _, mats = _model(64)
+    _, _, (descs, n, keep) = rt.gguf_parse(np.frombuffer(image, np.uint8))
+    ptr, size, _ = rt._image_ptr(keep)
+    a = _ffi.call("qw35_hip_store_create", ptr, size, descs, n)
+    b = _ffi.call("qw35_hip_store_create", ptr, size, descs, n)
+    other = (_ffi.TensorDesc * n)()
+    C.memmove(other, descs, C.sizeof(other))
+    i = next(j for j in range(n) if C.string_at(descs[j].name, descs[j].name_len) == b"output.weight")
+    new_name = C.create_string_buffer(b"output.renamed")
+    other[i].name = C.cast(new_name, C.c_void_p).value
+    other[i].name_len = len(b"output.renamed")
+    c = _ffi.call("qw35_hip_store_create", ptr, size, other, n)
+    try:
+        assert a == b and c != a
+        w = _ffi.Weight()
+        _ffi.call("qw35_hip_store_weight", C.c_void_p(c), b"output.renamed", len(b"output.renamed"), C.byref(w))
+        assert (w.rows, w.k) == (mats["output.weight"][1], mats["output.weight"][2])
+        with pytest.raises(_ffi.Qw35Error, match="no tensor named output.renamed"):
+            _ffi.call("qw35_hip_store_weight", C.c_void_p(a), b"output.renamed", len(b"output.renamed"),
+                      C.byref(w))
+    finally:
+        for h in (a, b, c):
+            _ffi.load().qw35_hip_store_destroy(C.c_void_p(h))

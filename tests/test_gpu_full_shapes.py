@@ -265,6 +265,16 @@ def _deq64(w):
     return _rt().dequantize(w).double()
 
 
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "q6_k", "gf2"])
+def test_head_dequant_pinned_to_oracle(cuda, heads, name):
+    """The dequantisation the head checks use is the oracle's on these
+    65549-row weights: the first and last 1024 rows and every 61st row, bit
+    for bit against the oracle on the same bytes."""
+    from tests.helpers import assert_dequant_pinned, pinned_rows
+
+    assert_dequant_pinned(heads[name], pinned_rows(HEAD_ROWS))
+
+
 @pytest.mark.parametrize("nb", [1, 4, 8])
 @pytest.mark.parametrize("name", ["q8_0", "q4_k", "q5_k", "q6_k", "gf2"])
 def test_head_sized_gemv(cuda, heads, name, nb):

@@ -132,3 +132,25 @@ def test_stack9b_shared_buffers_match_distinct(cuda, stack9b):
     for a, b in zip(*res):
         assert torch.equal(a, b)
 
+
+
+def test_stack9b_dequant_pinned_to_oracle(cuda, stack9b):
+    """The dequantisation the checks above use is the oracle's at the stack's
+    real shapes: for the 248320-row Q4_K head and one weight of every other
+    shape (q8_0 mixers, GF4 gate / up / down), the first and last 1024 rows
+    and every 61st row, bit for bit against the oracle on the same bytes."""
+    from tests.helpers import assert_dequant_pinned, pinned_rows
+
+    seen = set()
+    for il, layer in enumerate(stack9b.layers):
+        for name, w in layer.items():
+            key = (w.type_id, w.rows, w.k)
+            if key in seen:
+                continue
+            seen.add(key)
+            print(f"dequant pin blk.{il}.{name} {w.rows}x{w.k}", flush=True)
+            assert_dequant_pinned(w, pinned_rows(w.rows))
+    want = {(w.type_id, w.rows, w.k) for layer in stack9b.layers for w in layer.values()}
+    assert seen == want and len(want) == 6  # q8_0 8192 / 4096 / 32 / 1024 rows x 4096; GF4 gate/up and down
+    print("dequant pin output.weight", flush=True)
+    assert_dequant_pinned(stack9b.head, pinned_rows(stack9b.head.rows))
