@@ -550,7 +550,45 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
     return out
 
 
-def bench_stack(b: Bench, cpu_rates: dict | None) -> dict:
+def cpu_stack_us(cpu: CpuBaseline, stack, m: int, head: bool) -> tuple[float, str]:
+    """CPU time (us) of one step of the stack's projections over m tokens:
+    every projection of one DeltaNet layer and one attention layer timed at
+    full size (oracle dequantisation + fp32 BLAS, median of the CpuBaseline's
+    runs) and scaled by the layer counts, plus the head on one token timed on
+    1/8 of its rows and scaled by 8."""
+    from qwowl35_amd import qwen35
+
+    hp = stack.hp
+    kinds = {}
+    for il in range(hp.transformer_layers):
+        kinds.setdefault(qwen35.is_attention_layer(hp, il), il)
+    total, parts = 0.0, []
+    for attn, il in kinds.items():
+        n_layers = sum(1 for j in range(hp.transformer_layers) if qwen35.is_attention_layer(hp, j) == attn)
+        t = 0.0
+        for p in qwen35.mixer_projections(hp, il) + qwen35.ffn_projections(hp):
+            w = stack.layers[il][p.name]
+            t_dq, t_mm = (cpu.matmul if m > 1 else cpu.gemv)(w.type_id, host_bytes(w), w.rows, w.k, m)
+            t += t_dq + t_mm
+        total += n_layers * t
+        parts.append(f"{'attention' if attn else 'DeltaNet'} layer {t * 1e3:.0f} ms x {n_layers}")
+    if head:
+        rows = hp.vocab // 8
+        w = stack.head
+        raw = host_bytes(w)[: rows * b_rt().row_bytes(w.type_id, w.k)]
+        t_dq, t_mv = cpu.gemv(w.type_id, raw, rows, w.k, 1)
+        total += 8 * (t_dq + t_mv)
+        parts.append(f"head {8e3 * (t_dq + t_mv):.0f} ms (1/8 of the rows x 8)")
+    return total * 1e6, ", ".join(parts)
+
+
+def b_rt():
+    from qwowl35_amd import runtime
+
+    return runtime
+
+
+def bench_stack(b: Bench, cpu: CpuBaseline | None) -> dict:
     """Config 5: the 32-layer Qwen3.5-9B decode-step projection stack as one
     recorded plan (hipGraph), in the reference's dispatch order: per layer the
     q8_0 mixer input projections (merged into one launch), the q8_0 output
@@ -558,7 +596,10 @@ def bench_stack(b: Bench, cpu_rates: dict | None) -> dict:
     projection (+= residual); then the Q4_K LM head.  The runtime's buffer
     sharing (one output buffer per role, no AWQ: the reference folds it into
     the norms) -- the same plan qw35_hip_runtime_eval_step records.  Every layer
-    has its own weight buffers (5.2 GB per step)."""
+    has its own weight buffers (5.2 GB per step).  Then one prefill chunk of
+    128 tokens (the reference server's default chunk) over the same stack, as
+    qw35_hip_runtime_eval_chunk records it: fp32 activations on the prefill
+    matmul, the head on the last token."""
     from qwowl35_amd import qwen35
 
     hp = qwen35.QWEN35_9B
@@ -572,24 +613,32 @@ def bench_stack(b: Bench, cpu_rates: dict | None) -> dict:
         us = b.time_plan(plan, 20) * 1e3
         line = {"gemvs": len(plan), "weight_bytes": int(total), "us_per_step": round(us, 1),
                 "us_per_token": round(us / nb, 1), "roofline": hbm_roofline(total, us)}
-        if cpu_rates is not None:
-            cpu_us = 0.0
-            for il in range(hp.transformer_layers):
-                for p in qwen35.mixer_projections(hp, il):
-                    cpu_us += p.rows * b.rt.row_bytes(stack.types.mixer, p.k) / cpu_rates["q8_0"]
-                for p in qwen35.ffn_projections(hp):
-                    cpu_us += p.rows * b.rt.row_bytes(stack.types.ffn, p.k) / cpu_rates["gf4"]
-            cpu_us += hp.vocab * b.rt.row_bytes(stack.types.head, hp.embedding_length) / cpu_rates["q4_k"]
-            cpu_us *= 1e6
-            line["cpu_baseline"] = {
-                "value": round(cpu_us / nb, 1), "unit": "us/token", "cores": cpu_rates["threads"], "kind": "port",
-                "sample": "the sum over the 217 projections of their weight bytes at the per-codec CPU rates "
-                          f"measured in this run at batch {cpu_rates['nb']} (GF4 {cpu_rates['gf4'] / 1e9:.3f}, q8_0 "
-                          f"{cpu_rates['q8_0'] / 1e9:.3f}, Q4_K {cpu_rates['q4_k'] / 1e9:.3f} GB/s), divided by the "
-                          f"batch; {cpu_model()}"}
+        if cpu is not None:
+            cpu_us, how = cpu_stack_us(cpu, stack, nb, head=True)
+            line["cpu_baseline"] = cpu.record(round(cpu_us / nb, 1), "us/token",
+                                              f"9B projection stack at batch {nb}, timed per projection: {how}; "
+                                              f"divided by the batch")
         out[f"decode_stack_9b_b{nb}"] = line
         plan.close()
-    del stack
+        del bufs
+    n = 128
+    bufs = qwen35.StepBuffers.make(hp, n, b.gen, awq=False, shared_outputs=True)
+    bufs.ffn_norm = bufs.norm
+    ws = qwen35.chunk_workspace(stack, n)
+    plan = qwen35.build_chunk_plan(stack, bufs, ws)
+    us = b.time_plan(plan, 5) * 1e3
+    flops = qwen35.chunk_flops(hp, n)
+    line = {"n_tokens": n, "ops": len(plan), "us_per_chunk": round(us, 1), "us_per_token": round(us / n, 2),
+            "tokens_per_s": round(n / us * 1e6, 1), "flops": flops,
+            "roofline": mfma_roofline(flops, us, "gf4_prefill_f16_kernel (GF4 / q8_0 weights, fp32 activations)")}
+    if cpu is not None:
+        cpu_us, how = cpu_stack_us(cpu, stack, n, head=True)
+        line["cpu_baseline"] = cpu.record(round(cpu_us / n, 1), "us/token",
+                                          f"9B projection stack over a 128-token chunk, timed per projection: {how}; "
+                                          f"divided by the tokens")
+    out["prefill_chunk_9b_m128"] = line
+    plan.close()
+    del stack, bufs, ws
     return out
 
 
@@ -645,13 +694,11 @@ def main() -> int:
         {"gf4", "q8", "q4k", "q6k", "prefill", "stack"} if args.extras == "all" else set(args.extras.split(",")))
 
     cpu_line = None
-    cpu_rates = None
     if cpu is not None:
         t_dq, t_mv = cpu.gemv(rt.TYPE_GF4, host_bytes(weights[0]), rows, k, 1)
         cpu_line = cpu.record(round(algo / (t_dq + t_mv) / 1e9, 3), "GB/s",
                               f"GF4 12288x4096 b1 at full size: dequant {t_dq * 1e3:.1f} ms + matvec "
                               f"{t_mv * 1e3:.2f} ms per call")
-        cpu_rates = {"gf4": algo / (t_dq + t_mv), "threads": cpu.threads, "nb": 1}
     if "gf4" in want:
         extra.update(bench_gf4_extra(b, weights, cpu, args.steps, args.warmup))
     del weights
@@ -666,12 +713,7 @@ def main() -> int:
     if "prefill" in want:
         extra.update(bench_prefill(b, cpu))
     if "stack" in want:
-        if cpu_rates is not None and "q8_0_layer_set_b1" in extra and "q4_k_head_b1_248320x4096" in extra:
-            cpu_rates["q8_0"] = extra["q8_0_layer_set_b1"]["cpu_baseline"]["value"] * 1e9
-            cpu_rates["q4_k"] = extra["q4_k_head_b1_248320x4096"]["cpu_baseline"]["value"] * 1e9
-        else:
-            cpu_rates = None
-        extra.update(bench_stack(b, cpu_rates))
+        extra.update(bench_stack(b, cpu))
     for key, v in extra.items():
         log(f"{key}: {v}")
 

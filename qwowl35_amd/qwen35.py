@@ -272,6 +272,51 @@ def build_plan(stack: ProjectionStack, bufs: StepBuffers, head: bool = True) -> 
     return plan.record()
 
 
+def chunk_workspace(stack: ProjectionStack, n_tokens: int, device=None) -> torch.Tensor:
+    """A prefill workspace that holds every projection's planned launch at n_tokens
+    (fp32 activations), as the projection runtime sizes its own."""
+    import ctypes as C
+
+    from . import _ffi
+
+    lib = _ffi.load()
+    size = max(int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(w.prefill.view), n_tokens))
+               for ws in stack.layers for w in ws.values())
+    return torch.empty(size, dtype=torch.uint8, device=device or stack.head.storage.device)
+
+
+def build_chunk_plan(stack: ProjectionStack, bufs: StepBuffers, workspace: torch.Tensor,
+                     head: bool = True) -> rt.DecodePlan:
+    """Record one prefill chunk's projections (the projection part of
+    ``evalTokens``, Qw35MetalRuntime.m:1227-1333) over the n rows of ``bufs``
+    (fp32 activations, n > 8): per layer the mixer input projections, the
+    output projection added into ``act``, gate/up/SwiGLU (the up projection's
+    SwiGLU epilogue) and the down projection added into ``act``, all on the
+    prefill matmul; then the head on the last token's norm row as a GEMV into
+    ``logits[0]`` -- the sequence ``qw35_hip_runtime_eval_chunk`` records."""
+    hp = stack.hp
+    plan = rt.DecodePlan()
+    for il, ws in enumerate(stack.layers):
+        mix = mixer_projections(hp, il)
+        for p in mix[:-1]:
+            plan.matmul(ws[p.name], bufs.norm, bufs.mixer_out[il][p.name], workspace)
+        out = mix[-1]
+        plan.matmul(ws[out.name], bufs.core[out.k], bufs.act, workspace, residual=True)
+        plan.matmul_swiglu(ws["ffn_gate"], ws["ffn_up"], bufs.ffn_norm, bufs.ffn_act[il], workspace, awq=bufs.awq)
+        plan.matmul(ws["ffn_down"], bufs.ffn_act[il], bufs.act, workspace, residual=True)
+    if head:
+        n = bufs.norm.shape[0]
+        plan.matvec(stack.head, bufs.norm[n - 1:n], bufs.logits[0:1])
+    return plan.record()
+
+
+def chunk_flops(hp: Hparams, n_tokens: int) -> float:
+    """Multiply-add flops of a chunk's projections (2 n rows k per projection; the head not counted)."""
+    per_token = sum(p.rows * p.k for il in range(hp.transformer_layers) for p in mixer_projections(hp, il))
+    per_token += hp.transformer_layers * sum(p.rows * p.k for p in ffn_projections(hp))
+    return 2.0 * n_tokens * per_token
+
+
 def gemv_count(hp: Hparams, head: bool = True) -> int:
     """GEMVs of one step as the reference dispatches them (fused gate/up counts once)."""
     n = sum(len(mixer_projections(hp, il)) + 2 for il in range(hp.transformer_layers))

@@ -510,6 +510,43 @@ class DecodePlan:
         self._keep.extend([token, workspace])
         return self
 
+    def matmul(self, w: HipWeight, x: torch.Tensor, dst: torch.Tensor, workspace: torch.Tensor,
+               residual: bool = False, awq: torch.Tensor | None = None) -> "DecodePlan":
+        """A prefill-chunk op: ``dst (+)= (awq * x) @ W^T`` for fp32 ``x`` [n_tokens, k]
+        on the prefill matmul (``w.prefill``), through ``workspace`` (ops may share one)."""
+        n = self._check_chunk(w.prefill, x, dst, awq, workspace)
+        self._add(_ffi.OP_MATMUL, n, residual, w.prefill, None, x, awq, dst)
+        self._set_ws(workspace)
+        return self
+
+    def matmul_swiglu(self, gate: HipWeight, up: HipWeight, x: torch.Tensor, dst: torch.Tensor,
+                      workspace: torch.Tensor, awq: torch.Tensor | None = None) -> "DecodePlan":
+        """``dst = silu((awq*x) @ Wg^T) * ((awq*x) @ Wu^T)`` over a chunk: two prefill
+        matmul launches, the second applying SwiGLU in its epilogue."""
+        n = self._check_chunk(gate.prefill, x, dst, awq, workspace)
+        self._add(_ffi.OP_MATMUL_SWIGLU, n, False, gate.prefill, up.prefill, x, awq, dst)
+        self._set_ws(workspace)
+        return self
+
+    def _check_chunk(self, w, x, dst, awq, workspace) -> int:
+        if x.dim() != 2 or x.dtype != torch.float32 or not x.is_contiguous() or x.shape[1] != w.k:
+            raise Qw35Error(f"chunk op: x must be a contiguous fp32 [n_tokens, {w.k}] tensor")
+        _check_awq(awq, w.k, x)
+        n = int(x.shape[0])
+        if dst.dtype != torch.float32 or not dst.is_contiguous() or dst.numel() < n * w.rows:
+            raise Qw35Error(f"chunk op: dst must be a contiguous fp32 tensor of >= {n} x {w.rows} values")
+        if workspace is None or workspace.dtype != torch.uint8 or not workspace.is_cuda:
+            raise Qw35Error("chunk op: a uint8 device workspace (prefill_workspace) is required")
+        return n
+
+    def _set_ws(self, workspace: torch.Tensor) -> None:
+        base = workspace.data_ptr()
+        pad = (-base) % 256
+        op = self._ops[-1]
+        op.workspace = base + pad
+        op.workspace_bytes = workspace.numel() - pad
+        self._keep.append(workspace)
+
     def _add(self, kind, nb, residual, w, up, x, awq, dst):
         if self._handle is not None:
             raise Qw35Error("plan already recorded")
