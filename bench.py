@@ -190,9 +190,10 @@ def gemv_line(b: Bench, weights, nb, launches, warmup, awq=None) -> dict:
     y = b.torch.zeros((nb, w0.rows), dtype=b.torch.float32, device=b.dev)
     ws = rt.decode_matvec_workspace(w0, nb, device=b.dev)
     ms, _ = b.time_launches(gemv_calls(rt, weights, x, y, awq, ws), launches, warmup)
-    kern = rt.gemv_kernel(w0, nb, awq=awq is not None, workspace=ws is not None)["name"]
+    kern = rt.gemv_kernel(w0, nb, awq=awq is not None, workspace=ws is not None)
     nbytes = gemv_bytes(rt, w0.type_id, w0.rows, w0.k, nb)
-    return {"us": round(ms * 1e3, 3), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms * 1e3, kern)}
+    return {"us": round(ms * 1e3, 3), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms * 1e3, kern["name"]),
+            "launch": {"grid": kern["grid"], "block": kern["block"]}}
 
 
 def stream_ceiling(b: Bench, bufs) -> dict:
@@ -476,7 +477,8 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
 
     def line(ms, m, rows, k, kern):
         flops = 2.0 * m * rows * k
-        r = {"us": round(ms * 1e3, 2), "roofline": mfma_roofline(flops, ms * 1e3, kern)}
+        r = {"us": round(ms * 1e3, 2), "flops": flops, "roofline": mfma_roofline(flops, ms * 1e3, kern["name"]),
+             "launch": {"grid": kern["grid"], "block": kern["block"], "splits": kern["splits"]}}
         r["frac_of_probe"] = round(flops / (ms * 1e-3) / 1e12 / ceiling, 4)
         return r
 
@@ -499,7 +501,7 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
             calls = [lambda s, w=w: rt.matmul_prefill(w, a, awq=awq, out_dtype=c_dt, dst=c, workspace=wsp, stream=s)
                      for w in ws]
             ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
-            kern = "gf4_prefill_f16_kernel" + (" (fp32 activations, hi/lo)" if tag else "")
+            kern = rt.prefill_kernel(ws[0], m, a_dt, awq=True, out_dtype=c_dt)
             out[f"prefill_gf4{tag}_m{m}_{rows}x{k}"] = with_cpu(line(ms, m, rows, k, kern), rt.TYPE_GF4, ws[0],
                                                                 rows, k, m, "GF4")
         del ws
@@ -518,7 +520,7 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
                 wsp = rt.prefill_workspace(wl[0], m, device=b.dev)
                 calls = [lambda s, w=w, wsp=wsp: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in wl]
                 ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
-                r = line(ms, m, rows, k, "gf4_prefill_f16_kernel" + (" (F16 weights)" if tag else " (q8_0 weights)"))
+                r = line(ms, m, rows, k, rt.prefill_kernel(wl[0], m))
                 if not tag:
                     r = with_cpu(r, rt.TYPE_Q8_0, q8[0], rows, k, m, "q8_0")
                 out[f"prefill_q8_0{tag}_m{m}_{rows}x{k}"] = r

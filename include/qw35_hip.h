@@ -488,6 +488,19 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_
  * epilogue is applied once, to the sum of the splits.  The reference runs
  * ffn_gate and ffn_up as two tiled matmuls and SwiGLU as a third dispatch
  * (Qw35MetalRuntime.m:1298-1301); here the third is the up matmul's epilogue. */
+/* The matmul kernel a qw35_hip_matmul_prefill(_epilogue) call with this
+ * weight, token count, activation and output type and AWQ presence launches
+ * -- with a workspace of the planned size when with_workspace != 0 (the
+ * staged path; its staging pass, prefill_stage_kernel, and a split's
+ * reduction, prefill_split_reduce, run beside it), else the path without
+ * one -- named as the profiler names it (e.g.
+ * "gf4_prefill_f16_kernel<64, 8, 1, 2, false, false, false, 4>"), with its
+ * grid, workgroup size, LDS bytes and K splits; nothing is launched.  No
+ * counterpart in the reference: it matches measurements and tests to the
+ * launch plan. */
+int qw35_hip_prefill_kernel(const qw35_hip_weight *w, uint32_t n_tokens, uint32_t a_dtype, int has_awq,
+                            uint32_t c_dtype, int with_workspace, char *name, uintptr_t name_len, uint32_t *grid,
+                            uint32_t *block, uint32_t *lds_bytes, uint32_t *splits, char *err, uintptr_t err_len);
 #define QW35_HIP_EPILOGUE_STORE 0u
 #define QW35_HIP_EPILOGUE_ADD 1u
 #define QW35_HIP_EPILOGUE_SWIGLU 2u

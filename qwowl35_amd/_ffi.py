@@ -201,6 +201,12 @@ PROTOTYPES: dict[str, tuple] = {
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
          C.c_uint64, C.c_void_p, C.c_char_p, C.c_size_t],
     ),
+    "qw35_hip_prefill_kernel": (
+        C.c_int,
+        [C.POINTER(Weight), C.c_uint32, C.c_uint32, C.c_int, C.c_uint32, C.c_int, C.c_char_p, C.c_size_t,
+         C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_char_p,
+         C.c_size_t],
+    ),
     "qw35_hip_matmul_prefill_epilogue": (
         C.c_int,
         [C.POINTER(Weight), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,

@@ -210,6 +210,19 @@ bool mergeable(const qw35_hip_plan_op& a, const qw35_hip_plan_op& b) {
     return !overlaps(a.dst, da, b.dst, db) && !overlaps(a.x, xa, a.dst, da) && !overlaps(a.x, xa, b.dst, db);
 }
 
+// What a prefill launch staged into its workspace: the activations, AWQ,
+// token count, k and column order (GF4 words take their own order).
+struct StageKey {
+    const float* x = nullptr;
+    const float* awq = nullptr;
+    const void* ws = nullptr;
+    uint32_t n = 0, k = 0;
+    bool gf4_order = false;
+    bool operator==(const StageKey& o) const {
+        return x == o.x && awq == o.awq && ws == o.ws && n == o.n && k == o.k && gf4_order == o.gf4_order;
+    }
+};
+
 // Weight form of the prefill kernel: 0 GF4 words, 1 F16, 2 q8_0 blocks; -1 none.
 int prefill_wkind(uint32_t type_id) {
     return type_id == qw35::kTypeGF4 ? 0 : type_id == qw35::kTypeF16 ? 1 : type_id == qw35::kTypeQ8_0 ? 2 : -1;
@@ -478,15 +491,28 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
             }
         }
         qw35::LaunchInfo info{};
+        StageKey stage_key{};
+        bool stage_valid = false;
         for (uint32_t i = 0; i < n_ops && launch == hipSuccess;) {
             const qw35_hip_plan_op& o = ops[i];
             if (o.kind == QW35_HIP_OP_MATMUL || o.kind == QW35_HIP_OP_MATMUL_SWIGLU) {
                 if (pass == 1) {
                     const bool sw = o.kind == QW35_HIP_OP_MATMUL_SWIGLU;
                     auto mm = [&](const qw35_hip_weight* w, uint32_t epi) {
-                        return qw35::launch_prefill(prefill_wkind(w->type_id), w->data, (int)w->rows, (int)w->k, o.x,
-                                                    1, o.awq, o.dst, (int)o.n_batch, 1, o.workspace,
-                                                    o.workspace_bytes, s, (int)epi);
+                        // The staging pass is skipped when the previous prefill launch
+                        // of the plan staged the same activations the same way into
+                        // the same workspace, and nothing written since overlaps them.
+                        const int wkind = prefill_wkind(w->type_id);
+                        const StageKey key{o.x, o.awq, o.workspace, o.n_batch, (uint32_t)w->k, wkind == 0};
+                        const bool staged = stage_valid && key == stage_key;
+                        const hipError_t e = qw35::launch_prefill(wkind, w->data, (int)w->rows, (int)w->k, o.x, 1,
+                                                                  o.awq, o.dst, (int)o.n_batch, 1, o.workspace,
+                                                                  o.workspace_bytes, s, (int)epi, nullptr, staged);
+                        stage_key = key;
+                        // this launch's output may be the next one's input
+                        const uint64_t xb = (uint64_t)o.n_batch * w->k * 4, db = (uint64_t)o.n_batch * w->rows * 4;
+                        stage_valid = !overlaps(o.dst, db, o.x, xb) && !(o.awq && overlaps(o.dst, db, o.awq, w->k * 4));
+                        return e;
                     };
                     launch = mm(o.w, sw          ? QW35_HIP_EPILOGUE_STORE
                                      : o.residual ? QW35_HIP_EPILOGUE_ADD
@@ -496,6 +522,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                 ++i;
                 continue;
             }
+            stage_valid = false;  // GEMV outputs are not tracked against the staged activations
             if (o.kind == QW35_HIP_OP_ARGMAX) {
                 qw35::GemvArgs a = gemv_args(o.w, nullptr, o.x, o.awq, nullptr, o.n_batch, 0);
                 a.am_token = static_cast<uint32_t*>(o.workspace);
@@ -628,9 +655,10 @@ int qw35_hip_matmul_prefill(const qw35_hip_weight* w, const void* a, uint32_t a_
                                             workspace, workspace_bytes, stream, err, err_len);
 }
 
-int qw35_hip_matmul_prefill_epilogue(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq,
-                                     void* c, uint32_t c_dtype, uint32_t epilogue, uint32_t n_tokens, void* workspace,
-                                     uint64_t workspace_bytes, void* stream, char* err, uintptr_t err_len) {
+// The checks of a prefill call, then its launch, or (info set) its description.
+static int prefill_call(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq, void* c,
+                        uint32_t c_dtype, uint32_t epilogue, uint32_t n_tokens, void* workspace,
+                        uint64_t workspace_bytes, void* stream, qw35::LaunchInfo* info, char* err, uintptr_t err_len) {
     if (!check_weight(w, "matmul_prefill", err, err_len) || !check_chunked_k(w, "matmul_prefill", err, err_len))
         return 0;
     if (epilogue > QW35_HIP_EPILOGUE_SWIGLU) {
@@ -697,10 +725,36 @@ int qw35_hip_matmul_prefill_epilogue(const qw35_hip_weight* w, const void* a, ui
     }
     return check_hip(qw35::launch_prefill(wkind, w->data, (int)w->rows, (int)w->k, a, a_f32, awq, c, (int)n_tokens,
                                           c_dtype == QW35_HIP_DTYPE_F32, workspace, workspace ? workspace_bytes : 0,
-                                          static_cast<hipStream_t>(stream), (int)epilogue),
+                                          static_cast<hipStream_t>(stream), (int)epilogue, info),
                      "matmul_prefill", err, err_len)
                ? 1
                : 0;
+}
+
+int qw35_hip_matmul_prefill_epilogue(const qw35_hip_weight* w, const void* a, uint32_t a_dtype, const float* awq,
+                                     void* c, uint32_t c_dtype, uint32_t epilogue, uint32_t n_tokens, void* workspace,
+                                     uint64_t workspace_bytes, void* stream, char* err, uintptr_t err_len) {
+    return prefill_call(w, a, a_dtype, awq, c, c_dtype, epilogue, n_tokens, workspace, workspace_bytes, stream,
+                        nullptr, err, err_len);
+}
+
+int qw35_hip_prefill_kernel(const qw35_hip_weight* w, uint32_t n_tokens, uint32_t a_dtype, int has_awq,
+                            uint32_t c_dtype, int with_workspace, char* name, uintptr_t name_len, uint32_t* grid,
+                            uint32_t* block, uint32_t* lds_bytes, uint32_t* splits, char* err, uintptr_t err_len) {
+    // Stand-in addresses for the validation: nothing is launched or read.
+    void* fake = reinterpret_cast<void*>(uintptr_t{256});
+    qw35::LaunchInfo info{};
+    info.splits = 1;
+    if (!prefill_call(w, fake, a_dtype, has_awq ? static_cast<const float*>(fake) : nullptr, fake, c_dtype,
+                      QW35_HIP_EPILOGUE_STORE, n_tokens, with_workspace ? fake : nullptr,
+                      with_workspace ? UINT64_MAX : 0, nullptr, &info, err, err_len))
+        return 0;
+    if (name && name_len) snprintf(name, (size_t)name_len, "%s", info.name);
+    if (grid) *grid = info.grid;
+    if (block) *block = info.block;
+    if (lds_bytes) *lds_bytes = info.lds;
+    if (splits) *splits = info.splits;
+    return 1;
 }
 
 int qw35_hip_quantize(uint32_t type_id, const float* src, uint64_t rows, uint64_t k, const float* col_scale,

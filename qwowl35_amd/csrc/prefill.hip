@@ -29,6 +29,8 @@
 // (qw35_hip_dequantize_f16: fp16_rne of the exact dequantised weight), which
 // is the precision of the reference's tiled matmul: qw35_kernel_mul_mm
 // dequantises its weight tiles to half (qw35_tiled_mm.metal:199-255).
+#include <stdio.h>
+
 #include <cmath>
 #include <type_traits>
 
@@ -56,6 +58,7 @@ struct PrefillArgs {
     int m_out;               // rows of c (tokens)
     int hilo;                // staged fp32 input: MFMA tiles 2i, 2i + 1 are one token tile's hi, lo rows
     int epi;                 // fp32 c: kEpiStore c = r, kEpiAdd c += r, kEpiSwiglu c = silu(c) * r
+    LaunchInfo* info;        // host pointer: describe the matmul launch here instead of launching
     int tiles_m, tiles_n;
     int splits;              // staged path: K split this many ways (1: none)
     int k_len;               // columns per split
@@ -860,6 +863,15 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     p.tiles_m = (a.m + BM - 1) / BM;
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
+    if (a.info) {
+        snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d>", BM, NW,
+                 FN, WPE, out_f32 ? "true" : "false", F16W ? "true" : "false", Q8W ? "true" : "false", KH);
+        a.info->grid = grid.x;
+        a.info->block = 64u * NW;
+        a.info->lds = (unsigned)lds;
+        a.info->splits = (unsigned)p.splits;
+        return hipSuccess;
+    }
     if (out_f32)
         hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W, KH>), grid, dim3(64 * NW), lds,
                            s, p);
@@ -877,6 +889,15 @@ hipError_t launch_tile(const PrefillArgs& a, bool a_f32, bool has_awq, bool out_
     p.tiles_m = (a.m + BM - 1) / BM;
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n);
+    if (a.info) {
+        snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_kernel<%d, %d, %d, %d, %s, %s, %s>", BM, BN, WGM, WGN,
+                 a_f32 ? "true" : "false", has_awq ? "true" : "false", out_f32 ? "true" : "false");
+        a.info->grid = grid.x;
+        a.info->block = (unsigned)NT;
+        a.info->lds = (unsigned)lds;
+        a.info->splits = 1;
+        return hipSuccess;
+    }
 #define QW35_PF(AF, AW, OF) \
     hipLaunchKernelGGL((gf4_prefill_kernel<BM, BN, WGM, WGN, AF, AW, OF>), grid, dim3(NT), lds, s, p)
     if (a_f32) {
@@ -1046,6 +1067,15 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
             best.kh = 4;
         }
     }
+    // fp32 activations of 65..128 tokens (129..256 staged rows) on GF4 rows of
+    // k <= 4096: a 128-row tile on 8 waves as two K halves, unsplit (same box,
+    // 12288x4096 M = 128: 47.0-50.5 us planned {128, fn 4, 4 splits} -> 40.3;
+    // 4096x12288 kept its plan, 41.1 against 42.3-149 us for the others).
+    if (hilo && !f16w && !q8w && m > 128 && m <= 256 && k <= 4096 && k % 512 == 0) {
+        best = PrefillCfg{128, 2, 1};
+        best.waves = 8;
+        best.kh = 2;
+    }
     return best;
 }
 
@@ -1092,7 +1122,7 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 // wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks (1 and 2 take column-order tokens and a workspace).
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
-                                  hipStream_t stream, int wkind, int epi) {
+                                  hipStream_t stream, int wkind, int epi, LaunchInfo* info, bool staged) {
     const bool f16w = wkind == 1, q8w = wkind == 2;
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
@@ -1103,6 +1133,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     p.m_out = m;
     p.hilo = 0;
     p.epi = epi;
+    p.info = info;
     // epilogues read fp32 c; the path without a workspace has none
     if (epi != kEpiStore && (!out_f32 || !workspace)) return hipErrorInvalidValue;
     if (epi < kEpiStore || epi > kEpiSwiglu) return hipErrorInvalidValue;
@@ -1130,10 +1161,13 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         float* rs = reinterpret_cast<float*>(ws + round256((size_t)ms * k * 2));
         float* partial = reinterpret_cast<float*>(ws + round256((size_t)ms * k * 2) + round256((size_t)m * 4));
         const unsigned stage_grid = af ? (unsigned)(ms / 2) : (unsigned)m;
+        if (info) info->ws_bytes = gf4_prefill_workspace_bytes(m, rows, k, cfg, af);
 #define QW35_STAGE(AF, AW, ORD)                                                                                   \
     hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, ORD>), dim3(stage_grid), dim3(kStageThreads), 0, stream, a, \
                        awq, m, k, a16, rs)
-        if (f16w || q8w) {
+        if (info || staged) {
+            // described only, or the workspace already holds these activations staged
+        } else if (f16w || q8w) {
             if (af) {
                 if (aw) QW35_STAGE(true, true, false); else QW35_STAGE(true, false, false);
             } else {
@@ -1147,7 +1181,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
             }
         }
 #undef QW35_STAGE
-        hipError_t e = hipGetLastError();
+        hipError_t e = info || staged ? hipSuccess : hipGetLastError();
         if (e != hipSuccess) return e;
         p.a = a16;
         p.awq = nullptr;
@@ -1205,7 +1239,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
             case 322: e = launch_f16_tile<32, 4, 2, 2>(p, kf32, stream); break;
             default: return hipErrorInvalidValue;
         }
-        if (e != hipSuccess || !split) return e;
+        if (e != hipSuccess || !split || info) return e;
         const size_t threads = (size_t)m * ((rows + 3) / 4);
         const dim3 grid((unsigned)((threads + kReduceThreads - 1) / kReduceThreads));
         if (of)
@@ -1226,11 +1260,13 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
 
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                           void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                          int epi) {
+                          int epi, LaunchInfo* info, bool staged) {
     if (!workspace && wkind != 0) return hipErrorInvalidValue;
+    if (staged && !workspace) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
     if (workspace) fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
-    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind, epi);
+    return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind, epi, info,
+                                  staged);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {

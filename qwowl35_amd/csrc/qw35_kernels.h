@@ -141,12 +141,18 @@ size_t prefill_workspace_bytes(int m, int rows, int k, int wkind, bool with_f32)
 // Smallest workspace the staged path accepts (no K split).
 size_t prefill_min_workspace_bytes(int m, int rows, int k, bool a_f32);
 // epi (fp32 c with a workspace only): 0 c = r, 1 c += r, 2 c = silu(c) * r.
+// info (host pointer, nullable): describe the matmul launch (name, grid,
+// block, LDS, splits; ws_bytes the workspace it uses) and launch nothing.
+// staged: the workspace already holds these activations staged for this
+// weight form (the previous launch on it staged the same a, awq, m, k and
+// column order), so the staging pass is not launched again.
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
-                                  int wkind = 0, int epi = 0);  // wkind 0 GF4, 1 F16, 2 q8_0
+                                  int wkind = 0, int epi = 0, LaunchInfo* info = nullptr,
+                                  bool staged = false);  // wkind 0 GF4, 1 F16, 2 q8_0
 // Planned launch; the workspace is required for F16 and q8_0 weights.
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                           void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                          int epi = 0);
+                          int epi = 0, LaunchInfo* info = nullptr, bool staged = false);
 
 }  // namespace qw35

@@ -385,6 +385,21 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
     return dst
 
 
+def prefill_kernel(w: HipWeight, n_tokens: int, a_dtype: torch.dtype = torch.bfloat16, awq: bool = False,
+                   out_dtype: torch.dtype = torch.bfloat16, workspace: bool = True) -> dict:
+    """The matmul kernel ``matmul_prefill`` launches for this call shape
+    (``qw35_hip_prefill_kernel``; nothing is launched): name as the profiler
+    shows it, grid, block, LDS bytes and K splits."""
+    name = C.create_string_buffer(160)
+    grid, block, lds, splits = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_uint32()
+    a_dt = _ffi.DTYPE_F32 if a_dtype == torch.float32 else _ffi.DTYPE_BF16
+    c_dt = _ffi.DTYPE_F32 if out_dtype == torch.float32 else _ffi.DTYPE_BF16
+    _ffi.call("qw35_hip_prefill_kernel", C.byref(w.view), n_tokens, a_dt, int(awq), c_dt, int(workspace), name,
+              C.sizeof(name), C.byref(grid), C.byref(block), C.byref(lds), C.byref(splits))
+    return {"name": name.value.decode(), "grid": grid.value, "block": block.value, "lds": lds.value,
+            "splits": splits.value}
+
+
 def matvec_batch(w: HipWeight, x: torch.Tensor, dst: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Multi-token matvec of fp32 activations [n_tokens, k] (``encodeMatvecBatch``, +FFN.m:260-306).
 
