@@ -465,9 +465,9 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
     staged path (workspace, fp16 MFMA; the time includes the staging pass).
     Each shape also at M = 128 with fp32 activations and fp32 out (the
     runtime's multi-token chunks: an fp16 hi/lo pair per activation, twice the
-    MFMA work).  Then the q8_0 projections (6 rotated copies), dequantised
-    inside the staged kernel and, for comparison, through their fp16 prefill
-    image.  Utilisation is against the nominal 2.5 PFLOP/s and against the
+    MFMA work).  Then q8_0 and Q4_K projections (6 rotated copies),
+    dequantised inside the staged kernel and, for comparison, through their
+    fp16 prefill image.  Utilisation is against the nominal 2.5 PFLOP/s and against the
     MFMA probe's sustained rate on this box.  Every line of this library's
     kernels carries the CPU baseline of the same shape and M (numpy
     dequantisation + fp32 BLAS)."""
@@ -505,26 +505,29 @@ def bench_prefill(b: Bench, cpu: CpuBaseline | None) -> dict:
             out[f"prefill_gf4{tag}_m{m}_{rows}x{k}"] = with_cpu(line(ms, m, rows, k, kern), rt.TYPE_GF4, ws[0],
                                                                 rows, k, m, "GF4")
         del ws
-    for rows, k in ((8192, 4096), (4096, 4096)):
-        q8 = [b.weight(rt.TYPE_Q8_0, rows, k) for _ in range(6)]
+    for type_id, name, rows, k, ms_list in ((rt.TYPE_Q8_0, "q8_0", 8192, 4096, (128, 512, 2048)),
+                                            (rt.TYPE_Q8_0, "q8_0", 4096, 4096, (128, 512, 2048)),
+                                            (rt.TYPE_Q4_K, "q4_k", 12288, 4096, (128, 512)),
+                                            (rt.TYPE_Q4_K, "q4_k", 4096, 12288, (128, 512))):
+        wq = [b.weight(type_id, rows, k) for _ in range(6)]
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
-        imgs = [rt.prefill_image(w) for w in q8]
+        imgs = [rt.prefill_image(w) for w in wq]
         ev1.record()
         torch.cuda.synchronize()
-        out[f"prefill_image_q8_0_{rows}x{k}_us"] = round(ev0.elapsed_time(ev1) * 1e3 / len(q8), 2)
-        for m in (128, 512, 2048):
+        out[f"prefill_image_{name}_{rows}x{k}_us"] = round(ev0.elapsed_time(ev1) * 1e3 / len(wq), 2)
+        for m in ms_list:
             a = b.normal((m, k)).to(torch.bfloat16)
             c = torch.empty((m, rows), dtype=torch.bfloat16, device=b.dev)
-            for tag, wl in (("", q8), ("_f16img", imgs)):
+            for tag, wl in (("", wq), ("_f16img", imgs)):
                 wsp = rt.prefill_workspace(wl[0], m, device=b.dev)
                 calls = [lambda s, w=w, wsp=wsp: rt.matmul_prefill(w, a, dst=c, workspace=wsp, stream=s) for w in wl]
                 ms, _ = b.time_launches(calls, max(24, 4800 // m), 12)
                 r = line(ms, m, rows, k, rt.prefill_kernel(wl[0], m))
                 if not tag:
-                    r = with_cpu(r, rt.TYPE_Q8_0, q8[0], rows, k, m, "q8_0")
-                out[f"prefill_q8_0{tag}_m{m}_{rows}x{k}"] = r
-        del q8, imgs
+                    r = with_cpu(r, type_id, wq[0], rows, k, m, name)
+                out[f"prefill_{name}{tag}_m{m}_{rows}x{k}"] = r
+        del wq, imgs
     # Reference point, not this library: the vendor's dense fp16 GEMM (torch.mm,
     # served by hipBLASLt) on the same shapes with fp16 weights in HBM (4 rotated
     # copies), timed eagerly with events on the bench stream.

@@ -429,18 +429,19 @@ void *qw35_hip_runtime_stream(void *runtime);
 /* The device tensor store the runtime reads its weights from. */
 const void *qw35_hip_runtime_store(void *runtime);
 
-/* Multi-token (prefill) matmul of a GF4, q8_0 or F16 weight on MFMA:
+/* Multi-token (prefill) matmul of a GF4, q8_0, Q4_K or F16 weight on MFMA:
  *   c[t][r] = sum_k W[r][k] * v[t][k],  v = awq[k] * a[t][k]   (awq == NULL: v = a)
  * a: device [n_tokens][k], a_dtype QW35_HIP_DTYPE_BF16 or QW35_HIP_DTYPE_F32;
  * c: device [n_tokens][rows], c_dtype QW35_HIP_DTYPE_BF16 (round-to-nearest-
  * even) or QW35_HIP_DTYPE_F32; fp32 accumulation.  Replaces encodeMatvecBatch /
  * encodeTiledKMatmul for type 100 (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366,
  * kernel qw35_mul_mm_gf4_f32 of qw35_tiled_mm.metal:203-255), for q8_0
- * dequantised in the kernel to fp16(d * q) (qw35_mul_mm_q8_0_f32), and,
- * through an F16 weight (the prefill image of qw35_hip_dequantize_f16), for
- * the GF2 / Q4_K / Q5_K / Q6_K projections
- * (qw35_mul_mm_{gf2,q4_k,q5_k,q6_k}_f32, qw35_tiled_mm.metal:208-254); a
- * q8_0 weight's image gives the same products, at 2 bytes per weight of HBM.
+ * and Q4_K dequantised in the kernel to the fp16 of their exact values
+ * (qw35_mul_mm_q8_0_f32, qw35_mul_mm_q4_k_f32), and, through an F16 weight
+ * (the prefill image of qw35_hip_dequantize_f16), for the GF2 / Q5_K / Q6_K
+ * projections (qw35_mul_mm_{gf2,q5_k,q6_k}_f32, qw35_tiled_mm.metal:208-254);
+ * a q8_0 or Q4_K weight's image gives the same products, at 2 bytes per
+ * weight of HBM.
  * 1 <= n_tokens <= 65536, rows <= 2^24; n_tokens * k <= 2^30 for bf16
  * activations, 2^29 for fp32. */
 #define QW35_HIP_DTYPE_F32 0u
@@ -469,8 +470,8 @@ const void *qw35_hip_runtime_store(void *runtime);
  * n_tokens); a smaller workspace that still holds the staged activations (2
  * bytes per staged activation, 4 per token, each part rounded up to 256
  * bytes; fp32 activations stage two rows per token in groups of 32 tokens:
- * 64 * ceil(n_tokens / 32) rows) is accepted and splits K less.  F16 and q8_0
- * weights always take the staged path (the workspace is required). */
+ * 64 * ceil(n_tokens / 32) rows) is accepted and splits K less.  F16, q8_0
+ * and Q4_K weights always take the staged path (the workspace is required). */
 uint64_t qw35_hip_matmul_prefill_workspace_size(const qw35_hip_weight *w, uint32_t n_tokens);
 int qw35_hip_matmul_prefill(const qw35_hip_weight *w, const void *a, uint32_t a_dtype, const float *awq, void *c,
                             uint32_t c_dtype, uint32_t n_tokens, void *workspace, uint64_t workspace_bytes,

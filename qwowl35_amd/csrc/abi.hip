@@ -223,9 +223,13 @@ struct StageKey {
     }
 };
 
-// Weight form of the prefill kernel: 0 GF4 words, 1 F16, 2 q8_0 blocks; -1 none.
+// Weight form of the prefill kernel: 0 GF4 words, 1 F16, 2 q8_0 blocks, 3 Q4_K super-blocks; -1 none.
 int prefill_wkind(uint32_t type_id) {
-    return type_id == qw35::kTypeGF4 ? 0 : type_id == qw35::kTypeF16 ? 1 : type_id == qw35::kTypeQ8_0 ? 2 : -1;
+    return type_id == qw35::kTypeGF4    ? 0
+           : type_id == qw35::kTypeF16  ? 1
+           : type_id == qw35::kTypeQ8_0 ? 2
+           : type_id == qw35::kTypeQ4_K ? 3
+                                        : -1;
 }
 
 // A MATMUL / MATMUL_SWIGLU plan op: the rules of qw35_hip_matmul_prefill(_epilogue)
@@ -234,7 +238,7 @@ bool check_matmul_op(const qw35_hip_plan_op& o, const char* what, char* err, uin
     const bool sw = o.kind == QW35_HIP_OP_MATMUL_SWIGLU;
     if (!check_weight(o.w, what, err, err_len) || !check_chunked_k(o.w, what, err, err_len)) return false;
     if (prefill_wkind(o.w->type_id) < 0) {
-        set_err(err, err_len, "%s: the prefill matmul takes GF4, q8_0 or F16 weights, got type %u", what,
+        set_err(err, err_len, "%s: the prefill matmul takes GF4, q8_0, Q4_K or F16 weights, got type %u", what,
                 o.w->type_id);
         return false;
     }
@@ -669,9 +673,9 @@ static int prefill_call(const qw35_hip_weight* w, const void* a, uint32_t a_dtyp
         set_err(err, err_len, "matmul_prefill: the add and SwiGLU epilogues take fp32 c and a workspace");
         return 0;
     }
-    if (w->type_id != qw35::kTypeGF4 && w->type_id != qw35::kTypeF16 && w->type_id != qw35::kTypeQ8_0) {
+    if (prefill_wkind(w->type_id) < 0) {
         set_err(err, err_len,
-                "matmul_prefill: GF4 (type 100), q8_0 (type 8) or F16 (type 1) weights, got %s; make the fp16 "
+                "matmul_prefill: GF4 (type 100), q8_0 (type 8), Q4_K (type 12) or F16 (type 1) weights, got %s; make the fp16 "
                 "prefill image of another k-quant weight with qw35_hip_dequantize_f16",
                 type_name(w->type_id));
         return 0;
@@ -717,7 +721,10 @@ static int prefill_call(const qw35_hip_weight* w, const void* a, uint32_t a_dtyp
         if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
             set_err(err, err_len,
                     "matmul_prefill: %s a 256-byte aligned workspace of >= %llu bytes for %u %s tokens, got %llu",
-                    wkind == 0 ? "the staged path needs" : wkind == 1 ? "f16 weights need" : "q8_0 weights need",
+                    wkind == 0   ? "the staged path needs"
+                    : wkind == 1 ? "f16 weights need"
+                    : wkind == 2 ? "q8_0 weights need"
+                                 : "q4_k weights need",
                     (unsigned long long)need, n_tokens, a_f32 ? "fp32" : "bf16",
                     (unsigned long long)(workspace ? workspace_bytes : 0));
             return 0;

@@ -462,7 +462,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   the range is read) and realigns with v_perm.  B = fp16(d * q): the int8
 //   to exact fp16 of the decode GEMVs, then one v_pk_mul_f16 by (d, d) -- the
 //   same bits as the F16 prefill image, fp16_rne(d * q).
-template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false, int KH = 1>
+// * Q4W: the weights are Q4_K super-blocks (144 bytes per 256 columns: fp16 d
+//   and dmin, 12 bytes of 6-bit sub-block scales and mins, 128 bytes of
+//   nibbles) dequantised in the kernel, as the reference's tiled matmul does
+//   (qw35_mul_mm_q4_k_f32, qw35_tiled_mm.metal:209-214), no image.  A step's
+//   64 columns are the sub-block pair 2j, 2j + 1 (j = kt mod 4) of each row,
+//   whose elements are the low and high nibbles of the same 32 bytes
+//   qs[32j .. 32j + 31]; lane half h takes sub-block 2j + h, 8 columns per
+//   sub-step in column order.  A lane loads the super-block's 16-byte header
+//   and the 32 bytes (three 16-byte loads; the header line stays cached for
+//   the four steps of a super-block).  B = fp16_rne(fl32(d sc q - dmin m)):
+//   d sc and dmin m are exact fp32 products formed once per step, one fma per
+//   weight rounds once -- the exact dequantised value of
+//   qw35_dequant_q4_k_at (qw35_matvec.metal:2-12), then the same fp16 bits as
+//   the F16 prefill image.
+template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false, int KH = 1,
+          bool Q4W = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
     constexpr int NWG = NW / KH;            // waves per K half
@@ -517,12 +532,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         a_off[i] = ((uint32_t)gm * (uint32_t)K + (uint32_t)k_begin + (uint32_t)col * 8u) * 2u;
         a_lds[i] = row * kLdsRow + col * 16;
     }
-    constexpr int WCH = F16W ? 4 : Q8W ? 3 : 1;  // 16-byte weight loads per lane per 32-row tile per step
+    constexpr int WCH = F16W ? 4 : (Q8W || Q4W) ? 3 : 1;  // 16-byte weight loads per lane per 32-row tile per step
     const uint8_t* w_src[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const size_t row = (size_t)min(n0 + 32 * j + l32, p.n - 1);
-        if constexpr (Q8W)
+        if constexpr (Q4W)
+            w_src[j] = reinterpret_cast<const uint8_t*>(p.w) + row * (size_t)(K / 256 * 144) + (k_begin / 256) * 144;
+        else if constexpr (Q8W)
             w_src[j] = reinterpret_cast<const uint8_t*>(p.w) + row * (size_t)(K / 32 * 34) + (k_begin / 32) * 34 +
                        32 * half;
         else
@@ -548,7 +565,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int c = 0; c < WCH; ++c)
-                w[j][c] = load_cached16(w_src[j] + (Q8W  ? (k0 / 64) * 68 - 4 * ((k0 / 64) & 3) + 16 * c
+                w[j][c] = load_cached16(w_src[j] + (Q4W   ? (k0 / 256) * 144 + (c ? 16 * c + 32 * ((k0 / 64) & 3) : 0)
+                                                    : Q8W  ? (k0 / 64) * 68 - 4 * ((k0 / 64) & 3) + 16 * c
                                                     : F16W ? k0 * 2 + 16 * c
                                                            : k0 / 2));
     };
@@ -579,10 +597,48 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             const uint4_t v = w[j][d >> 2];
             return (d & 3) == 0 ? v.x : (d & 3) == 1 ? v.y : (d & 3) == 2 ? v.z : v.w;
         };
+        // Q4W: the step's sub-block scale and min of this lane half, per tile
+        // (sub-block 2 * (kt mod 4) + half, unpacked as get_scale_min_k4)
+        float q4_dsc[FN], q4_dm[FN];
+        if constexpr (Q4W) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint4_t hd = w[j][0];
+                const half2_t dd = as_half2(hd.x);
+                uint32_t sc, mn;
+                if constexpr (s0 < 2) {  // sub-blocks 0..3: scales[sb] and scales[sb + 4], low 6 bits
+                    const uint32_t sh = 8u * (2u * s0 + (uint32_t)half);
+                    sc = (hd.y >> sh) & 63u;
+                    mn = (hd.z >> sh) & 63u;
+                } else {  // sub-blocks 4..7: low / high nibble of scales[sb + 4], top bits of scales[sb - 4] / [sb]
+                    const uint32_t sh = 8u * (2u * (s0 - 2) + (uint32_t)half);
+                    const uint32_t hi = hd.w >> sh;
+                    sc = (hi & 0x0Fu) | (((hd.y >> sh) >> 6 & 3u) << 4);
+                    mn = ((hi >> 4) & 0x0Fu) | (((hd.z >> sh) >> 6 & 3u) << 4);
+                }
+                q4_dsc[j] = (float)dd.x * (float)sc;
+                q4_dm[j] = (float)dd.y * (float)mn;
+            }
+        }
         auto fetch = [&](int kk, int s) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                if constexpr (Q8W) {
+                if constexpr (Q4W) {
+                    // bytes 8kk .. 8kk + 7 of the pair's 32: loads 1 (bytes 0..15) and 2 (16..31)
+                    const uint4_t v = w[j][1 + (kk >> 1)];
+                    uint32_t q2[2] = {(kk & 1) ? v.z : v.x, (kk & 1) ? v.w : v.y};
+                    float e[8];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t nib = (half ? q2[h] >> 4 : q2[h]) & 0x0F0F0F0Fu;
+#pragma unroll
+                        for (int b = 0; b < 4; ++b)  // v_cvt_f32_ubyte<b>; fp32 rounding, then fp16
+                            e[4 * h + b] =
+                                keep_f32(__builtin_fmaf(q4_dsc[j], (float)((nib >> (8 * b)) & 0xFFu), -q4_dm[j]));
+                    }
+                    wf[s][j] = __builtin_bit_cast(half8_t, uint4_t{as_u32(h2(e[0], e[1])), as_u32(h2(e[2], e[3])),
+                                                                   as_u32(h2(e[4], e[5])), as_u32(h2(e[6], e[7]))});
+                } else if constexpr (Q8W) {
                     const half2_t d2 = as_half2(__builtin_amdgcn_perm(span(j, 0), span(j, 0), q8_dsel));
                     uint32_t b[4];
 #pragma unroll
@@ -634,7 +690,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             if (kk < 3) {
                 // per MFMA: one LDS read (the first FM of them) and a share of
                 // the next sub-step's decode (15 VALU per word, FN words)
-                constexpr int kValuPerMfma = F16W ? 0 : ((Q8W ? 16 : 15) * FN + FM * FN - 1) / (FM * FN);
+                constexpr int kValuPerMfma =
+                    F16W ? 0 : ((Q4W ? 26 : Q8W ? 16 : 15) * FN + FM * FN - 1) / (FM * FN);
 #pragma unroll
                 for (int q = 0; q < FM * FN; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -854,7 +911,7 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     }
 }
 
-template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, int KH = 1>
+template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, int KH = 1, bool Q4W = false>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     constexpr int BN = 32 * FN * NW / KH;
     const size_t lds = 2 * (size_t)KH * BM * kLdsRow;
@@ -864,8 +921,9 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     p.tiles_n = (a.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (a.info) {
-        snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d>", BM, NW,
-                 FN, WPE, out_f32 ? "true" : "false", F16W ? "true" : "false", Q8W ? "true" : "false", KH);
+        snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s>", BM,
+                 NW, FN, WPE, out_f32 ? "true" : "false", F16W ? "true" : "false", Q8W ? "true" : "false", KH,
+                 Q4W ? "true" : "false");
         a.info->grid = grid.x;
         a.info->block = 64u * NW;
         a.info->lds = (unsigned)lds;
@@ -873,10 +931,10 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
         return hipSuccess;
     }
     if (out_f32)
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W, KH>), grid, dim3(64 * NW), lds,
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W, KH, Q4W>), grid, dim3(64 * NW), lds,
                            s, p);
     else
-        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W, Q8W, KH>), grid, dim3(64 * NW), lds,
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W, Q8W, KH, Q4W>), grid, dim3(64 * NW), lds,
                            s, p);
     return hipGetLastError();
 }
@@ -976,8 +1034,12 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // fp32 input (hilo) stages two rows per token in 32-token groups: the tiles
 // are planned over the staged rows, of at least 64 (one hi and one lo MFMA
 // tile per wave), and the K-split partial sums stay one row per token.
-PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool hilo) {
+// Q4_K blocks (q4w) plan as q8_0 blocks do (the same load ring and one-tile
+// waves), with their own bytes per weight.
+PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool hilo, bool q4w = false) {
     const int m = staged_rows(m_tokens, hilo);
+    const double w_bytes = f16w ? 2.0 : q4w ? 144.0 / 256.0 : q8w ? 34.0 / 32.0 : 0.5;
+    q8w = q8w || q4w;
     constexpr double kUsPerMflop = 0.108, kUsPerMB = 29.9;
     // K-split partial sums cost less relative to fp16 weight tiles than to GF4
     // ones: with 0.5 the F16 plan for 8192x4096 M=128 was {64,2,4} 57.1 us,
@@ -988,7 +1050,6 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
     const double kUsPerPartialMB = (f16w || q8w) ? 0.35 : 0.5;
     const int cus = num_cus();
     const int chunks = k / 256;
-    const double w_bytes = f16w ? 2.0 : q8w ? 34.0 / 32.0 : 0.5;
     // 256-token tiles (one wave per SIMD, 256 accumulator registers) only for
     // F16 and q8_0 weights: q8_0 8192x4096 M = 2048 200 us against 331 with
     // 128 tokens, F16 172 against 244; GF4 was slower with them (236-260 us
@@ -1000,6 +1061,7 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
         const int bm = sh[0], fn = sh[1], bn = 128 * fn;
         if ((f16w || q8w) && fn != 2) continue;
         if (bm == 256 && !(f16w || q8w)) continue;
+        if (bm == 256 && q4w) continue;  // its 8-wave 256-token tile spills registers
         if (bm > 32 && m <= bm / 2) continue;  // half the token tile or more would be padding
         if (hilo && bm < 64) continue;
         const long tiles = (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn);
@@ -1047,6 +1109,16 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
         best.kh = 2;
         best.splits /= 2;
     }
+    // Q4_K: every block dequantises its whole weight tile on the VALU, so a
+    // 64-token tile over more than 64 tokens decodes each weight twice as
+    // often as a 128-token tile; take the latter with twice the K split.
+    // Same-box sweep, bf16 activations, 4096x12288 M = 128: {64, split 4,
+    // halves} 44.0 us -> {128, split 8, halves} 37.3 us.
+    if (q4w && !hilo && best.bm == 64 && m > 64 && chunks % (2 * best.splits * best.kh) == 0 &&
+        k / (2 * best.splits * best.kh) >= 512) {
+        best.bm = 128;
+        best.splits *= 2;
+    }
     // K quarters for GF4 at 33..128 tokens and k <= 4096: each 64-token block
     // runs four parts of its K range (16 steps each at k = 4096, summed in
     // LDS) instead of two of 32, with no K split and so no reduction launch,
@@ -1080,7 +1152,7 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
 }
 
 PrefillCfg plan_prefill_kind(int m, int rows, int k, int wkind, bool a_f32) {
-    return plan_prefill(m, rows, k, wkind == 1, wkind == 2, a_f32);
+    return plan_prefill(m, rows, k, wkind == 1, wkind == 2, a_f32, wkind == 3);
 }
 
 PrefillCfg plan_gf4_prefill(int m, int rows, int k, bool a_f32) { return plan_prefill_kind(m, rows, k, 0, a_f32); }
@@ -1119,11 +1191,12 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 
 }  // namespace
 
-// wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks (1 and 2 take column-order tokens and a workspace).
+// wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks, 3 Q4_K super-blocks (1..3 take column-order tokens and a
+// workspace).
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
                                   hipStream_t stream, int wkind, int epi, LaunchInfo* info, bool staged) {
-    const bool f16w = wkind == 1, q8w = wkind == 2;
+    const bool f16w = wkind == 1, q8w = wkind == 2, q4w = wkind == 3;
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
     p.a = a;
@@ -1153,7 +1226,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         if (cfg.kh == 2 && (f16w || cfg.waves != 8 || cfg.fn != 2 || (cfg.bm != 64 && cfg.bm != 128)))
             return hipErrorInvalidValue;
         // K quarters: the 64-token GF4 tile on 16 waves (128 rows) or 8 (64 rows)
-        if (cfg.kh == 4 && (f16w || q8w || (cfg.waves != 16 && cfg.waves != 8) || cfg.fn != 2 || cfg.bm != 64))
+        if (cfg.kh == 4 && (f16w || q8w || q4w || (cfg.waves != 16 && cfg.waves != 8) || cfg.fn != 2 || cfg.bm != 64))
             return hipErrorInvalidValue;
         const int ms = staged_rows(m, af);
         uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -1167,7 +1240,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
                        awq, m, k, a16, rs)
         if (info || staged) {
             // described only, or the workspace already holds these activations staged
-        } else if (f16w || q8w) {
+        } else if (f16w || q8w || q4w) {
             if (af) {
                 if (aw) QW35_STAGE(true, true, false); else QW35_STAGE(true, false, false);
             } else {
@@ -1193,7 +1266,20 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const bool split = cfg.splits > 1;
         if (split) p.c = partial;
         const bool kf32 = of || split;
-        if (q8w) {
+        if (q4w) {  // no 256-token tiles (plan_prefill never picks them for Q4_K)
+            switch (cfg.bm * 10 + cfg.fn) {
+                case 1282:
+                    e = cfg.kh == 2 ? launch_f16_tile<128, 8, 1, 2, false, false, 2, true>(p, kf32, stream)
+                                    : launch_f16_tile<128, 8, 1, 2, false, false, 1, true>(p, kf32, stream);
+                    break;
+                case 642:
+                    e = cfg.kh == 2 ? launch_f16_tile<64, 8, 1, 2, false, false, 2, true>(p, kf32, stream)
+                                    : launch_f16_tile<64, 8, 1, 2, false, false, 1, true>(p, kf32, stream);
+                    break;
+                case 322: e = launch_f16_tile<32, 4, 2, 2, false, false, 1, true>(p, kf32, stream); break;
+                default: return hipErrorInvalidValue;
+            }
+        } else if (q8w) {
             switch (cfg.bm * 10 + cfg.fn) {
                 case 2562:
                     e = cfg.waves == 8 ? launch_f16_tile<256, 8, 1, 2, false, true>(p, kf32, stream)

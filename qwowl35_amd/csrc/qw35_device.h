@@ -129,6 +129,15 @@ __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
 __device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
+// v as a materialised fp32 value: the empty asm keeps the compiler from fusing
+// the fma that produced v with a following fp16 conversion into v_fma_mix,
+// whose single rounding straight to fp16 differs from fp16(fl32(x)) whenever
+// the fp32 rounding of x is inexact.
+__device__ __forceinline__ float keep_f32(float v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 // fp32 -> fp16 round-to-nearest-even, packed.
 __device__ __forceinline__ half2_t h2(float lo, float hi) {
     half2_t r;

@@ -273,10 +273,10 @@ std::vector<qw35_hip_plan_op> chunk_ops(const Runtime& r, uint32_t n, int mode) 
     return ops;
 }
 
-// The prefill matmul's weight for w: w itself (GF4, q8_0), else its fp16
-// image, made on the runtime's stream and owned by the runtime.
+// The prefill matmul's weight for w: w itself (GF4, q8_0, Q4_K), else its
+// fp16 image, made on the runtime's stream and owned by the runtime.
 bool prefill_form(Runtime* r, const qw35_hip_weight& w, qw35_hip_weight* pf, char* err, uintptr_t err_len) {
-    if (w.type_id == QW35_HIP_TYPE_GF4 || w.type_id == QW35_HIP_TYPE_Q8_0) {
+    if (w.type_id == QW35_HIP_TYPE_GF4 || w.type_id == QW35_HIP_TYPE_Q8_0 || w.type_id == QW35_HIP_TYPE_Q4_K) {
         *pf = w;
         return true;
     }

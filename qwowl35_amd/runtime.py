@@ -68,10 +68,10 @@ class HipWeight:
 
     @property
     def prefill(self) -> "HipWeight":
-        """The weight ``matmul_prefill`` takes: itself for GF4 / F16 / q8_0 (q8_0
-        is dequantised inside the prefill kernel), else its fp16 prefill image
-        (``prefill_image``), made on first use and kept."""
-        if self.type_id in (TYPE_GF4, TYPE_F16, TYPE_Q8_0):
+        """The weight ``matmul_prefill`` takes: itself for GF4 / F16 / q8_0 /
+        Q4_K (q8_0 and Q4_K are dequantised inside the prefill kernel), else
+        its fp16 prefill image (``prefill_image``), made on first use and kept."""
+        if self.type_id in (TYPE_GF4, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K):
             return self
         img = getattr(self, "_prefill", None)
         if img is None:
@@ -347,9 +347,9 @@ def matmul_prefill(w: HipWeight, a: torch.Tensor, awq: torch.Tensor | None = Non
                    out_dtype: torch.dtype = torch.bfloat16, dst: torch.Tensor | None = None,
                    workspace: torch.Tensor | None | bool = True, stream=None,
                    epilogue: int = _ffi.EPILOGUE_STORE) -> torch.Tensor:
-    """``C[t] = (awq * a[t]) @ W^T`` for a GF4, q8_0 or F16 weight
+    """``C[t] = (awq * a[t]) @ W^T`` for a GF4, q8_0, Q4_K or F16 weight
     (``encodeTiledKMatmul``; the other k-quants enter as their fp16 image,
-    ``w.prefill``).  q8_0 and F16 need a workspace.
+    ``w.prefill``).  q8_0, Q4_K and F16 need a workspace.
 
     ``a``: [n_tokens, k] bf16 or fp32 device tensor; result [n_tokens, rows] in
     ``out_dtype`` (bfloat16, rounded to nearest even, or float32).

@@ -25,6 +25,21 @@ def make_weight(type_id: int, rows: int, k: int, seed: int, std: float = 0.02):
     return raw, om.dequant(type_id, raw, rows, k)
 
 
+def random_kq_bytes(rng: np.random.Generator, type_id: int, rows: int, k: int) -> np.ndarray:
+    """Arbitrary Q4_K / Q5_K bytes (every nibble, high bit and 6-bit scale/min
+    pattern) with d and dmin drawn from fp16 values, negative and subnormal ones
+    included, that keep every dequantised weight inside fp16's range
+    (|d| * 63 * 31 < 65504).  Mixed magnitudes of d * sc * q and dmin * m make
+    the fp32 rounding of the weight inexact, which separates fp16(fl32(w))
+    from a single rounding of w straight to fp16."""
+    bb = {om.TYPE_Q4_K: 144, om.TYPE_Q5_K: 176}[type_id]
+    raw = rng.integers(0, 256, size=(rows, k // 256, bb), dtype=np.uint8)
+    pick = np.array([2.0 ** -24, 2.0 ** -14, 2.0 ** -10, 0.013, -0.5, 1.0, 3.5, -30.0], np.float16)
+    for off in (0, 2):
+        raw[:, :, off:off + 2] = rng.choice(pick, size=(rows, k // 256)).view(np.uint8).reshape(rows, k // 256, 2)
+    return raw.reshape(-1)
+
+
 def random_gf4_words(rng: np.random.Generator, shape) -> np.ndarray:
     """Arbitrary 32-bit GF4 words with finite scale bytes (exponent != 31)."""
     w = rng.integers(0, 2**32, size=shape, dtype=np.uint64).astype(np.uint32)

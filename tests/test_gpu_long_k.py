@@ -139,7 +139,7 @@ def test_long_k_gf4_prefill_fp32_input(cuda):
 
 @pytest.mark.parametrize("name", ["q8_0", "q4_k"])
 def test_long_k_kquant_prefill(cuda, name):
-    """q8_0 dequantised in the kernel, Q4_K through its fp16 prefill image."""
+    """q8_0 and Q4_K dequantised in the kernel (no fp16 image)."""
     import torch
 
     type_id = TYPES[name]
@@ -153,7 +153,8 @@ def test_long_k_kquant_prefill(cuda, name):
     bits = om.f32_to_bf16_bits(a32)
     a_dev = torch.from_numpy(bits.view(np.int16)).to(cuda).view(torch.bfloat16)
     img = om.prefill_image(type_id, raw, n, k).astype(np.float32)
-    pw = w.prefill if name == "q8_0" else _rt().prefill_image(w)
+    pw = w.prefill
+    assert pw is w
     for a_host, a in ((bits, a_dev), (a32, _t(a32, cuda))):
         out = _rt().matmul_prefill(pw, a, awq=_t(awq, cuda), out_dtype=torch.float32)
         check_prefill(out, a_host, awq, img, w_exact=om.dequant(type_id, raw, n, k))

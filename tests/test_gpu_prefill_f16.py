@@ -19,7 +19,7 @@ import pytest
 
 from oracle import matvec as om
 from oracle import q6_k as oq6
-from tests.helpers import activations, awq_scales, bf16_normal, check_prefill, make_weight
+from tests.helpers import activations, awq_scales, bf16_normal, check_prefill, make_weight, random_kq_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -60,6 +60,17 @@ def test_prefill_image_bit_exact(cuda, name, rows, k):
     # the F16 weight dequantises back to exactly the fp16 values
     back = _rt().dequantize(img).cpu().numpy()
     assert np.array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", ["q4_k", "q5_k"])
+def test_prefill_image_bit_exact_random_bytes(cuda, name):
+    """Arbitrary super-block bytes: the image is fp16 of the fp32 weight (two
+    roundings), also where the fp32 rounding is inexact."""
+    rows, k = 64, 1024
+    raw = random_kq_bytes(np.random.default_rng(31), NAMES[name], rows, k)
+    w = _rt().HipWeight.upload(raw, NAMES[name], rows, k)
+    got = _rt().prefill_image(w).storage.cpu().numpy().view(np.uint16).reshape(rows, k)
+    assert np.array_equal(got, om.prefill_image(NAMES[name], raw, rows, k).view(np.uint16))
 
 
 def _bf16_tensor(bits, cuda):
@@ -104,7 +115,7 @@ def test_f16_prefill_fp32_input(cuda):
 @pytest.mark.parametrize("name", ["gf2", "q8_0", "q4_k", "q5_k", "q6_k"])
 def test_matvec_batch_long_kquant_chunk(cuda, name):
     """More than 8 fp32 tokens on a k-quant weight: the prefill matmul on its
-    fp16 image (q8_0: decoded in the kernel to the same values) with fp32
+    fp16 image (q8_0, Q4_K: decoded in the kernel to the same values) with fp32
     activation precision; against the exact weights the fp16 weights cost
     ~2^-12 per weight, under the 1e-3 bar."""
     rows, k, m = 700, 4096, 64

@@ -2,7 +2,8 @@
 projection part of qw35_metal_runtime_eval_tokens (qw35-server/src/metal/
 bridge/Qw35FFI.h:97-105; evalTokens, Qw35MetalRuntime.m:1227-1333), on the
 synthetic GGUF images of test_gpu_runtime.py (q8_0 mixers, GF4 FFN, Q6_K head)
-and on one with Q4_K projections (fp16 prefill images made by the runtime).
+and on one with Q4_K mixers (dequantised in the kernel) and a Q5_K FFN (fp16
+prefill images made by the runtime).
 
 * Chunks of 9, 128 and 256 tokens (the reference server's default chunk is
   128, its maximum 256: qw35-server/src/model.rs:30-31): every output -- the
@@ -223,14 +224,14 @@ def test_short_chunk_runs_the_decode_gemvs(cuda, small):
 
 
 def test_chunk_with_kquant_projections(cuda):
-    """Q4_K mixers and FFN: the runtime makes their fp16 prefill images (the
-    half weights of the reference's tiled matmul, qw35_tiled_mm.metal:199-255)
-    and runs the chunk on them; the same bars."""
+    """Q4_K mixers (dequantised in the prefill kernel) and a Q5_K FFN (the
+    runtime makes its fp16 prefill images): both give the half weights of the
+    reference's tiled matmul, qw35_tiled_mm.metal:199-255; the same bars."""
     from qwowl35_amd import qwen35
     from qwowl35_amd import runtime as rt
 
     hp = _hp()
-    stack = qwen35.ProjectionStack.synthetic(hp, qwen35.StackTypes(mixer=rt.TYPE_Q4_K, ffn=rt.TYPE_Q4_K, head=14),
+    stack = qwen35.ProjectionStack.synthetic(hp, qwen35.StackTypes(mixer=rt.TYPE_Q4_K, ffn=rt.TYPE_Q5_K, head=14),
                                              seed=9, distinct=True, device=cuda)
     r = rt.ProjectionRuntime(_image(stack), hp, vocab=hp.vocab, max_batch=1, prefill_chunk=64)
     norm, core, act = _inputs(cuda, hp, 64, 1024, seed=3)
