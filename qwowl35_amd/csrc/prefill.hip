@@ -111,14 +111,17 @@ __device__ __forceinline__ uint4_t gf4_word_to_bf16x8(uint32_t w) {
 // or in column order for the F16 and q8_0 weight kernels.
 constexpr int kStageThreads = 256;
 
-template <bool A_F32, bool HAS_AWQ, bool GF4_ORDER = true>
+// G: groups of 8 columns each thread keeps in registers between the two
+// passes (ceil(k / 2048), at most 6: k <= 12288); every one of its loads is
+// issued before the first is used (an index past the row re-reads the row's
+// last group and is left out of the maximum and the stores), so a thread
+// waits for one load latency, not G in turn.  Longer rows read the rest again
+// for the second pass.
+template <bool A_F32, bool HAS_AWQ, bool GF4_ORDER, int G>
 __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void* __restrict__ a,
                                                                       const float* __restrict__ awq, int m, int k,
                                                                       uint16_t* __restrict__ a16,
                                                                       float* __restrict__ row_scale) {
-    // Up to 12288 columns stay in registers between the two passes; longer rows
-    // are read again for the second.
-    constexpr int kMaxGroups = 12288 / 8 / kStageThreads;  // resident groups of 8 columns per thread
     constexpr bool HILO = A_F32;
     const int row = blockIdx.x;
     const int groups = k >> 3;
@@ -162,17 +165,21 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
             }
         }
     };
-    float v[kMaxGroups][8];
+    float v[G][8];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const int g = threadIdx.x + j * kStageThreads;
+        load8(g < groups ? g : groups - 1, v[j]);
+    }
     float mx = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxGroups; ++j) {
-        const int g = threadIdx.x + j * kStageThreads;
-        if (g >= groups) break;
-        load8(g, v[j]);
+    for (int j = 0; j < G; ++j) {
+        float mj = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
+        for (int q = 0; q < 8; ++q) mj = fmaxf(mj, fabsf(v[j][q]));
+        if (threadIdx.x + j * kStageThreads < groups) mx = fmaxf(mx, mj);
     }
-    for (int g = threadIdx.x + kMaxGroups * kStageThreads; g < groups; g += kStageThreads) {
+    for (int g = threadIdx.x + G * kStageThreads; g < groups; g += kStageThreads) {
         float t[8];
         load8(g, t);
 #pragma unroll
@@ -205,16 +212,34 @@ __global__ __launch_bounds__(kStageThreads) void prefill_stage_kernel(const void
         }
     };
 #pragma unroll
-    for (int j = 0; j < kMaxGroups; ++j) {
+    for (int j = 0; j < G; ++j) {
         const int g = threadIdx.x + j * kStageThreads;
-        if (g >= groups) break;
-        store8(g, v[j]);
+        if (g < groups) store8(g, v[j]);
     }
-    for (int g = threadIdx.x + kMaxGroups * kStageThreads; g < groups; g += kStageThreads) {
+    for (int g = threadIdx.x + G * kStageThreads; g < groups; g += kStageThreads) {
         float t[8];
         load8(g, t);
         store8(g, t);
     }
+}
+
+// The staging launch: G from k (groups of 8 columns per thread held in registers).
+template <bool A_F32, bool HAS_AWQ, bool GF4_ORDER>
+void launch_stage(unsigned grid, hipStream_t stream, const void* a, const float* awq, int m, int k, uint16_t* a16,
+                  float* rs) {
+    const int g = (k / 8 + kStageThreads - 1) / kStageThreads;
+#define QW35_STAGE_G(GG)                                                                                        \
+    hipLaunchKernelGGL((prefill_stage_kernel<A_F32, HAS_AWQ, GF4_ORDER, GG>), dim3(grid), dim3(kStageThreads), 0, \
+                       stream, a, awq, m, k, a16, rs)
+    switch (g <= 1 ? 1 : g >= 6 ? 6 : g) {
+        case 1: QW35_STAGE_G(1); break;
+        case 2: QW35_STAGE_G(2); break;
+        case 3: QW35_STAGE_G(3); break;
+        case 4: QW35_STAGE_G(4); break;
+        case 5: QW35_STAGE_G(5); break;
+        default: QW35_STAGE_G(6); break;
+    }
+#undef QW35_STAGE_G
 }
 
 // Staged rows for m tokens: one per token, or (fp32 input) a hi and a lo row
@@ -854,6 +879,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 // written through the epilogue (fp32 C).  One thread per 4 consecutive
 // outputs of a row.
 constexpr int kReduceThreads = 256;
+constexpr int kMaxPrefillSplits = 16;  // plan_prefill splits K at most 16 ways
 
 template <bool OUT_F32>
 __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const float* __restrict__ partial,
@@ -872,12 +898,20 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     float d[4] = {0.f, 0.f, 0.f, 0.f};
     const bool vec = (n & 3) == 0 && ((uintptr_t)c & 15) == 0;
     if (vec) {
-        for (int sp = 0; sp < splits; ++sp) {
-            const float4_t v = *reinterpret_cast<const float4_t*>(partial + sp * stride + o);
-            d[0] += v.x;
-            d[1] += v.y;
-            d[2] += v.z;
-            d[3] += v.w;
+        // every split's load in flight before the first add (splits <= 16 is
+        // uniform), then the sum in split order
+        float4_t v[kMaxPrefillSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMaxPrefillSplits; ++sp)
+            if (sp < splits) v[sp] = *reinterpret_cast<const float4_t*>(partial + sp * stride + o);
+#pragma unroll
+        for (int sp = 0; sp < kMaxPrefillSplits; ++sp) {
+            if (sp < splits) {
+                d[0] += v[sp].x;
+                d[1] += v[sp].y;
+                d[2] += v[sp].z;
+                d[3] += v[sp].w;
+            }
         }
     } else {
         for (int sp = 0; sp < splits; ++sp)
@@ -1114,7 +1148,7 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
     // often as a 128-token tile; take the latter with twice the K split.
     // Same-box sweep, bf16 activations, 4096x12288 M = 128: {64, split 4,
     // halves} 44.0 us -> {128, split 8, halves} 37.3 us.
-    if (q4w && !hilo && best.bm == 64 && m > 64 && chunks % (2 * best.splits * best.kh) == 0 &&
+    if (q4w && !hilo && best.bm == 64 && m > 64 && 2 * best.splits <= 16 && chunks % (2 * best.splits * best.kh) == 0 &&
         k / (2 * best.splits * best.kh) >= 512) {
         best.bm = 128;
         best.splits *= 2;
@@ -1217,7 +1251,8 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     bool af = a_f32 != 0, aw = awq != nullptr;
     const bool of = out_f32 != 0;
     if (workspace) {
-        if (cfg.splits < 1 || (cfg.kh != 1 && cfg.kh != 2 && cfg.kh != 4) || k % cfg.splits != 0 ||
+        if (cfg.splits < 1 || cfg.splits > kMaxPrefillSplits || (cfg.kh != 1 && cfg.kh != 2 && cfg.kh != 4) ||
+            k % cfg.splits != 0 ||
             (k / cfg.splits) % (256 * cfg.kh) != 0)
             return hipErrorInvalidValue;
         // fp32 input: hi and lo tiles pair up inside a wave's token tiles
@@ -1235,9 +1270,7 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         float* partial = reinterpret_cast<float*>(ws + round256((size_t)ms * k * 2) + round256((size_t)m * 4));
         const unsigned stage_grid = af ? (unsigned)(ms / 2) : (unsigned)m;
         if (info) info->ws_bytes = gf4_prefill_workspace_bytes(m, rows, k, cfg, af);
-#define QW35_STAGE(AF, AW, ORD)                                                                                   \
-    hipLaunchKernelGGL((prefill_stage_kernel<AF, AW, ORD>), dim3(stage_grid), dim3(kStageThreads), 0, stream, a, \
-                       awq, m, k, a16, rs)
+#define QW35_STAGE(AF, AW, ORD) launch_stage<AF, AW, ORD>(stage_grid, stream, a, awq, m, k, a16, rs)
         if (info || staged) {
             // described only, or the workspace already holds these activations staged
         } else if (f16w || q8w || q4w) {
