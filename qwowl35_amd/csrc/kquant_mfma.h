@@ -332,12 +332,14 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
             }
             if (HAS_AWQ) av[sl] = *reinterpret_cast<const float4_t*>(args.awq + (size_t)chunk * 256 + 4 * lane);
         }
+        // Tile-major issue order (the order the tiles are consumed in), so that
+        // tile t can be decoded while the loads of the tiles after it are in flight.
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? wmat : args.w_up) +
-                                   (size_t)row0 * row_bytes + chunk_seg_base<FMT>(chunk);
+        for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int t = 0; t < RT; ++t)
+            for (int m = 0; m < NM; ++m) {
+                const uint8_t* wbase = static_cast<const uint8_t*>(m == 0 ? wmat : args.w_up) +
+                                       (size_t)row0 * row_bytes + chunk_seg_base<FMT>(chunk);
 #pragma unroll
                 for (int i = 0; i < LPT; ++i) {
                     if constexpr (FMT == kFmtQ6K) {
@@ -385,7 +387,9 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
             constexpr int c = decltype(CI)::value;
             constexpr int sl = c % P;
             constexpr int later = (CPW - 1 - c) < (P - 1) ? (CPW - 1 - c) : (P - 1);  // chunks issued after c
-            kq_wait_vmcnt<later * LPC>();
+            // chunk c's activations (issued before its weights); each tile's weight
+            // loads are waited for where the tile is first read
+            kq_wait_vmcnt<later * LPC + WPC>();
             const bool live = rb + c * KS + wave < cps;
             if (live) {
                 // Stage chunk c's activations: fp16 hi/lo with a per-chunk power-of-two
