@@ -647,8 +647,13 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                             const float4_t sxd = *reinterpret_cast<const float4_t*>(sx + b1 * 8 + 4);
                             const float sx0[8] = {sxa[0], sxa[1], sxa[2], sxa[3], sxb[0], sxb[1], sxb[2], sxb[3]};
                             const float sx1[8] = {sxc[0], sxc[1], sxc[2], sxc[3], sxd[0], sxd[1], sxd[2], sxd[3]};
-                            // Sub-block scales as exact fp16 pairs (sc_2i, sc_2i+1) and their
-                            // -1024 multiples (|sc| < 64, so -1024 sc is exact).
+                            // Q4_K's odd sub-blocks (the high nibbles) are decoded in place:
+                            // the masked byte 16q under exponent byte 0x54 is the fp16 64 + q
+                            // (ulp 1/16 at 64), which saves the shift of the low-nibble path.
+                            constexpr bool kHiInPlace = FMT == kFmtQ4K;
+                            // Sub-block scales as exact fp16 pairs (sc_2i, sc_2i+1) and the
+                            // bias multiples of their biased codes: -1024 sc (1024 + q) and, for
+                            // in-place high nibbles, -64 sc (64 + q); |sc| < 64, so both are exact.
                             half2_t scp[4], nbp[4];
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
@@ -656,11 +661,11 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                                 scp[i] = as_half2(__builtin_amdgcn_perm(0x64646464u, w,
                                                                         (i & 1) ? 0x04030402u : 0x04010400u)) +
                                          h2(-1024.0f, -1024.0f);
-                                nbp[i] = scp[i] * h2(-1024.0f, -1024.0f);
+                                nbp[i] = scp[i] * (kHiInPlace ? h2(-1024.0f, -64.0f) : h2(-1024.0f, -1024.0f));
                             }
-                            // B = sc_j * q as one fused multiply-add of the biased 1024 + q:
-                            // (1024 + q) sc - 1024 sc = sc q <= 63 * 31, exact; the eight MFMAs
-                            // then accumulate sum_j sc_j sum q x in one register set.
+                            // B = sc_j * q as one fused multiply-add of the biased code:
+                            // (1024 + q) sc - 1024 sc = sc q <= 63 * 31, exact (64 + q likewise);
+                            // the eight MFMAs then accumulate sum_j sc_j sum q x in one register set.
                             // Q5_K: bit j of qh byte l (bytes 8kq.. of this lane) is bit 4 of q.
                             constexpr int kQs = FMT == kFmtQ5K ? 48 : 16;
                             const uint2_t_ qh = FMT == kFmtQ5K ? *reinterpret_cast<const uint2_t_*>(wrow + 16 + 8 * kq)
@@ -672,8 +677,10 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
 #pragma unroll
                                 for (int hi = 0; hi < 2; ++hi) {
                                     const int j = 2 * cc + hi;
-                                    uint32_t t0 = (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
-                                    uint32_t t1 = (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
+                                    const bool in_place = kHiInPlace && hi;
+                                    const uint32_t ebase = in_place ? 0x54545454u : 0x64646464u;
+                                    uint32_t t0 = in_place ? qd.x & 0xF0F0F0F0u : (hi ? (qd.x >> 4) : qd.x) & 0x0F0F0F0Fu;
+                                    uint32_t t1 = in_place ? qd.y & 0xF0F0F0F0u : (hi ? (qd.y >> 4) : qd.y) & 0x0F0F0F0Fu;
                                     if constexpr (FMT == kFmtQ5K) {
                                         const uint32_t h0 = j <= 4 ? qh.x << (4 - j) : qh.x >> (j - 4);
                                         const uint32_t h1 = j <= 4 ? qh.y << (4 - j) : qh.y >> (j - 4);
@@ -685,13 +692,13 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                                     const half2_t n2 = (j & 1) ? half2_t{np.y, np.y} : half2_t{np.x, np.x};
                                     uint32_t b4[4];
                                     b4[0] = as_u32(__builtin_elementwise_fma(
-                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04010400u)), s2, n2));
+                                        as_half2(__builtin_amdgcn_perm(ebase, t0, 0x04010400u)), s2, n2));
                                     b4[1] = as_u32(__builtin_elementwise_fma(
-                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t0, 0x04030402u)), s2, n2));
+                                        as_half2(__builtin_amdgcn_perm(ebase, t0, 0x04030402u)), s2, n2));
                                     b4[2] = as_u32(__builtin_elementwise_fma(
-                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04010400u)), s2, n2));
+                                        as_half2(__builtin_amdgcn_perm(ebase, t1, 0x04010400u)), s2, n2));
                                     b4[3] = as_u32(__builtin_elementwise_fma(
-                                        as_half2(__builtin_amdgcn_perm(0x64646464u, t1, 0x04030402u)), s2, n2));
+                                        as_half2(__builtin_amdgcn_perm(ebase, t1, 0x04030402u)), s2, n2));
                                     const half8_t bop =
                                         __builtin_bit_cast(half8_t, uint4_t{b4[0], b4[1], b4[2], b4[3]});
                                     const half8_t aop = *reinterpret_cast<const half8_t*>(arow + a_step * j + 8 * kq);
@@ -700,12 +707,23 @@ __device__ __forceinline__ void kq_gemv_body(GemvArgs args) {
                             }
                             // y += d sum_j sc_j sum q x - dmin sum_j m_j sum x
                             float ms0 = 0.0f, ms1 = 0.0f;
+                            if constexpr (NB == 1) {
+                                // The four lane groups hold the same batch row: group kq takes
+                                // sub-blocks 2kq and 2kq + 1, and the groups' sums are added.
+                                const uint32_t mnw = (kq < 2 ? mn_lo : mn_hi) >> (16 * (kq & 1));
+                                const float2_t s2x = *reinterpret_cast<const float2_t*>(sx + 2 * kq);
+                                float pm = __builtin_fmaf((float)((mnw >> 8) & 0xFFu), s2x[1],
+                                                          (float)(mnw & 0xFFu) * s2x[0]);
+                                pm += __shfl_xor(pm, 16);
+                                ms0 = pm + __shfl_xor(pm, 32);
+                            } else {
 #pragma unroll
-                            for (int j = 0; j < 8; ++j) {
-                                const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
-                                const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
-                                ms0 = __builtin_fmaf(mnj, sx0[j], ms0);
-                                if constexpr (NB > 1) ms1 = __builtin_fmaf(mnj, sx1[j], ms1);
+                                for (int j = 0; j < 8; ++j) {
+                                    const uint32_t mnw = j < 4 ? mn_lo : mn_hi;
+                                    const float mnj = (float)((mnw >> (8 * (j & 3))) & 0xFFu);
+                                    ms0 = __builtin_fmaf(mnj, sx0[j], ms0);
+                                    ms1 = __builtin_fmaf(mnj, sx1[j], ms1);
+                                }
                             }
                             const float v0 = __builtin_fmaf(-dmin, ms0, d * (dd[0] + dd[1]));
                             acc[t][m][0] = __builtin_fmaf(inv_sc[0], v0, acc[t][m][0]);
