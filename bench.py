@@ -424,7 +424,7 @@ def bench_q4k(b: Bench, cpu: CpuBaseline | None, steps: int, warmup: int) -> dic
     return out
 
 
-def bench_q6k_head(b: Bench, steps: int) -> dict:
+def bench_q6k_head(b: Bench, steps: int, cpu: CpuBaseline | None = None) -> dict:
     """The 9B LM head as the reference requires it (Q6_K, 248320 x 4096,
     Qw35MetalRuntime.m:202-208): the full-logits GEMV and the fused greedy
     head (GEMV + per-workgroup argmax + reduction, no logits written), b1 and b8."""
@@ -434,7 +434,16 @@ def bench_q6k_head(b: Bench, steps: int) -> dict:
     wbytes = head.storage.numel()
     out = {}
     for nb in (1, 8):
-        out[f"q6_k_head_b{nb}_248320x4096"] = gemv_line(b, [head], nb, 200, 20)
+        line = out[f"q6_k_head_b{nb}_248320x4096"] = gemv_line(b, [head], nb, 200, 20)
+        if cpu is not None:
+            # a sample of 1/64 of the rows (3880 x 4096; the numpy Q6_K unpacking
+            # is ~10x slower per row than Q4_K's), time scaled by 64
+            rows = vocab // 64
+            raw = host_bytes(head)[: rows * rt.row_bytes(rt.TYPE_Q6_K, hidden)]
+            t_dq, t_mv = cpu.gemv(rt.TYPE_Q6_K, raw, rows, hidden, nb)
+            line["cpu_baseline"] = cpu.record(round(line["bytes"] / (64 * (t_dq + t_mv)) / 1e9, 3), "GB/s",
+                                              f"Q6_K head b{nb}: 3880 of the 248320 rows (dequant "
+                                              f"{t_dq * 1e3:.1f} ms + matvec {t_mv * 1e3:.2f} ms), scaled by 64")
         x = b.normal((nb, hidden))
         ws = rt.output_argmax_workspace(head, nb, device=b.dev)
         ms, _ = b.time_launches([lambda s: rt.output_argmax(head, x, workspace=ws, stream=s)], 200, 20)
@@ -712,7 +721,7 @@ def main() -> int:
     if "q4k" in want:
         extra.update(bench_q4k(b, cpu, args.steps, args.warmup))
     if "q6k" in want:
-        extra.update(bench_q6k_head(b, args.steps))
+        extra.update(bench_q6k_head(b, args.steps, cpu))
     if "codecs" in want:
         extra.update(bench_codecs(b, args.steps // 4, args.warmup // 2))
     if "prefill" in want:
