@@ -281,7 +281,16 @@ typedef struct {
     uint64_t workspace_bytes;
 } qw35_hip_plan_op;
 
-/* Validate the ops (same rules as the single calls) and record them; NULL on
+/* Consecutive ops over the same x, awq and batch may be recorded as one
+ * launch: MATVEC ops of a q8_0 / Q4_K / Q6_K type with disjoint outputs, and
+ * MATMUL ops of one weight form and k with the same workspace and residual
+ * flag, row counts that are multiples of 4 and disjoint outputs (a mixer's
+ * input projections); up to 4 ops per launch.  A merged MATMUL launch is
+ * planned for the summed rows, so its outputs may differ from the single
+ * calls' in the last bits (the K split and the order of the partial sums),
+ * not in precision.
+ *
+ * Validate the ops (same rules as the single calls) and record them; NULL on
  * error.  Recording launches nothing.  A plan whose launches split K (see
  * qw35_hip_decode_matvec_ws) allocates and zeroes one workspace for them at
  * creation, freed by qw35_hip_plan_destroy; replays of one plan must not

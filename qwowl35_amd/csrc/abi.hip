@@ -275,6 +275,23 @@ bool check_matmul_op(const qw35_hip_plan_op& o, const char* what, char* err, uin
     return true;
 }
 
+// Consecutive MATMUL ops over the same activations (a mixer's input
+// projections) share one prefill launch: same weight form and k, same x, AWQ,
+// token count, workspace and epilogue, row counts that are multiples of 4, and
+// no op's output overlapping another's or the shared inputs.
+bool prefill_mergeable(const qw35_hip_plan_op& a, const qw35_hip_plan_op& b) {
+    if (a.kind != QW35_HIP_OP_MATMUL || b.kind != QW35_HIP_OP_MATMUL) return false;
+    if (prefill_wkind(b.w->type_id) != prefill_wkind(a.w->type_id) || b.w->k != a.w->k || b.x != a.x ||
+        b.awq != a.awq || b.n_batch != a.n_batch || b.workspace != a.workspace ||
+        b.workspace_bytes != a.workspace_bytes || (b.residual != 0) != (a.residual != 0) || a.w->rows % 4 != 0 ||
+        b.w->rows % 4 != 0)
+        return false;
+    const uint64_t xa = (uint64_t)a.n_batch * a.w->k * 4, wa = a.awq ? a.w->k * 4 : 0;
+    const uint64_t da = (uint64_t)a.n_batch * a.w->rows * 4, db = (uint64_t)b.n_batch * b.w->rows * 4;
+    return !overlaps(a.dst, da, b.dst, db) && !overlaps(a.x, xa, a.dst, da) && !overlaps(a.x, xa, b.dst, db) &&
+           !(a.awq && (overlaps(a.awq, wa, a.dst, da) || overlaps(a.awq, wa, b.dst, db)));
+}
+
 // Greedy head workspace: per batch row, one (token, logit) partial per
 // workgroup of the GEMV launch; tokens first, logits at a 256-byte boundary.
 uint64_t argmax_ws_part(const qw35_hip_weight* w, uint32_t n_batch) {
@@ -500,8 +517,28 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
         for (uint32_t i = 0; i < n_ops && launch == hipSuccess;) {
             const qw35_hip_plan_op& o = ops[i];
             if (o.kind == QW35_HIP_OP_MATMUL || o.kind == QW35_HIP_OP_MATMUL_SWIGLU) {
+                const bool sw = o.kind == QW35_HIP_OP_MATMUL_SWIGLU;
+                // ops [i, j) run as one launch (segments) when mergeable
+                uint32_t j = i + 1;
+                while (!sw && j < n_ops && j - i < (uint32_t)qw35::kMaxSegments) {
+                    bool ok = true;
+                    for (uint32_t q = i; q < j && ok; ++q) ok = prefill_mergeable(ops[q], ops[j]);
+                    if (!ok) break;
+                    ++j;
+                }
                 if (pass == 1) {
-                    const bool sw = o.kind == QW35_HIP_OP_MATMUL_SWIGLU;
+                    qw35::PrefillSegs segs;
+                    uint64_t rows = o.w->rows;
+                    if (j - i > 1) {
+                        segs.n = (int)(j - i);
+                        rows = 0;
+                        for (uint32_t q = i; q < j; ++q) {
+                            segs.w[q - i] = ops[q].w->data;
+                            segs.c[q - i] = ops[q].dst;
+                            segs.rows[q - i] = (int)ops[q].w->rows;
+                            rows += ops[q].w->rows;
+                        }
+                    }
                     auto mm = [&](const qw35_hip_weight* w, uint32_t epi) {
                         // The staging pass is skipped when the previous prefill launch
                         // of the plan staged the same activations the same way into
@@ -509,13 +546,21 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                         const int wkind = prefill_wkind(w->type_id);
                         const StageKey key{o.x, o.awq, o.workspace, o.n_batch, (uint32_t)w->k, wkind == 0};
                         const bool staged = stage_valid && key == stage_key;
-                        const hipError_t e = qw35::launch_prefill(wkind, w->data, (int)w->rows, (int)w->k, o.x, 1,
-                                                                  o.awq, o.dst, (int)o.n_batch, 1, o.workspace,
-                                                                  o.workspace_bytes, s, (int)epi, nullptr, staged);
+                        const bool multi = segs.n > 1 && w == o.w;
+                        const hipError_t e = qw35::launch_prefill(
+                            wkind, w->data, multi ? (int)rows : (int)w->rows, (int)w->k, o.x, 1, o.awq, o.dst,
+                            (int)o.n_batch, 1, o.workspace, o.workspace_bytes, s, (int)epi, nullptr, staged,
+                            multi ? &segs : nullptr);
                         stage_key = key;
-                        // this launch's output may be the next one's input
-                        const uint64_t xb = (uint64_t)o.n_batch * w->k * 4, db = (uint64_t)o.n_batch * w->rows * 4;
-                        stage_valid = !overlaps(o.dst, db, o.x, xb) && !(o.awq && overlaps(o.dst, db, o.awq, w->k * 4));
+                        // this launch's outputs may be the next one's input
+                        const uint64_t xb = (uint64_t)o.n_batch * w->k * 4;
+                        stage_valid = true;
+                        for (uint32_t q = i; q < (multi ? j : i + 1); ++q) {
+                            const uint64_t db = (uint64_t)o.n_batch * ops[q].w->rows * 4;
+                            const void* d = multi ? ops[q].dst : o.dst;
+                            if (overlaps(d, db, o.x, xb) || (o.awq && overlaps(d, db, o.awq, w->k * 4)))
+                                stage_valid = false;
+                        }
                         return e;
                     };
                     launch = mm(o.w, sw          ? QW35_HIP_EPILOGUE_STORE
@@ -523,7 +568,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                                                   : QW35_HIP_EPILOGUE_STORE);
                     if (launch == hipSuccess && sw) launch = mm(o.w_up, QW35_HIP_EPILOGUE_SWIGLU);
                 }
-                ++i;
+                i = j;
                 continue;
             }
             stage_valid = false;  // GEMV outputs are not tracked against the staged activations

@@ -62,6 +62,16 @@ struct PrefillArgs {
     int tiles_m, tiles_n;
     int splits;              // staged path: K split this many ways (1: none)
     int k_len;               // columns per split
+    // Staged path, n_seg > 1: up to kMaxSegments matrices over the same
+    // activations in one launch.  Segment s has seg_n[s] rows, its weights at
+    // seg_w[s] and its own output seg_c[s] ([m_out][seg_n[s]]); its blocks are
+    // the seg_tiles[s] weight tiles after those of the segments before it.
+    // Split launches write the partial sums of all segments as one
+    // [m_out][n] array (n = the sum of seg_n), segment s at column seg_col[s].
+    int n_seg;
+    int seg_n[kMaxSegments], seg_col[kMaxSegments], seg_tiles[kMaxSegments];
+    const void* seg_w[kMaxSegments];
+    void* seg_c[kMaxSegments];
 };
 
 // How a result r is written to fp32 c.
@@ -534,12 +544,34 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const int split = t / tiles;
     t -= split * tiles;
     const int m0 = (t % p.tiles_m) * BM;
+    // The block's matrix (uniform): its weights, rows, output and the output's
+    // row stride and first column.
+    int tn = t / p.tiles_m;
+    const uint32_t* W = p.w;
+    int N = p.n;
+    void* C = p.c;
+    int ld = p.n, col0 = 0;
+    if (p.n_seg > 1) {
+        int sg = 0;
+        while (sg + 1 < p.n_seg && tn >= p.seg_tiles[sg]) {
+            tn -= p.seg_tiles[sg];
+            ++sg;
+        }
+        W = static_cast<const uint32_t*>(p.seg_w[sg]);
+        N = p.seg_n[sg];
+        if (p.splits > 1) {
+            col0 = p.seg_col[sg];  // C: the partial sums of all segments, ld = p.n
+        } else {
+            C = p.seg_c[sg];
+            ld = N;
+        }
+    }
     // KH = 2 (4): waves [kh NWG, (kh + 1) NWG) take part kh of the block's K
     // range, two halves (four quarters), over the same rows, each part with its
     // own token tile; the parts are summed in LDS at the end.
     const int kh = KH > 1 ? wave / NWG : 0;
     const int tg = tid - kh * NTG;
-    const int n0 = (t / p.tiles_m) * BN + (wave - kh * NWG) * 32 * FN;
+    const int n0 = tn * BN + (wave - kh * NWG) * 32 * FN;
     const int K = p.k;
     const int k_len = p.k_len / KH;
     const int k_begin = split * p.k_len + kh * k_len;
@@ -561,15 +593,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const uint8_t* w_src[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const size_t row = (size_t)min(n0 + 32 * j + l32, p.n - 1);
+        const size_t row = (size_t)min(n0 + 32 * j + l32, N - 1);
         if constexpr (Q4W)
-            w_src[j] = reinterpret_cast<const uint8_t*>(p.w) + row * (size_t)(K / 256 * 144) + (k_begin / 256) * 144;
+            w_src[j] = reinterpret_cast<const uint8_t*>(W) + row * (size_t)(K / 256 * 144) + (k_begin / 256) * 144;
         else if constexpr (Q8W)
-            w_src[j] = reinterpret_cast<const uint8_t*>(p.w) + row * (size_t)(K / 32 * 34) + (k_begin / 32) * 34 +
+            w_src[j] = reinterpret_cast<const uint8_t*>(W) + row * (size_t)(K / 32 * 34) + (k_begin / 32) * 34 +
                        32 * half;
         else
-            w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(p.w) + (row * K + k_begin + 32 * half) * 2
-                            : reinterpret_cast<const uint8_t*>(p.w + row * words_per_row + (k_begin >> 3) + 4 * half);
+            w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(W) + (row * K + k_begin + 32 * half) * 2
+                            : reinterpret_cast<const uint8_t*>(W + row * words_per_row + (k_begin >> 3) + 4 * half);
     }
     // Q8W: byte selectors for this lane half (span dword i -> q dword i; d -> (d, d))
     const uint32_t q8_sel = half ? 0x07060504u : 0x05040302u;
@@ -809,8 +841,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
     // Split launches write unscaled fp32 partial sums, split s at
     // c + s * m_out * n (OUT_F32 is then true); prefill_split_reduce finishes.
-    void* const c = OUT_F32 ? static_cast<void*>(static_cast<float*>(p.c) + (size_t)split * p.m_out * p.n) : p.c;
-    const bool vec_ok = (p.n & 3) == 0 && ((uintptr_t)p.c & 15) == 0;
+    void* const c = OUT_F32 ? static_cast<void*>(static_cast<float*>(C) + (size_t)split * p.m_out * ld + col0) : C;
+    const bool vec_ok = (ld & 3) == 0 && (col0 & 3) == 0 && ((uintptr_t)C & 15) == 0;
     // split launches write partial sums; the reduction applies the epilogue
     const int epi = OUT_F32 && p.splits == 1 ? p.epi : kEpiStore;
     // token gm's 4 x 4 outputs of weight tile j: d(g, r) is row n0 + 32 j + 8 g + 4 half + r
@@ -818,9 +850,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int gn = n0 + 32 * j + 8 * g + 4 * half;
-            const size_t o = (size_t)gm * p.n + gn;
+            const size_t o = (size_t)gm * ld + gn;
             float d[4] = {d_of(g, 0) * rs, d_of(g, 1) * rs, d_of(g, 2) * rs, d_of(g, 3) * rs};
-            if (vec_ok && gn + 3 < p.n) {
+            if (vec_ok && gn + 3 < N) {
                 if constexpr (OUT_F32) {
                     float4_t* const dst = reinterpret_cast<float4_t*>(static_cast<float*>(c) + o);
                     if (epi != kEpiStore) {
@@ -836,7 +868,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if (gn + r < p.n) {
+                    if (gn + r < N) {
                         if constexpr (OUT_F32) {
                             float* const dst = static_cast<float*>(c) + o + r;
                             *dst = epi != kEpiStore ? epilogue(epi, *dst, d[r]) : d[r];
@@ -877,26 +909,39 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 
 // C[m][n] = row_scale[m] * sum_s partial[s][m][n], splits summed in order,
 // written through the epilogue (fp32 C).  One thread per 4 consecutive
-// outputs of a row.
+// outputs of a row.  Segment launches: columns [col[s], col[s] + n[s]) of the
+// partial sums are segment s's output c[s] ([m][n[s]]; every n[s] a multiple
+// of 4, so no 4-column group straddles two segments).
 constexpr int kReduceThreads = 256;
 constexpr int kMaxPrefillSplits = 16;  // plan_prefill splits K at most 16 ways
+
+struct ReduceOut {
+    int n_seg;  // 1: c[0] is [m][n]
+    void* c[kMaxSegments];
+    int n[kMaxSegments], col[kMaxSegments];
+};
 
 template <bool OUT_F32>
 __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const float* __restrict__ partial,
                                                                        int splits, int m, int n,
                                                                        const float* __restrict__ row_scale,
-                                                                       void* __restrict__ c, int epi) {
+                                                                       ReduceOut out, int epi) {
     const int n4 = (n + 3) >> 2;
     const size_t idx = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
     if (idx >= (size_t)m * n4) return;
     const int row = (int)(idx / n4);
     const int col = (int)(idx - (size_t)row * n4) * 4;
-    const size_t o = (size_t)row * n + col;
     const size_t stride = (size_t)m * n;
     const float rs = row_scale[row];
     const int cnt = min(4, n - col);
     float d[4] = {0.f, 0.f, 0.f, 0.f};
-    const bool vec = (n & 3) == 0 && ((uintptr_t)c & 15) == 0;
+    int sg = 0;
+    while (sg + 1 < out.n_seg && col >= out.col[sg + 1]) ++sg;
+    void* const c = out.c[sg];
+    const int nc = out.n_seg > 1 ? out.n[sg] : n;  // the output's row length
+    const size_t oc = (size_t)row * nc + (col - (out.n_seg > 1 ? out.col[sg] : 0));
+    const size_t o = (size_t)row * n + col;
+    const bool vec = (n & 3) == 0 && (nc & 3) == 0 && ((uintptr_t)c & 15) == 0;
     if (vec) {
         // every split's load in flight before the first add (splits <= 16 is
         // uniform), then the sum in split order
@@ -921,7 +966,7 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     for (int r = 0; r < 4; ++r) d[r] *= rs;
     if (vec) {
         if constexpr (OUT_F32) {
-            float4_t* const dst = reinterpret_cast<float4_t*>(static_cast<float*>(c) + o);
+            float4_t* const dst = reinterpret_cast<float4_t*>(static_cast<float*>(c) + oc);
             if (epi != kEpiStore) {
                 const float4_t old = *dst;
 #pragma unroll
@@ -930,16 +975,16 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
             *dst = float4_t{d[0], d[1], d[2], d[3]};
         } else {
             typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + o) =
+            *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(c) + oc) =
                 uint2_t{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
         }
     } else {
         for (int r = 0; r < cnt; ++r) {
             if constexpr (OUT_F32) {
-                float* const dst = static_cast<float*>(c) + o + r;
+                float* const dst = static_cast<float*>(c) + oc + r;
                 *dst = epi != kEpiStore ? epilogue(epi, *dst, d[r]) : d[r];
             } else {
-                static_cast<uint16_t*>(c)[o + r] = (uint16_t)pack_bf16(d[r], 0.0f);
+                static_cast<uint16_t*>(c)[oc + r] = (uint16_t)pack_bf16(d[r], 0.0f);
             }
         }
     }
@@ -953,6 +998,13 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     PrefillArgs p = a;
     p.tiles_m = (a.m + BM - 1) / BM;
     p.tiles_n = (a.n + BN - 1) / BN;
+    if (a.n_seg > 1) {
+        p.tiles_n = 0;
+        for (int s = 0; s < a.n_seg; ++s) {
+            p.seg_tiles[s] = (a.seg_n[s] + BN - 1) / BN;
+            p.tiles_n += p.seg_tiles[s];
+        }
+    }
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (a.info) {
         snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s>", BM,
@@ -1229,7 +1281,8 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 // workspace).
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
-                                  hipStream_t stream, int wkind, int epi, LaunchInfo* info, bool staged) {
+                                  hipStream_t stream, int wkind, int epi, LaunchInfo* info, bool staged,
+                                  const PrefillSegs* segs) {
     const bool f16w = wkind == 1, q8w = wkind == 2, q4w = wkind == 3;
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
@@ -1244,6 +1297,28 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
     // epilogues read fp32 c; the path without a workspace has none
     if (epi != kEpiStore && (!out_f32 || !workspace)) return hipErrorInvalidValue;
     if (epi < kEpiStore || epi > kEpiSwiglu) return hipErrorInvalidValue;
+    ReduceOut out{};
+    out.n_seg = 1;
+    out.c[0] = c;
+    if (segs && segs->n > 1) {
+        // segments: staged path only, rows = their sum, each a multiple of 4
+        if (!workspace || segs->n > kMaxSegments) return hipErrorInvalidValue;
+        int total = 0;
+        for (int s = 0; s < segs->n; ++s) {
+            if (segs->rows[s] < 1 || segs->rows[s] % 4 != 0 || !segs->w[s] || !segs->c[s])
+                return hipErrorInvalidValue;
+            p.seg_w[s] = segs->w[s];
+            p.seg_c[s] = segs->c[s];
+            p.seg_n[s] = segs->rows[s];
+            p.seg_col[s] = total;
+            out.c[s] = segs->c[s];
+            out.n[s] = segs->rows[s];
+            out.col[s] = total;
+            total += segs->rows[s];
+        }
+        if (total != rows) return hipErrorInvalidValue;
+        p.n_seg = out.n_seg = segs->n;
+    }
     p.n = rows;
     p.k = k;
     p.splits = 1;
@@ -1363,13 +1438,14 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const dim3 grid((unsigned)((threads + kReduceThreads - 1) / kReduceThreads));
         if (of)
             hipLaunchKernelGGL((prefill_split_reduce<true>), grid, dim3(kReduceThreads), 0, stream, partial,
-                               cfg.splits, m, rows, rs, c, epi);
+                               cfg.splits, m, rows, rs, out, epi);
         else
             hipLaunchKernelGGL((prefill_split_reduce<false>), grid, dim3(kReduceThreads), 0, stream, partial,
-                               cfg.splits, m, rows, rs, c, kEpiStore);
+                               cfg.splits, m, rows, rs, out, kEpiStore);
         return hipGetLastError();
     }
     // Direct path: largest tile that still gives every CU a block.
+    if (p.n_seg > 1) return hipErrorInvalidValue;
     const long cus = num_cus();
     auto tiles = [&](int bm, int bn) { return (long)((m + bm - 1) / bm) * ((rows + bn - 1) / bn); };
     if (!af && tiles(256, 128) >= cus) return launch_tile<256, 128, 4, 2>(p, af, aw, of, stream);
@@ -1379,13 +1455,13 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
 
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                           void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                          int epi, LaunchInfo* info, bool staged) {
+                          int epi, LaunchInfo* info, bool staged, const PrefillSegs* segs) {
     if (!workspace && wkind != 0) return hipErrorInvalidValue;
     if (staged && !workspace) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
     if (workspace) fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
     return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind, epi, info,
-                                  staged);
+                                  staged, segs);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {

@@ -140,6 +140,17 @@ size_t gf4_prefill_workspace_bytes(int m, int rows, int k, PrefillCfg cfg, bool 
 size_t prefill_workspace_bytes(int m, int rows, int k, int wkind, bool with_f32);
 // Smallest workspace the staged path accepts (no K split).
 size_t prefill_min_workspace_bytes(int m, int rows, int k, bool a_f32);
+// Up to kMaxSegments matrices of one weight form and k that read the same
+// activations (a mixer's input projections), as one staged launch: the
+// weight tiles of all of them form one grid and each writes its own output
+// c[s] ([m][rows[s]]).  rows[s] must be multiples of 4; the launch is planned
+// for their sum, which the rows argument must equal.
+struct PrefillSegs {
+    int n = 0;  // 0 or 1: the single matrix (w, c, rows)
+    const void* w[kMaxSegments] = {};
+    void* c[kMaxSegments] = {};
+    int rows[kMaxSegments] = {};
+};
 // epi (fp32 c with a workspace only): 0 c = r, 1 c += r, 2 c = silu(c) * r.
 // info (host pointer, nullable): describe the matmul launch (name, grid,
 // block, LDS, splits; ws_bytes the workspace it uses) and launch nothing.
@@ -149,10 +160,12 @@ size_t prefill_min_workspace_bytes(int m, int rows, int k, bool a_f32);
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
                                   int wkind = 0, int epi = 0, LaunchInfo* info = nullptr,
-                                  bool staged = false);  // wkind 0 GF4, 1 F16, 2 q8_0
+                                  bool staged = false,  // wkind 0 GF4, 1 F16, 2 q8_0, 3 Q4_K
+                                  const PrefillSegs* segs = nullptr);
 // Planned launch; the workspace is required for F16 and q8_0 weights.
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                           void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                          int epi = 0, LaunchInfo* info = nullptr, bool staged = false);
+                          int epi = 0, LaunchInfo* info = nullptr, bool staged = false,
+                          const PrefillSegs* segs = nullptr);
 
 }  // namespace qw35

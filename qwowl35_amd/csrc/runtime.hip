@@ -38,6 +38,7 @@
 #include <vector>
 
 #include "../../include/qw35_hip.h"
+#include "qw35_kernels.h"
 
 namespace {
 
@@ -449,6 +450,23 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
                     return nullptr;
                 }
                 r->pf_ws_bytes = std::max(r->pf_ws_bytes, b);
+            }
+        }
+        // A layer's mixer input projections of one weight form and k run as one
+        // launch over their summed rows (the plan's segment launches): size that
+        // launch too.
+        for (const Layer& l : r->layers) {
+            for (size_t i = 0; i < l.mix.size();) {
+                qw35_hip_weight merged = l.mix[i].pf;
+                size_t j = i + 1;
+                while (j < l.mix.size() && j - i < (size_t)qw35::kMaxSegments && merged.rows % 4 == 0 &&
+                       l.mix[j].pf.type_id == merged.type_id && l.mix[j].pf.k == merged.k &&
+                       l.mix[j].pf.rows % 4 == 0)
+                    merged.rows += l.mix[j++].pf.rows;
+                if (j - i > 1)
+                    for (uint32_t n = QW35_HIP_MAX_BATCH + 1; n <= prefill_chunk; ++n)
+                        r->pf_ws_bytes = std::max(r->pf_ws_bytes, qw35_hip_matmul_prefill_workspace_size(&merged, n));
+                i = j;
             }
         }
         if (!rt_hip(hipMalloc(&r->pf_ws, r->pf_ws_bytes), "runtime_create: prefill workspace", err, err_len) ||

@@ -282,6 +282,21 @@ def chunk_workspace(stack: ProjectionStack, n_tokens: int, device=None) -> torch
     lib = _ffi.load()
     size = max(int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(w.prefill.view), n_tokens))
                for ws in stack.layers for w in ws.values())
+    # a layer's mixer input projections of one weight form run as one launch
+    # over their summed rows (the plan merges them): size that launch too
+    for il, ws in enumerate(stack.layers):
+        views = [ws[p.name].prefill.view for p in mixer_projections(stack.hp, il)[:-1]]
+        i = 0
+        while i < len(views):
+            merged = _ffi.Weight.from_buffer_copy(views[i])
+            j = i + 1
+            while (j < len(views) and j - i < 4 and merged.rows % 4 == 0 and views[j].type_id == merged.type_id
+                   and views[j].k == merged.k and views[j].rows % 4 == 0):
+                merged.rows += views[j].rows
+                j += 1
+            if j - i > 1:
+                size = max(size, int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(merged), n_tokens)))
+            i = j
     return torch.empty(size, dtype=torch.uint8, device=device or stack.head.storage.device)
 
 

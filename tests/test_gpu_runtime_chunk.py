@@ -9,10 +9,12 @@ prefill images made by the runtime).
   128, its maximum 256: qw35-server/src/model.rs:30-31): every output -- the
   last writer of each mixer buffer, the SwiGLU output, the residual stream
   and the last token's logits -- equals, bit for bit, the same sequence of
-  single calls (qw35_hip_matmul_prefill_epilogue with fp32 activations: STORE
-  for the input projections and ffn_gate, SWIGLU for ffn_up, ADD for the
-  output projections and ffn_down; qw35_hip_decode_matvec for the head on the
-  last token);
+  calls (qw35_hip_matmul_prefill_epilogue with fp32 activations: SWIGLU for
+  ffn_up after ffn_gate's STORE, ADD for the output projections and ffn_down;
+  qw35_hip_decode_matvec for the head on the last token; a layer's mixer input
+  projections as one plan of MATMUL ops, which records them as one merged
+  launch as the runtime does -- tests/test_gpu_prefill_segments.py checks
+  that launch against the single calls);
 * the same outputs on sampled tokens within 1e-3 relative L2 of fp64 on the
   oracle-dequantised weights (the residual stream as act + sum over layers);
 * chunks of up to 8 tokens equal eval_step's projections; the greedy head
@@ -55,17 +57,11 @@ def _inputs(cuda, hp, n, core_k, seed):
 
 
 def _workspace(stack, n, device):
-    """A prefill workspace that holds every projection's planned launch at n tokens."""
-    import ctypes as C
+    """A prefill workspace that holds every projection's planned launch at n
+    tokens, the merged mixer launches included."""
+    from qwowl35_amd import qwen35
 
-    import torch
-
-    from qwowl35_amd import _ffi
-
-    lib = _ffi.load()
-    size = max(int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(w.prefill.view), n))
-               for layer in stack.layers for w in layer.values())
-    return torch.empty(size, dtype=torch.uint8, device=device)
+    return qwen35.chunk_workspace(stack, n, device=device)
 
 
 def _single_calls(stack, n, norm, core, act):
@@ -85,8 +81,14 @@ def _single_calls(stack, n, norm, core, act):
     ffn = torch.empty((n, hp.feed_forward_length), dtype=f32, device=norm.device)
     for il, layer in enumerate(stack.layers):
         projs = qwen35.mixer_projections(hp, il)
+        plan = rt.DecodePlan()
         for p in projs[:-1]:
-            mix[(il, p.name)] = rt.matmul_prefill(layer[p.name].prefill, norm, out_dtype=f32, workspace=ws)
+            mix[(il, p.name)] = torch.empty((n, p.rows), dtype=f32, device=norm.device)
+            plan.matmul(layer[p.name].prefill, norm, mix[(il, p.name)], ws)
+        plan.record()
+        plan.launch()
+        torch.cuda.synchronize()
+        plan.close()
         out = projs[-1]
         rt.matmul_prefill(layer[out.name].prefill, core[:, :out.k].contiguous(), out_dtype=f32, dst=act, workspace=ws,
                           epilogue=_ffi.EPILOGUE_ADD)
