@@ -539,7 +539,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                             rows += ops[q].w->rows;
                         }
                     }
-                    auto mm = [&](const qw35_hip_weight* w, uint32_t epi) {
+                    auto mm = [&](const qw35_hip_weight* w, uint32_t epi, const qw35_hip_weight* w_up) {
                         // The staging pass is skipped when the previous prefill launch
                         // of the plan staged the same activations the same way into
                         // the same workspace, and nothing written since overlaps them.
@@ -550,7 +550,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                         const hipError_t e = qw35::launch_prefill(
                             wkind, w->data, multi ? (int)rows : (int)w->rows, (int)w->k, o.x, 1, o.awq, o.dst,
                             (int)o.n_batch, 1, o.workspace, o.workspace_bytes, s, (int)epi, nullptr, staged,
-                            multi ? &segs : nullptr);
+                            multi ? &segs : nullptr, w_up ? w_up->data : nullptr);
                         stage_key = key;
                         // this launch's outputs may be the next one's input
                         const uint64_t xb = (uint64_t)o.n_batch * w->k * 4;
@@ -563,10 +563,15 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                         }
                         return e;
                     };
+                    // gate/up: one fused launch where the gate's planned launch has that form
+                    const bool fused = sw && qw35::prefill_swiglu_fusable(prefill_wkind(o.w->type_id), (int)o.n_batch,
+                                                                          (int)o.w->rows, (int)o.w->k, 1,
+                                                                          o.workspace_bytes);
                     launch = mm(o.w, sw          ? QW35_HIP_EPILOGUE_STORE
                                      : o.residual ? QW35_HIP_EPILOGUE_ADD
-                                                  : QW35_HIP_EPILOGUE_STORE);
-                    if (launch == hipSuccess && sw) launch = mm(o.w_up, QW35_HIP_EPILOGUE_SWIGLU);
+                                                  : QW35_HIP_EPILOGUE_STORE,
+                                fused ? o.w_up : nullptr);
+                    if (launch == hipSuccess && sw && !fused) launch = mm(o.w_up, QW35_HIP_EPILOGUE_SWIGLU, nullptr);
                 }
                 i = j;
                 continue;

@@ -72,6 +72,9 @@ struct PrefillArgs {
     int seg_n[kMaxSegments], seg_col[kMaxSegments], seg_tiles[kMaxSegments];
     const void* seg_w[kMaxSegments];
     void* seg_c[kMaxSegments];
+    // Fused gate/up (GF4 words, staged path, no split): the up projection's
+    // words; c = silu(gate) * up.
+    const uint32_t* w_up;
 };
 
 // How a result r is written to fp32 c.
@@ -511,19 +514,28 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   weight rounds once -- the exact dequantised value of
 //   qw35_dequant_q4_k_at (qw35_matvec.metal:2-12), then the same fp16 bits as
 //   the F16 prefill image.
+// * SWI (fused gate/up, GF4 words, FN = 2): tile 0 of a wave is 32 rows of the
+//   gate projection and tile 1 the same rows of the up projection (p.w_up);
+//   the epilogue writes silu(g) * u, g and u each the fp32 value the gate
+//   launch (STORE) and the up launch (SWIGLU epilogue) of the same plan would
+//   form -- the same K partition and MFMA order per tile, so the same bits.
 template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false, int KH = 1,
-          bool Q4W = false>
+          bool Q4W = false, bool SWI = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
+    static_assert(!SWI || (FN == 2 && OUT_F32 && !F16W && !Q8W && !Q4W && KH <= 2),
+                  "fused gate/up: GF4 words, a gate and an up tile per wave, K halves at most");
     constexpr int NWG = NW / KH;            // waves per K half
     constexpr int NTG = 64 * NWG;           // threads per K half
-    constexpr int BN = 32 * FN * NWG;
+    constexpr int TPW = SWI ? 1 : FN;       // distinct 32-row output tiles per wave
+    constexpr int BN = 32 * TPW * NWG;
     constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave; FN: 32-row weight tiles per wave
     constexpr int A_CHUNKS = BM * 8 / NTG;  // 16-byte token chunks per thread per step
     constexpr int BUF = BM * kLdsRow;
     static_assert(BM % 32 == 0 && BM * 8 % NTG == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
     static_assert((KH == 1 || KH == 2 || KH == 4) && NW % KH == 0, "one, two or four K parts of equal wave counts");
-    static_assert(KH == 1 || (KH / 2) * NWG * FM * FN * 16 * 64 * 4 <= 2 * KH * BUF,
+    // (the fused gate/up kernel hands its gate and up sums over in two passes)
+    static_assert(KH == 1 || (KH / 2) * NWG * FM * (SWI ? 1 : FN) * 16 * 64 * 4 <= 2 * KH * BUF,
                   "K-part partial sums fit the token buffers");
     typedef float float16_t __attribute__((ext_vector_type(16)));
     typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
@@ -571,7 +583,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // own token tile; the parts are summed in LDS at the end.
     const int kh = KH > 1 ? wave / NWG : 0;
     const int tg = tid - kh * NTG;
-    const int n0 = tn * BN + (wave - kh * NWG) * 32 * FN;
+    const int n0 = tn * BN + (wave - kh * NWG) * 32 * TPW;
     const int K = p.k;
     const int k_len = p.k_len / KH;
     const int k_begin = split * p.k_len + kh * k_len;
@@ -593,7 +605,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const uint8_t* w_src[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const size_t row = (size_t)min(n0 + 32 * j + l32, N - 1);
+        const size_t row = (size_t)min(n0 + (SWI ? 0 : 32 * j) + l32, N - 1);
         if constexpr (Q4W)
             w_src[j] = reinterpret_cast<const uint8_t*>(W) + row * (size_t)(K / 256 * 144) + (k_begin / 256) * 144;
         else if constexpr (Q8W)
@@ -601,7 +613,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                        32 * half;
         else
             w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(W) + (row * K + k_begin + 32 * half) * 2
-                            : reinterpret_cast<const uint8_t*>(W + row * words_per_row + (k_begin >> 3) + 4 * half);
+                            : reinterpret_cast<const uint8_t*>((SWI && j == 1 ? p.w_up : W) + row * words_per_row +
+                                                               (k_begin >> 3) + 4 * half);
     }
     // Q8W: byte selectors for this lane half (span dword i -> q dword i; d -> (d, d))
     const uint32_t q8_sel = half ? 0x07060504u : 0x05040302u;
@@ -822,7 +835,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][j][r] += x[((i * FN + j) * 16 + r) * 64];
         };
-        if constexpr (KH == 4) {
+        if constexpr (SWI) {
+            // the gate tiles, then the up tiles: one tile's sums per pass fit the token buffers
+            float* const x1 = reinterpret_cast<float*>(smem) + (size_t)(wave - kh * NWG) * FM * 16 * 64 + lane;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if (kh == 1) {
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) x1[(i * 16 + r) * 64] = acc[i][j][r];
+                }
+                __syncthreads();
+                if (kh == 0) {
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] += x1[(i * 16 + r) * 64];
+                }
+                __syncthreads();
+            }
+            if (kh == 1) return;
+        } else if constexpr (KH == 4) {
             if (kh & 1) put(xch + (kh >> 1) * kPart);
             __syncthreads();
             if (!(kh & 1)) add(xch + (kh >> 1) * kPart);
@@ -830,12 +864,56 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
             if (kh == 2) put(xch);
             __syncthreads();
             if (kh != 0) return;
+            add(xch);
         } else {
             if (kh == 1) put(xch);
             __syncthreads();
             if (kh == 1) return;
+            add(xch);
         }
-        add(xch);
+    }
+    if constexpr (SWI) {
+        // c = silu(g) * u: g and u as the gate launch stores them and the up
+        // launch's SWIGLU epilogue forms them (the sums times the row scale)
+        float* const cf = static_cast<float*>(C);
+        const bool vec = (ld & 3) == 0 && ((uintptr_t)C & 15) == 0;
+        auto put_row = [&](int gm, float rs, auto v_of) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int gn = n0 + 8 * g + 4 * half;
+                float d[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) d[r] = epilogue(kEpiSwiglu, v_of(0, g, r) * rs, v_of(1, g, r) * rs);
+                float* const dst = cf + (size_t)gm * ld + gn;
+                if (vec && gn + 3 < N) {
+                    *reinterpret_cast<float4_t*>(dst) = float4_t{d[0], d[1], d[2], d[3]};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (gn + r < N) dst[r] = d[r];
+                }
+            }
+        };
+        if (p.hilo) {
+            if constexpr (FM % 2 == 0) {
+#pragma unroll
+                for (int i = 0; i < FM / 2; ++i) {
+                    const int gm = m0 / 2 + 32 * i + l32;
+                    if (gm >= p.m_out) continue;
+                    put_row(gm, p.row_scale[gm], [&](int j, int g, int r) {
+                        return acc[2 * i][j][4 * g + r] + acc[2 * i + 1][j][4 * g + r] * 0x1p-11f;
+                    });
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int gm = m0 + 32 * i + l32;
+                if (gm >= p.m_out) continue;
+                put_row(gm, p.row_scale[gm], [&](int j, int g, int r) { return acc[i][j][4 * g + r]; });
+            }
+        }
+        return;
     }
 
     // Lane l holds D[n = 8 g + 4 h + r][m = l % 32] in acc[..][4 g + r].
@@ -990,9 +1068,10 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
     }
 }
 
-template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, int KH = 1, bool Q4W = false>
+template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, int KH = 1, bool Q4W = false,
+          bool SWI = false>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
-    constexpr int BN = 32 * FN * NW / KH;
+    constexpr int BN = 32 * (SWI ? 1 : FN) * NW / KH;
     const size_t lds = 2 * (size_t)KH * BM * kLdsRow;
     if ((a.k_len / KH) % 256 != 0) return hipErrorInvalidValue;  // whole four-step loop bodies per half
     PrefillArgs p = a;
@@ -1007,8 +1086,10 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     }
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (a.info) {
-        snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s>", BM,
-                 NW, FN, WPE, out_f32 ? "true" : "false", F16W ? "true" : "false", Q8W ? "true" : "false", KH,
+        snprintf(a.info->name, sizeof a.info->name,
+                 SWI ? "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s, true>"
+                     : "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s>",
+                 BM, NW, FN, WPE, out_f32 ? "true" : "false", F16W ? "true" : "false", Q8W ? "true" : "false", KH,
                  Q4W ? "true" : "false");
         a.info->grid = grid.x;
         a.info->block = 64u * NW;
@@ -1016,12 +1097,17 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
         a.info->splits = (unsigned)p.splits;
         return hipSuccess;
     }
-    if (out_f32)
+    if constexpr (SWI) {
+        if (!out_f32) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, false, false, KH, false, true>), grid,
+                           dim3(64 * NW), lds, s, p);
+    } else if (out_f32) {
         hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, true, F16W, Q8W, KH, Q4W>), grid, dim3(64 * NW), lds,
                            s, p);
-    else
+    } else {
         hipLaunchKernelGGL((gf4_prefill_f16_kernel<BM, NW, FN, WPE, false, F16W, Q8W, KH, Q4W>), grid, dim3(64 * NW), lds,
                            s, p);
+    }
     return hipGetLastError();
 }
 
@@ -1275,6 +1361,16 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
     if ((k / cfg.splits) % (256 * cfg.kh) != 0) cfg.kh = 1;
 }
 
+// The gate launches the fused gate/up kernel replaces: GF4 words, unsplit, the
+// 8-wave 64- or 128-token tile of one 32-row weight tile per wave, with K
+// halves or without (the fused kernel then holds a gate and an up tile per
+// wave; q8_0 and Q4_K hold three 16-byte loads per tile in their load ring and
+// would spill).
+bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
+    return wkind == 0 && cfg.splits == 1 && cfg.waves == 8 && cfg.fn == 2 && (cfg.kh == 1 || cfg.kh == 2) &&
+           (cfg.bm == 64 || cfg.bm == 128);
+}
+
 }  // namespace
 
 // wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks, 3 Q4_K super-blocks (1..3 take column-order tokens and a
@@ -1282,10 +1378,14 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg,
                                   hipStream_t stream, int wkind, int epi, LaunchInfo* info, bool staged,
-                                  const PrefillSegs* segs) {
+                                  const PrefillSegs* segs, const void* w_up) {
     const bool f16w = wkind == 1, q8w = wkind == 2, q4w = wkind == 3;
     PrefillArgs p{};
     p.w = static_cast<const uint32_t*>(w);
+    p.w_up = static_cast<const uint32_t*>(w_up);
+    // fused gate/up: the configurations prefill_swiglu_fusable accepts, STORE of silu(g) * u
+    if (w_up && (!swiglu_cfg_ok(wkind, cfg) || !workspace || !out_f32 || epi != kEpiStore || (segs && segs->n > 1)))
+        return hipErrorInvalidValue;
     p.a = a;
     p.awq = awq;
     p.c = c;
@@ -1374,6 +1474,13 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const bool split = cfg.splits > 1;
         if (split) p.c = partial;
         const bool kf32 = of || split;
+        if (w_up) {
+            if (cfg.bm == 128)
+                return cfg.kh == 2 ? launch_f16_tile<128, 8, 2, 2, false, false, 2, false, true>(p, true, stream)
+                                   : launch_f16_tile<128, 8, 2, 2, false, false, 1, false, true>(p, true, stream);
+            return cfg.kh == 2 ? launch_f16_tile<64, 8, 2, 2, false, false, 2, false, true>(p, true, stream)
+                               : launch_f16_tile<64, 8, 2, 2, false, false, 1, false, true>(p, true, stream);
+        }
         if (q4w) {  // no 256-token tiles (plan_prefill never picks them for Q4_K)
             switch (cfg.bm * 10 + cfg.fn) {
                 case 1282:
@@ -1455,13 +1562,19 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
 
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                           void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                          int epi, LaunchInfo* info, bool staged, const PrefillSegs* segs) {
+                          int epi, LaunchInfo* info, bool staged, const PrefillSegs* segs, const void* w_up) {
     if (!workspace && wkind != 0) return hipErrorInvalidValue;
     if (staged && !workspace) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
     if (workspace) fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
     return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind, epi, info,
-                                  staged, segs);
+                                  staged, segs, w_up);
+}
+
+bool prefill_swiglu_fusable(int wkind, int m, int rows, int k, int a_f32, size_t workspace_bytes) {
+    PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
+    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
+    return swiglu_cfg_ok(wkind, cfg);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {

@@ -161,11 +161,16 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
                                   void* c, int m, int out_f32, void* workspace, PrefillCfg cfg, hipStream_t stream,
                                   int wkind = 0, int epi = 0, LaunchInfo* info = nullptr,
                                   bool staged = false,  // wkind 0 GF4, 1 F16, 2 q8_0, 3 Q4_K
-                                  const PrefillSegs* segs = nullptr);
+                                  const PrefillSegs* segs = nullptr, const void* w_up = nullptr);
 // Planned launch; the workspace is required for F16 and q8_0 weights.
 hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void* a, int a_f32, const float* awq,
                           void* c, int m, int out_f32, void* workspace, size_t workspace_bytes, hipStream_t stream,
                           int epi = 0, LaunchInfo* info = nullptr, bool staged = false,
-                          const PrefillSegs* segs = nullptr);
+                          const PrefillSegs* segs = nullptr, const void* w_up = nullptr);
+// w_up (with w the gate): c = silu(gate v) * (up v) in one launch, the bits of
+// the gate launch (STORE) followed by the up launch (SWIGLU epilogue), where
+// prefill_swiglu_fusable says the planned gate launch has the fused form (GF4
+// words, fp32 c, a workspace, epi STORE); invalid otherwise.
+bool prefill_swiglu_fusable(int wkind, int m, int rows, int k, int a_f32, size_t workspace_bytes);
 
 }  // namespace qw35

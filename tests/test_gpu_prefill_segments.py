@@ -16,8 +16,16 @@ them, each segment writing its own output.
 * two replays give the same bits; ops that do not merge (a row count that is
   not a multiple of 4, another weight form, an output that is another op's
   input) still give their single calls' bits.
+
+The gate/up op (MATMUL_SWIGLU) of GF4 weights runs as one launch holding a
+gate and an up tile per wave where the gate's planned launch is an unsplit
+8-wave tile; its output equals, bit for bit, the gate call (STORE) followed by
+the up call (SWIGLU epilogue), which is also what it runs where the plan has
+another form.
 """
 from __future__ import annotations
+
+import re
 
 import numpy as np
 import pytest
@@ -215,3 +223,44 @@ def test_merged_delta_mixer_full_size(cuda, n):
         sub = np.concatenate([raw[i * rb:(i + 1) * rb] for i in sel])
         img = om.prefill_image(rt.TYPE_Q8_0, sub, len(sel), k).astype(np.float32)
         check_prefill(g[:, sel], x32, None, img, w_exact=om.dequant(rt.TYPE_Q8_0, sub, len(sel), k))
+
+
+@pytest.mark.parametrize("rows,k,n", [(12288, 4096, 128), (1024, 2048, 100), (512, 1024, 40), (2048, 4096, 64),
+                                      (12288, 4096, 200), (520, 1024, 77)])
+@pytest.mark.parametrize("awq_on", [False, True])
+def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
+    import torch
+
+    from qwowl35_amd import _ffi
+
+    rt = _rt()
+    t = rt.TYPE_GF4
+    rng = np.random.default_rng(rows + k + n + awq_on)
+    gate = rt.HipWeight.upload(make_weight(t, rows, k, seed=rows + 1)[0], t, rows, k, device=cuda)
+    up = rt.HipWeight.upload(make_weight(t, rows, k, seed=rows + 2)[0], t, rows, k, device=cuda)
+    x = _t(activations(rng, n, k), cuda)
+    aw = _t(awq_scales(rng, k), cuda) if awq_on else None
+    desc = rt.prefill_kernel(gate, n, a_dtype=torch.float32, awq=awq_on, out_dtype=torch.float32)
+    fused = bool(re.fullmatch(r"gf4_prefill_f16_kernel<(64|128), 8, 1, 2, true, false, false, [12], false>",
+                              desc["name"])) and desc["splits"] == 1
+    print(f"gate/up {rows}x{k} n={n} awq={awq_on} gate launch {desc['name']} splits {desc['splits']} "
+          f"fused={fused}", flush=True)
+    if (rows, k, n) == (12288, 4096, 128):
+        assert fused  # the 9B's FFN at the default chunk takes the fused launch
+    ws = _workspace([gate, up], n, cuda)
+    dst = torch.full((n, rows), float("nan"), dtype=torch.float32, device=cuda)
+    plan = rt.DecodePlan()
+    plan.matmul_swiglu(gate, up, x, dst, ws, awq=aw)
+    plan.record()
+    outs = []
+    for _ in range(2):
+        dst.fill_(float("nan"))
+        plan.launch()
+        torch.cuda.synchronize()
+        outs.append(dst.clone())
+    plan.close()
+    want = rt.matmul_prefill(gate, x, awq=aw, out_dtype=torch.float32, workspace=ws)
+    rt.matmul_prefill(up, x, awq=aw, out_dtype=torch.float32, dst=want, workspace=ws, epilogue=_ffi.EPILOGUE_SWIGLU)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int32), want.view(torch.int32))
