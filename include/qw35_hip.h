@@ -259,7 +259,10 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight *w, void *dst, void *stream, c
  * into fp32 dst, n_batch = the chunk's tokens (1..65536), through the op's
  * workspace (qw35_hip_matmul_prefill_epilogue). */
 #define QW35_HIP_OP_MATMUL 3u        /* dst (+)= W (awq * x): STORE, or ADD with residual */
-#define QW35_HIP_OP_MATMUL_SWIGLU 4u /* dst = silu(gate (awq*x)) * (up (awq*x)): two launches (STORE, SWIGLU) */
+/* dst = silu(gate (awq*x)) * (up (awq*x)): the gate launch (STORE) and the up
+ * launch (SWIGLU epilogue), or for GF4 weights where the gate's planned launch
+ * allows it one fused launch with the same bits */
+#define QW35_HIP_OP_MATMUL_SWIGLU 4u
 typedef struct {
     uint32_t kind;               /* QW35_HIP_OP_* */
     uint32_t n_batch;            /* 1..8; MATMUL / MATMUL_SWIGLU: tokens, 1..65536 */
