@@ -293,6 +293,7 @@ class CpuBaseline:
             t2 = time.perf_counter()
             t_dq.append(t1 - t0)
             t_mv.append(t2 - t1)
+        self._quiesce()
         return float(np.median(t_dq)), float(np.median(t_mv))
 
     def matmul(self, type_id, raw: np.ndarray, rows: int, k: int, m: int, seed: int = 0) -> tuple[float, float]:
@@ -310,7 +311,16 @@ class CpuBaseline:
             t2 = time.perf_counter()
             t_dq.append(t1 - t0)
             t_mm.append(t2 - t1)
+        self._quiesce()
         return float(np.median(t_dq)), float(np.median(t_mm))
+
+    @staticmethod
+    def _quiesce() -> None:
+        """OpenBLAS worker threads spin for a while after a call before they
+        sleep; the GPU line timed next must not share the job's CPUs with them
+        (a timed window of few graph replays stalls when the submitting thread
+        is descheduled: one such line measured 3x its time)."""
+        time.sleep(0.3)
 
     def record(self, value, unit, sample: str) -> dict:
         return {"value": value, "unit": unit, "cores": self.threads, "kind": "port",
