@@ -1,6 +1,6 @@
 """Config 5 at its real shapes: the 32-layer Qwen3.5-9B decode-step projection
 stack (q8_0 mixers, GF4 FFN, Q4_K head; 217 GEMVs recorded as one plan) at
-batch 1 and 8.  Every layer has its own weights (distinct seeds) and its own
+batch 1 and 8, and its 128-token prefill chunk.  Every layer has its own weights (distinct seeds) and its own
 output buffers, so every output of every projection is checked against the
 fp64 product of the library's dequantised weights (which the dequantisation
 tests pin bit for bit to the oracle), within GEMV_REL_L2; the residual
@@ -107,6 +107,75 @@ def test_stack9b_every_output(cuda, stack9b, nb, awq):
         assert torch.equal(bufs.logits, first["logits"]), rep
         for il, a in enumerate(bufs.ffn_act):
             assert torch.equal(a, first["ffn_act"][il]), (rep, il)
+    plan.close()
+
+
+def test_stack9b_chunk_every_output(cuda, stack9b):
+    """The 128-token prefill chunk of the same stack (qwen35.build_chunk_plan:
+    fp32 activations on the prefill matmul, each layer's mixer input
+    projections as one merged launch, gate/up/SwiGLU as one fused launch, the
+    head on the last token): every projection output, the residual stream and
+    the last token's logits against fp64 on the dequantised weights within
+    GEMV_REL_L2, and two replays bit for bit."""
+    import torch
+
+    from qwowl35_amd import qwen35
+
+    hp = stack9b.hp
+    n = 128
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(300)
+    bufs = qwen35.StepBuffers.make(hp, n, gen, awq=True, shared_outputs=False)
+    act0 = bufs.act.clone()
+    ws = qwen35.chunk_workspace(stack9b, n)
+    plan = qwen35.build_chunk_plan(stack9b, bufs, ws)
+    print(f"stack9b chunk n={n}: launching the recorded chunk plan", flush=True)
+    plan.launch()
+    torch.cuda.synchronize()
+    first = {"act": bufs.act.clone(), "logits": bufs.logits[0:1].clone(),
+             "mix": [{k: v.clone() for k, v in d.items()} for d in bufs.mixer_out],
+             "ffn_act": [a.clone() for a in bufs.ffn_act]}
+
+    x = bufs.norm.double().T
+    fx = (bufs.ffn_norm.double() * bufs.awq.double()).T
+    want_act = act0.double().clone()
+    worst = 0.0
+    for il, layer in enumerate(stack9b.layers):
+        mix = qwen35.mixer_projections(hp, il)
+        for p in mix[:-1]:
+            e = _rel(bufs.mixer_out[il][p.name], (_deq64(layer[p.name]) @ x).T)
+            worst = max(worst, e)
+            assert e <= GEMV_REL_L2, (il, p.name, e)
+        out = mix[-1]
+        want_act += (_deq64(layer[out.name]) @ bufs.core[out.k].double().T).T
+        gate = _deq64(layer["ffn_gate"]) @ fx
+        up = _deq64(layer["ffn_up"]) @ fx
+        e = _rel(bufs.ffn_act[il], (gate / (1.0 + torch.exp(-gate)) * up).T)
+        worst = max(worst, e)
+        assert e <= GEMV_REL_L2, (il, "ffn_gate_up_swiglu", e)
+        want_act += (_deq64(layer["ffn_down"]) @ bufs.ffn_act[il].double().T).T
+    e = _rel(bufs.act, want_act)
+    assert e <= GEMV_REL_L2, ("residual stream", e)
+    e_head = _rel(bufs.logits[0:1], (_deq64(stack9b.head) @ x[:, n - 1:n]).T)
+    assert e_head <= GEMV_REL_L2, ("output.weight", e_head)
+    print(f"stack9b chunk: worst projection rel-L2 {worst:.2e}, residual {e:.2e}, head {e_head:.2e}", flush=True)
+
+    for rep in range(2):
+        bufs.act.copy_(act0)
+        bufs.logits.fill_(float("nan"))
+        for d in bufs.mixer_out:
+            for v in d.values():
+                v.fill_(float("nan"))
+        for a in bufs.ffn_act:
+            a.fill_(float("nan"))
+        plan.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(bufs.act, first["act"]), rep
+        assert torch.equal(bufs.logits[0:1], first["logits"]), rep
+        for il in range(hp.transformer_layers):
+            assert torch.equal(bufs.ffn_act[il], first["ffn_act"][il]), (rep, il)
+            for k, v in bufs.mixer_out[il].items():
+                assert torch.equal(v, first["mix"][il][k]), (rep, il, k)
     plan.close()
 
 
