@@ -1,34 +1,31 @@
-// GF4 prefill dequant-matmul on bf16 MFMA (gfx950):
+// Prefill dequant-matmul on MFMA (gfx950): the tiled multi-token matmul of
+// encodeMatvecBatch / encodeTiledKMatmul
+// (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366; kernels
+// qw35_mul_mm_gf4_f32 / qw35_kernel_mul_mm in qw35_tiled_mm.metal:36-255):
 //
-//   C[m][n] = sum_k bf16_rne(awq[k] * A[m][k]) * W[n][k]        (awq == nullptr: A[m][k])
+//   C[m][n] = sum_k v[m][k] * W[n][k],  v = awq[k] * A[m][k] (fp32), fp32 accumulation,
 //
-// A: [M][K] bf16 (or fp32) activations, W: GF4 tensor [N][K], C: [M][N] bf16 (RNE)
-// or fp32, fp32 accumulation.  This is the tiled multi-token matmul of
-// encodeMatvecBatch / encodeTiledKMatmul for type 100
-// (qw35-server/src/metal/bridge/Qw35MetalRuntime+FFN.m:260-366, kernel
-// qw35_mul_mm_gf4_f32 in qw35_tiled_mm.metal:203-255), designed for CDNA4:
+// A: [M][K] bf16 or fp32 activations, W: [N][K] weights, C: [M][N] bf16 (RNE) or
+// fp32 (STORE, or the ADD / SwiGLU epilogues of the runtime's chunk).
 //
-// * A block computes a BM x BN tile of C with WGM x WGN waves; each wave owns a
-//   (BM/WGM) x (BN/WGN) sub-tile of 16x16 v_mfma_f32_16x16x32_bf16 accumulators.
-// * Per 64-wide k step the block stages A and the dequantised W tile as bf16 in
-//   LDS (double buffered, 16-byte row padding against bank conflicts).  Global
-//   loads run two steps ahead in two register stages; a step's conversion (AWQ
-//   multiply + RNE for A, GF4 decode for W) follows the MFMAs of the step
-//   before it, so one barrier per step suffices.
-// * The W tile is the MFMA's first operand: lane l accumulates
-//   D[n = 4 (l / 16) + r][m = l % 16], four consecutive outputs of one token
-//   row, stored as one 8- or 16-byte vector.
-// * GF4 decode is exact in bf16: w_i = -sext3(c_i) * s / 4, s = fp16(b << 8)
-//   (the format of tools/qw35_cook_common.py:79 with c = q_raw ^ 4).
+// * Staged path (the default; the caller passes a workspace):
+//   prefill_stage_kernel writes v as fp16 with a per-token power-of-two scale
+//   (fp32 input: an fp16 hi and lo row per token, ~22 significant bits), and
+//   gf4_prefill_f16_kernel contracts it on v_mfma_f32_32x32x16_f16 against the
+//   weights decoded in registers: GF4 words (exact in fp16), q8_0 blocks and
+//   Q4_K super-blocks dequantised in the kernel to fp16 of their exact value,
+//   or F16 weights (the fp16 prefill image of the other k-quants).  Tiles,
+//   K halves / quarters within a block and K splits across blocks (fp32
+//   partial sums, prefill_split_reduce) follow plan_prefill.  A launch may
+//   cover up to kMaxSegments matrices over the same activations (a mixer's
+//   input projections), and a GF4 gate/up pair as one fused launch.
+// * Direct path (GF4, bf16 activations without AWQ, no workspace):
+//   gf4_prefill_kernel stages A and the GF4 tile decoded to bf16 in LDS and
+//   contracts on v_mfma_f32_16x16x32_bf16.  GF4 decode is exact in bf16 and
+//   fp16: w_i = -sext3(c_i) * s / 4, s = fp16(b << 8) (the format of
+//   tools/qw35_cook_common.py:79 with c = q_raw ^ 4).
 // * Blocks are assigned XCD by XCD (consecutive block ids land on different
-//   XCDs), M-tile fastest, so the blocks that share a W tile share an L2.
-//
-// F16 weights (GGUF type 1) take the staged kernel with fp16 weight loads in
-// place of the GF4 decode (gf4_prefill_f16_kernel<..., F16W>).  They serve the
-// q8_0 / Q4_K / Q6_K projections through their fp16 prefill image
-// (qw35_hip_dequantize_f16: fp16_rne of the exact dequantised weight), which
-// is the precision of the reference's tiled matmul: qw35_kernel_mul_mm
-// dequantises its weight tiles to half (qw35_tiled_mm.metal:199-255).
+//   XCDs), so the blocks that share a weight tile share an L2.
 #include <stdio.h>
 
 #include <cmath>
