@@ -520,8 +520,8 @@ template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool
           bool Q4W = false, bool SWI = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
-    static_assert(!SWI || (FN == 2 && OUT_F32 && !F16W && !Q8W && !Q4W && KH <= 2),
-                  "fused gate/up: GF4 words, a gate and an up tile per wave, K halves at most");
+    static_assert(!SWI || (FN == 2 && OUT_F32 && !F16W && !Q8W && !Q4W),
+                  "fused gate/up: GF4 words, a gate and an up tile per wave");
     constexpr int NWG = NW / KH;            // waves per K half
     constexpr int NTG = 64 * NWG;           // threads per K half
     constexpr int TPW = SWI ? 1 : FN;       // distinct 32-row output tiles per wave
@@ -833,26 +833,41 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                     for (int r = 0; r < 16; ++r) acc[i][j][r] += x[((i * FN + j) * 16 + r) * 64];
         };
         if constexpr (SWI) {
-            // the gate tiles, then the up tiles: one tile's sums per pass fit the token buffers
+            // the gate tiles, then the up tiles (one tile's sums per pass fit the
+            // token buffers), each in the order of the unfused kernel
+            constexpr int kPart1 = NWG * FM * 16 * 64;  // floats of one part's sums of one tile
             float* const x1 = reinterpret_cast<float*>(smem) + (size_t)(wave - kh * NWG) * FM * 16 * 64 + lane;
+            auto put1 = [&](float* x, int j) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) x[(i * 16 + r) * 64] = acc[i][j][r];
+            };
+            auto add1 = [&](const float* x, int j) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += x[(i * 16 + r) * 64];
+            };
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                if (kh == 1) {
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) x1[(i * 16 + r) * 64] = acc[i][j][r];
+                if constexpr (KH == 4) {
+                    if (kh & 1) put1(x1 + (kh >> 1) * kPart1, j);
+                    __syncthreads();
+                    if (!(kh & 1)) add1(x1 + (kh >> 1) * kPart1, j);
+                    __syncthreads();
+                    if (kh == 2) put1(x1, j);
+                    __syncthreads();
+                    if (kh == 0) add1(x1, j);
+                    __syncthreads();
+                } else {
+                    if (kh == 1) put1(x1, j);
+                    __syncthreads();
+                    if (kh == 0) add1(x1, j);
+                    __syncthreads();
                 }
-                __syncthreads();
-                if (kh == 0) {
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][j][r] += x1[(i * 16 + r) * 64];
-                }
-                __syncthreads();
             }
-            if (kh == 1) return;
+            if (kh != 0) return;
         } else if constexpr (KH == 4) {
             if (kh & 1) put(xch + (kh >> 1) * kPart);
             __syncthreads();
@@ -1358,14 +1373,15 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
     if ((k / cfg.splits) % (256 * cfg.kh) != 0) cfg.kh = 1;
 }
 
-// The gate launches the fused gate/up kernel replaces: GF4 words, unsplit, the
-// 8-wave 64- or 128-token tile of one 32-row weight tile per wave, with K
-// halves or without (the fused kernel then holds a gate and an up tile per
-// wave; q8_0 and Q4_K hold three 16-byte loads per tile in their load ring and
-// would spill).
+// The gate launches the fused gate/up kernel replaces: GF4 words, unsplit, 8
+// waves of one 32-row weight tile each over 64 or 128 tokens, with K halves,
+// quarters (64 tokens) or neither (the fused kernel then holds a gate and an
+// up tile per wave; the 16-wave quarters would spill, and q8_0 and Q4_K hold
+// three 16-byte loads per tile in their load ring).
 bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
-    return wkind == 0 && cfg.splits == 1 && cfg.waves == 8 && cfg.fn == 2 && (cfg.kh == 1 || cfg.kh == 2) &&
-           (cfg.bm == 64 || cfg.bm == 128);
+    if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2 || cfg.waves != 8) return false;
+    if (cfg.kh == 4) return cfg.bm == 64;
+    return (cfg.kh == 1 || cfg.kh == 2) && (cfg.bm == 64 || cfg.bm == 128);
 }
 
 }  // namespace
@@ -1475,6 +1491,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
             if (cfg.bm == 128)
                 return cfg.kh == 2 ? launch_f16_tile<128, 8, 2, 2, false, false, 2, false, true>(p, true, stream)
                                    : launch_f16_tile<128, 8, 2, 2, false, false, 1, false, true>(p, true, stream);
+            // K quarters: two waves per SIMD (a gate and an up tile per wave
+            // need more than the 128 VGPRs of the unfused form's four)
+            if (cfg.kh == 4) return launch_f16_tile<64, 8, 2, 2, false, false, 4, false, true>(p, true, stream);
             return cfg.kh == 2 ? launch_f16_tile<64, 8, 2, 2, false, false, 2, false, true>(p, true, stream)
                                : launch_f16_tile<64, 8, 2, 2, false, false, 1, false, true>(p, true, stream);
         }

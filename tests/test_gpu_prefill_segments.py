@@ -19,7 +19,7 @@ them, each segment writing its own output.
 
 The gate/up op (MATMUL_SWIGLU) of GF4 weights runs as one launch holding a
 gate and an up tile per wave where the gate's planned launch is an unsplit
-8-wave tile; its output equals, bit for bit, the gate call (STORE) followed by
+8-wave tile (K halves, quarters or neither); its output equals, bit for bit, the gate call (STORE) followed by
 the up call (SWIGLU epilogue), which is also what it runs where the plan has
 another form.
 """
@@ -225,8 +225,9 @@ def test_merged_delta_mixer_full_size(cuda, n):
         check_prefill(g[:, sel], x32, None, img, w_exact=om.dequant(rt.TYPE_Q8_0, sub, len(sel), k))
 
 
-@pytest.mark.parametrize("rows,k,n", [(12288, 4096, 128), (1024, 2048, 100), (512, 1024, 40), (2048, 4096, 64),
-                                      (12288, 4096, 200), (520, 1024, 77)])
+@pytest.mark.parametrize("rows,k,n", [(12288, 4096, 128), (12288, 4096, 9), (12288, 4096, 32), (1024, 2048, 100),
+                                      (512, 1024, 40), (2048, 4096, 64), (12288, 4096, 200), (520, 1024, 77),
+                                      (4096, 4096, 20)])
 @pytest.mark.parametrize("awq_on", [False, True])
 def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
     import torch
@@ -241,12 +242,17 @@ def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
     x = _t(activations(rng, n, k), cuda)
     aw = _t(awq_scales(rng, k), cuda) if awq_on else None
     desc = rt.prefill_kernel(gate, n, a_dtype=torch.float32, awq=awq_on, out_dtype=torch.float32)
-    fused = bool(re.fullmatch(r"gf4_prefill_f16_kernel<(64|128), 8, 1, 2, true, false, false, [12], false>",
-                              desc["name"])) and desc["splits"] == 1
+    # the gate launches the plan fuses: unsplit 8-wave tiles of one weight tile per wave, 64 or 128 tokens
+    # with K halves or none, 64 tokens with K quarters
+    m = re.fullmatch(r"gf4_prefill_f16_kernel<(\d+), (\d+), (\d+), \d+, true, false, false, (\d), false>",
+                     desc["name"])
+    bm, nw, fn, kh = (int(v) for v in m.groups()) if m else (0, 0, 0, 0)
+    fused = (desc["splits"] == 1 and nw == 8 and fn == 1 and
+             ((kh in (1, 2) and bm in (64, 128)) or (kh == 4 and bm == 64)))
     print(f"gate/up {rows}x{k} n={n} awq={awq_on} gate launch {desc['name']} splits {desc['splits']} "
           f"fused={fused}", flush=True)
-    if (rows, k, n) == (12288, 4096, 128):
-        assert fused  # the 9B's FFN at the default chunk takes the fused launch
+    if (rows, k) == (12288, 4096) and n <= 128:
+        assert fused  # the 9B's FFN at chunks of up to 128 tokens takes the fused launch
     ws = _workspace([gate, up], n, cuda)
     dst = torch.full((n, rows), float("nan"), dtype=torch.float32, device=cuda)
     plan = rt.DecodePlan()
