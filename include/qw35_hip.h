@@ -260,8 +260,9 @@ int qw35_hip_dequantize_f16(const qw35_hip_weight *w, void *dst, void *stream, c
  * workspace (qw35_hip_matmul_prefill_epilogue). */
 #define QW35_HIP_OP_MATMUL 3u        /* dst (+)= W (awq * x): STORE, or ADD with residual */
 /* dst = silu(gate (awq*x)) * (up (awq*x)): the gate launch (STORE) and the up
- * launch (SWIGLU epilogue), or for GF4 weights where the gate's planned launch
- * allows it one fused launch with the same bits */
+ * launch (SWIGLU epilogue), or for GF4 weights one fused launch -- with the
+ * same bits where it keeps the gate's planned tile, else (some chunk lengths)
+ * within fp32 rounding of them */
 #define QW35_HIP_OP_MATMUL_SWIGLU 4u
 typedef struct {
     uint32_t kind;               /* QW35_HIP_OP_* */

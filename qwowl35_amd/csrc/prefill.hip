@@ -1384,6 +1384,39 @@ bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
     return (cfg.kh == 1 || cfg.kh == 2) && (cfg.bm == 64 || cfg.bm == 128);
 }
 
+// The fused gate/up launch of m tokens (fp32 input: the runtime's chunks):
+// the gate's own plan where it has the fused form; else, for fp32 input,
+//  * in place of the 16-wave 64-token K quarters (33..64 tokens): the 8-wave
+//    64-token tile with K halves;
+//  * in place of a split plan at 129..256 tokens: the unsplit 8-wave
+//    128-token tile,
+// where the fused grid still gives at least half the CUs a block.  Same box,
+// GF4 12288x4096, gate/up as one op, us (two launches -> fused): 48 tokens
+// 55.0 -> 44.5, 64 tokens 56.2 -> 45.3, 192 tokens 138.5 -> 95.3, 256 tokens
+// 147.9 -> 105.5.  The gate's own plan gives the two launches' bits; the
+// others sum K in another grouping (within fp32 rounding of them).  False:
+// the op runs as the gate and up launches.
+bool plan_swiglu(int wkind, int m, int rows, int k, bool a_f32, size_t workspace_bytes, PrefillCfg& cfg) {
+    cfg = plan_prefill_kind(m, rows, k, wkind, a_f32);
+    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32);
+    if (swiglu_cfg_ok(wkind, cfg)) return true;
+    if (wkind != 0 || !a_f32) return false;
+    const int ms = staged_rows(m, a_f32);
+    PrefillCfg alt{64, 2, 1};
+    alt.waves = 8;
+    long blocks = 0;
+    if (cfg.bm == 64 && cfg.kh == 4 && cfg.waves == 16 && k % 512 == 0) {
+        alt.kh = 2;  // 64 tokens by 128 rows per block
+        blocks = (long)((ms + 63) / 64) * ((rows + 127) / 128);
+    } else if (ms > 256 && ms <= 512) {
+        alt.bm = 128;  // 128 tokens by 256 rows per block
+        blocks = (long)((ms + 127) / 128) * ((rows + 255) / 256);
+    }
+    if (2 * blocks < num_cus()) return false;
+    cfg = alt;
+    return true;
+}
+
 }  // namespace
 
 // wkind: 0 GF4 words, 1 F16 weights, 2 q8_0 blocks, 3 Q4_K super-blocks (1..3 take column-order tokens and a
@@ -1583,14 +1616,14 @@ hipError_t launch_prefill(int wkind, const void* w, int rows, int k, const void*
     if (staged && !workspace) return hipErrorInvalidValue;
     PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
     if (workspace) fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
+    if (w_up && !plan_swiglu(wkind, m, rows, k, a_f32 != 0, workspace_bytes, cfg)) return hipErrorInvalidValue;
     return launch_gf4_prefill_cfg(w, rows, k, a, a_f32, awq, c, m, out_f32, workspace, cfg, stream, wkind, epi, info,
                                   staged, segs, w_up);
 }
 
 bool prefill_swiglu_fusable(int wkind, int m, int rows, int k, int a_f32, size_t workspace_bytes) {
-    PrefillCfg cfg = plan_prefill_kind(m, rows, k, wkind, a_f32 != 0);
-    fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32 != 0);
-    return swiglu_cfg_ok(wkind, cfg);
+    PrefillCfg cfg{};
+    return plan_swiglu(wkind, m, rows, k, a_f32 != 0, workspace_bytes, cfg);
 }
 
 hipError_t launch_mfma_probe(unsigned workgroups, unsigned iters, float* sink, hipStream_t stream) {

@@ -18,10 +18,11 @@ them, each segment writing its own output.
   input) still give their single calls' bits.
 
 The gate/up op (MATMUL_SWIGLU) of GF4 weights runs as one launch holding a
-gate and an up tile per wave where the gate's planned launch is an unsplit
-8-wave tile (K halves, quarters or neither); its output equals, bit for bit, the gate call (STORE) followed by
-the up call (SWIGLU epilogue), which is also what it runs where the plan has
-another form.
+gate and an up tile per wave.  Where the gate's planned launch is an unsplit
+8-wave tile (K halves, quarters or neither) the fused launch uses that tile
+and its output equals, bit for bit, the gate call (STORE) followed by the up
+call (SWIGLU epilogue); at other chunk lengths it runs on another tile (or as
+those two launches) within 2^-20 rel-L2 of them.
 """
 from __future__ import annotations
 
@@ -250,9 +251,9 @@ def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
     fused = (desc["splits"] == 1 and nw == 8 and fn == 1 and
              ((kh in (1, 2) and bm in (64, 128)) or (kh == 4 and bm == 64)))
     print(f"gate/up {rows}x{k} n={n} awq={awq_on} gate launch {desc['name']} splits {desc['splits']} "
-          f"fused={fused}", flush=True)
-    if (rows, k) == (12288, 4096) and n <= 128:
-        assert fused  # the 9B's FFN at chunks of up to 128 tokens takes the fused launch
+          f"fused with its tile={fused}", flush=True)
+    if (rows, k) == (12288, 4096) and (n <= 32 or 65 <= n <= 128):
+        assert fused  # the 9B's FFN at these chunk lengths takes the fused launch of the gate's own tile
     ws = _workspace([gate, up], n, cuda)
     dst = torch.full((n, rows), float("nan"), dtype=torch.float32, device=cuda)
     plan = rt.DecodePlan()
@@ -268,5 +269,10 @@ def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
     want = rt.matmul_prefill(gate, x, awq=aw, out_dtype=torch.float32, workspace=ws)
     rt.matmul_prefill(up, x, awq=aw, out_dtype=torch.float32, dst=want, workspace=ws, epilogue=_ffi.EPILOGUE_SWIGLU)
     torch.cuda.synchronize()
-    for o in outs:
-        assert torch.equal(o.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    if fused:
+        assert torch.equal(outs[0].view(torch.int32), want.view(torch.int32))
+    else:
+        # the two launches, or the fused launch on another tile (K summed in another grouping)
+        got64, want64 = outs[0].cpu().numpy().astype(np.float64), want.cpu().numpy().astype(np.float64)
+        assert om.rel_l2(got64, want64) <= MERGED_REL_L2
