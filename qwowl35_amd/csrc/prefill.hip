@@ -1293,6 +1293,17 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
         best.kh = 2;
         best.splits /= 2;
     }
+    // q8_0 over one token tile of at most 64 staged rows: K parts of down to
+    // 256 columns (the K halves of 512-column splits) until the grid fills the
+    // CUs once; the cost model stops at 512-column splits.  Same box, µs,
+    // plan -> more splits: 4096x4096 fp32 9 / 32 tokens 21.3 / 21.9 -> 16.8 /
+    // 18.4, bf16 16 / 64 tokens 20.5 / 22.7 -> 16.4 / 21.0; 2048x4096 fp32 9
+    // tokens 20.7 -> 15.4 (grids of more row tiles keep their plans).
+    if (q8w && !q4w && m <= 64 && best.bm == 64 && best.waves == 8 && best.kh == 2) {
+        const long tiles = (rows + 127) / 128;
+        while (tiles * best.splits * 2 <= cus && best.splits * 2 <= 16 && k % (best.splits * 2 * 2 * 256) == 0)
+            best.splits *= 2;
+    }
     // Q4_K: every block dequantises its whole weight tile on the VALU, so a
     // 64-token tile over more than 64 tokens decodes each weight twice as
     // often as a 128-token tile; take the latter with twice the K split.

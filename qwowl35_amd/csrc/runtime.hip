@@ -462,7 +462,7 @@ void* qw35_hip_runtime_create(const void* model_map, uint64_t model_size, const 
                 while (j < l.mix.size() && j - i < (size_t)qw35::kMaxSegments && merged.rows % 4 == 0 &&
                        l.mix[j].pf.type_id == merged.type_id && l.mix[j].pf.k == merged.k &&
                        l.mix[j].pf.rows % 4 == 0)
-                    merged.rows += l.mix[j++].pf.rows;
+                    merged.rows += l.mix[j].pf.rows, merged.bytes += l.mix[j++].pf.bytes;
                 if (j - i > 1)
                     for (uint32_t n = QW35_HIP_MAX_BATCH + 1; n <= prefill_chunk; ++n)
                         r->pf_ws_bytes = std::max(r->pf_ws_bytes, qw35_hip_matmul_prefill_workspace_size(&merged, n));

@@ -293,6 +293,7 @@ def chunk_workspace(stack: ProjectionStack, n_tokens: int, device=None) -> torch
             while (j < len(views) and j - i < 4 and merged.rows % 4 == 0 and views[j].type_id == merged.type_id
                    and views[j].k == merged.k and views[j].rows % 4 == 0):
                 merged.rows += views[j].rows
+                merged.bytes += views[j].bytes
                 j += 1
             if j - i > 1:
                 size = max(size, int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(merged), n_tokens)))

@@ -63,6 +63,7 @@ def _workspace(ws_list, n, cuda, merged_rows=None):
     size = max(int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(w.view), n)) for w in ws_list)
     if merged_rows:
         v = _ffi.Weight.from_buffer_copy(ws_list[0].view)
+        v.bytes = v.bytes // v.rows * merged_rows
         v.rows = merged_rows
         size = max(size, int(lib.qw35_hip_matmul_prefill_workspace_size(C.byref(v), n)))
     return torch.empty(size, dtype=torch.uint8, device=cuda)
