@@ -1098,11 +1098,10 @@ hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     }
     const dim3 grid(p.tiles_m * p.tiles_n * p.splits);
     if (a.info) {
-        snprintf(a.info->name, sizeof a.info->name,
-                 SWI ? "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s, true>"
-                     : "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s>",
+        // every template argument, as the profiler names the instantiation
+        snprintf(a.info->name, sizeof a.info->name, "gf4_prefill_f16_kernel<%d, %d, %d, %d, %s, %s, %s, %d, %s, %s>",
                  BM, NW, FN, WPE, out_f32 ? "true" : "false", F16W ? "true" : "false", Q8W ? "true" : "false", KH,
-                 Q4W ? "true" : "false");
+                 Q4W ? "true" : "false", SWI ? "true" : "false");
         a.info->grid = grid.x;
         a.info->block = 64u * NW;
         a.info->lds = (unsigned)lds;

@@ -246,7 +246,7 @@ def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
     desc = rt.prefill_kernel(gate, n, a_dtype=torch.float32, awq=awq_on, out_dtype=torch.float32)
     # the gate launches the plan fuses: unsplit 8-wave tiles of one weight tile per wave, 64 or 128 tokens
     # with K halves or none, 64 tokens with K quarters
-    m = re.fullmatch(r"gf4_prefill_f16_kernel<(\d+), (\d+), (\d+), \d+, true, false, false, (\d), false>",
+    m = re.fullmatch(r"gf4_prefill_f16_kernel<(\d+), (\d+), (\d+), \d+, true, false, false, (\d), false, false>",
                      desc["name"])
     bm, nw, fn, kh = (int(v) for v in m.groups()) if m else (0, 0, 0, 0)
     fused = (desc["splits"] == 1 and nw == 8 and fn == 1 and
