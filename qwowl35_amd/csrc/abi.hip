@@ -563,7 +563,7 @@ void* qw35_hip_plan_create(const qw35_hip_plan_op* ops, uint32_t n_ops, char* er
                         }
                         return e;
                     };
-                    // gate/up: one fused launch where the gate's planned launch has that form
+                    // gate/up: one fused launch where plan_swiglu finds a fused tile for it
                     const bool fused = sw && qw35::prefill_swiglu_fusable(prefill_wkind(o.w->type_id), (int)o.n_batch,
                                                                           (int)o.w->rows, (int)o.w->k, 1,
                                                                           o.workspace_bytes);
