@@ -110,21 +110,22 @@ def test_stack9b_every_output(cuda, stack9b, nb, awq):
     plan.close()
 
 
-def test_stack9b_chunk_every_output(cuda, stack9b):
-    """The 128-token prefill chunk of the same stack (qwen35.build_chunk_plan:
-    fp32 activations on the prefill matmul, each layer's mixer input
-    projections as one merged launch, gate/up/SwiGLU as one fused launch, the
-    head on the last token): every projection output, the residual stream and
-    the last token's logits against fp64 on the dequantised weights within
+@pytest.mark.parametrize("n", [128, 48, 192])
+def test_stack9b_chunk_every_output(cuda, stack9b, n):
+    """Prefill chunks of the same stack (qwen35.build_chunk_plan: fp32
+    activations on the prefill matmul, each layer's mixer input projections as
+    one merged launch, gate/up/SwiGLU as one fused launch -- on the gate's own
+    tile at 128 tokens, on tiles of its own at 48 and 192 -- the head on the
+    last token): every projection output, the residual stream and the last
+    token's logits against fp64 on the dequantised weights within
     GEMV_REL_L2, and two replays bit for bit."""
     import torch
 
     from qwowl35_amd import qwen35
 
     hp = stack9b.hp
-    n = 128
     gen = torch.Generator(device=cuda)
-    gen.manual_seed(300)
+    gen.manual_seed(300 + n)
     bufs = qwen35.StepBuffers.make(hp, n, gen, awq=True, shared_outputs=False)
     act0 = bufs.act.clone()
     ws = qwen35.chunk_workspace(stack9b, n)
