@@ -292,7 +292,9 @@ typedef struct {
  * input projections); up to 4 ops per launch.  A merged MATMUL launch is
  * planned for the summed rows, so its outputs may differ from the single
  * calls' in the last bits (the K split and the order of the partial sums),
- * not in precision.
+ * not in precision.  Its workspace holds the planned K split when sized by
+ * qw35_hip_matmul_prefill_workspace_size of a view with the summed rows and
+ * bytes; a smaller one (still at least each op's minimum) splits less.
  *
  * Validate the ops (same rules as the single calls) and record them; NULL on
  * error.  Recording launches nothing.  A plan whose launches split K (see
