@@ -227,9 +227,9 @@ def test_merged_delta_mixer_full_size(cuda, n):
         check_prefill(g[:, sel], x32, None, img, w_exact=om.dequant(rt.TYPE_Q8_0, sub, len(sel), k))
 
 
-@pytest.mark.parametrize("rows,k,n", [(12288, 4096, 128), (12288, 4096, 9), (12288, 4096, 32), (1024, 2048, 100),
-                                      (512, 1024, 40), (2048, 4096, 64), (12288, 4096, 200), (520, 1024, 77),
-                                      (4096, 4096, 20)])
+@pytest.mark.parametrize("rows,k,n", [(12288, 4096, 128), (12288, 4096, 9), (12288, 4096, 32), (12288, 4096, 48),
+                                      (1024, 2048, 100), (512, 1024, 40), (2048, 4096, 64), (12288, 4096, 200),
+                                      (12288, 4096, 256), (520, 1024, 77), (4096, 4096, 20)])
 @pytest.mark.parametrize("awq_on", [False, True])
 def test_plan_gate_up_equals_gate_then_up(cuda, rows, k, n, awq_on):
     import torch
