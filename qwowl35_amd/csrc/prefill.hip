@@ -527,9 +527,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     constexpr int TPW = SWI ? 1 : FN;       // distinct 32-row output tiles per wave
     constexpr int BN = 32 * TPW * NWG;
     constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave; FN: 32-row weight tiles per wave
-    constexpr int A_CHUNKS = BM * 8 / NTG;  // 16-byte token chunks per thread per step
+    // 16-byte token chunks per thread per step: BM * 8 over the part's
+    // threads, the last one only where the split is uneven (three waves per part)
+    constexpr int A_ALL = BM * 8;
+    constexpr int A_CHUNKS = (A_ALL + NTG - 1) / NTG;
     constexpr int BUF = BM * kLdsRow;
-    static_assert(BM % 32 == 0 && BM * 8 % NTG == 0 && A_CHUNKS >= 1, "token tile must split over the threads");
+    static_assert(BM % 32 == 0 && A_CHUNKS >= 1, "token tile rows in whole MFMA tiles");
     static_assert((KH == 1 || KH == 2 || KH == 4) && NW % KH == 0, "one, two or four K parts of equal wave counts");
     // (the fused gate/up kernel hands its gate and up sums over in two passes)
     static_assert(KH == 1 || (KH / 2) * NWG * FM * (SWI ? 1 : FN) * 16 * 64 * 4 <= 2 * KH * BUF,
@@ -589,9 +592,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
 
     uint32_t a_off[A_CHUNKS];
     int a_lds[A_CHUNKS];
+    // an uneven split: the last chunk of threads past the tile re-reads the
+    // tile's last chunk and stores nothing
+    const bool a_last = A_ALL % NTG == 0 || tg + (A_CHUNKS - 1) * NTG < A_ALL;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-        const int c = tg + i * NTG;
+        const int c = min(tg + i * NTG, A_ALL - 1);
         const int row = c >> 3;
         const int col = c & 7;
         const int gm = min(m0 + row, p.m - 1);
@@ -639,7 +645,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     };
     auto store_tokens = [&](const Tokens& a, uint8_t* buf) {
 #pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4_t*>(buf + a_lds[i]) = a[i];
+        for (int i = 0; i < A_CHUNKS; ++i)
+            if (i + 1 < A_CHUNKS || a_last) *reinterpret_cast<uint4_t*>(buf + a_lds[i]) = a[i];
     };
 
     float16_t acc[FM][FN];
@@ -1316,15 +1323,22 @@ PrefillCfg plan_prefill(int m_tokens, int rows, int k, bool f16w, bool q8w, bool
     // K quarters for GF4 at 33..128 tokens and k <= 4096: each 64-token block
     // runs four parts of its K range (16 steps each at k = 4096, summed in
     // LDS) instead of two of 32, with no K split and so no reduction launch,
-    // on 8 waves over 64 rows or 16 over 128, whichever fills half the CUs to
-    // all of them in one round.
+    // on 8 waves over 64 rows, 12 over 96 or 16 over 128, the first that
+    // fills half the CUs to all of them in one round.
     // Same-box A/B at M = 128 (us, plan -> quarters): 8192x4096 28.3 -> 22.0
     // (8 waves), 4096x4096 21.5 -> 19.9 (8), 12288x4096 29.5 -> 28.0 (16
     // waves); 4096x12288 (48-step quarters) was not faster, 30.5 -> 30.5-36.4.
+    // 12 waves (three per SIMD) give 12288 rows of two token tiles 256 blocks
+    // in place of 192 of 16 waves: same box, 16 -> 12 waves, us: bf16 M = 128
+    // 29.5-31.4 -> 28.1, M = 96 28.1-28.4 -> 26.7; fp32 M = 64 28.8-29.5 ->
+    // 27.7-28.2, M = 48 28.3-28.6 -> 26.7-27.0.
     if (!f16w && !q8w && m > 32 && m <= 128 && k <= 4096 && k % 1024 == 0) {
         const long tm = (m + 63) / 64;
-        const long b64 = tm * ((rows + 63) / 64), b128 = tm * ((rows + 127) / 128);
-        const int waves = 2 * b64 >= cus && b64 <= cus ? 8 : 2 * b128 >= cus && b128 <= cus ? 16 : 0;
+        const long b64 = tm * ((rows + 63) / 64), b96 = tm * ((rows + 95) / 96), b128 = tm * ((rows + 127) / 128);
+        const int waves = 2 * b64 >= cus && b64 <= cus     ? 8
+                          : 2 * b96 >= cus && b96 <= cus   ? 12
+                          : 2 * b128 >= cus && b128 <= cus ? 16
+                                                           : 0;
         if (waves) {
             best.bm = 64;
             best.fn = 2;
@@ -1385,9 +1399,11 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 
 // The gate launches the fused gate/up kernel replaces: GF4 words, unsplit, 8
 // waves of one 32-row weight tile each over 64 or 128 tokens, with K halves,
-// quarters (64 tokens) or neither (the fused kernel then holds a gate and an
-// up tile per wave; the 16-wave quarters would spill, and q8_0 and Q4_K hold
-// three 16-byte loads per tile in their load ring).
+// quarters (64 tokens) or neither; the fused kernel then holds a gate and an
+// up tile per wave.  q8_0 and Q4_K hold three 16-byte loads per tile in their
+// load ring.  The 16-wave quarters would spill; a fused 12-wave form ran about
+// the same (same box, 12288x4096: 43-44 us against 44-45 for the 8-wave K
+// halves at 48-64 tokens, 79 against 68-70 at 128 tokens) and is not built.
 bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
     if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2 || cfg.waves != 8) return false;
     if (cfg.kh == 4) return cfg.bm == 64;
@@ -1396,8 +1412,8 @@ bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
 
 // The fused gate/up launch of m tokens (fp32 input: the runtime's chunks):
 // the gate's own plan where it has the fused form; else, for fp32 input,
-//  * in place of the 16-wave 64-token K quarters (33..64 tokens): the 8-wave
-//    64-token tile with K halves;
+//  * in place of the 12- or 16-wave 64-token K quarters (33..64 tokens): the
+//    8-wave 64-token tile with K halves;
 //  * in place of a split plan at 129..256 tokens: the unsplit 8-wave
 //    128-token tile,
 // where the fused grid still gives at least half the CUs a block.  Same box,
@@ -1415,7 +1431,7 @@ bool plan_swiglu(int wkind, int m, int rows, int k, bool a_f32, size_t workspace
     PrefillCfg alt{64, 2, 1};
     alt.waves = 8;
     long blocks = 0;
-    if (cfg.bm == 64 && cfg.kh == 4 && cfg.waves == 16 && k % 512 == 0) {
+    if (cfg.bm == 64 && cfg.kh == 4 && cfg.waves > 8 && k % 512 == 0) {
         alt.kh = 2;  // 64 tokens by 128 rows per block
         blocks = (long)((ms + 63) / 64) * ((rows + 127) / 128);
     } else if (ms > 256 && ms <= 512) {
@@ -1491,8 +1507,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         // K halves exist for the 8-wave 64- and 128-token tiles of GF4 and q8_0 weights only
         if (cfg.kh == 2 && (f16w || cfg.waves != 8 || cfg.fn != 2 || (cfg.bm != 64 && cfg.bm != 128)))
             return hipErrorInvalidValue;
-        // K quarters: the 64-token GF4 tile on 16 waves (128 rows) or 8 (64 rows)
-        if (cfg.kh == 4 && (f16w || q8w || q4w || (cfg.waves != 16 && cfg.waves != 8) || cfg.fn != 2 || cfg.bm != 64))
+        // K quarters: the 64-token GF4 tile on 16 waves (128 rows), 12 (96) or 8 (64)
+        if (cfg.kh == 4 &&
+            (f16w || q8w || q4w || (cfg.waves != 16 && cfg.waves != 12 && cfg.waves != 8) || cfg.fn != 2 || cfg.bm != 64))
             return hipErrorInvalidValue;
         const int ms = staged_rows(m, af);
         uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -1589,8 +1606,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
                 break;
             case 1284: e = launch_f16_tile<128, 4, 4, 1>(p, kf32, stream); break;
             case 642:
-                e = cfg.kh == 4      ? (cfg.waves == 16 ? launch_f16_tile<64, 16, 1, 4, false, false, 4>(p, kf32, stream)
-                                                        : launch_f16_tile<64, 8, 1, 4, false, false, 4>(p, kf32, stream))
+                e = cfg.kh == 4      ? (cfg.waves == 16   ? launch_f16_tile<64, 16, 1, 4, false, false, 4>(p, kf32, stream)
+                                        : cfg.waves == 12 ? launch_f16_tile<64, 12, 1, 4, false, false, 4>(p, kf32, stream)
+                                                          : launch_f16_tile<64, 8, 1, 4, false, false, 4>(p, kf32, stream))
                     : cfg.kh == 2    ? launch_f16_tile<64, 8, 1, 2, false, false, 2>(p, kf32, stream)
                     : cfg.waves == 8 ? launch_f16_tile<64, 8, 1, 2>(p, kf32, stream)
                                      : launch_f16_tile<64, 4, 2, 2>(p, kf32, stream);

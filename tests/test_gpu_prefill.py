@@ -219,20 +219,26 @@ def test_prefill_fp32_activations_full_shapes(cuda, m, n, k):
     print(f"fp32 activations {n}x{k} M={m}: rel-L2 {err:.2e}")
 
 
-@pytest.mark.parametrize("m,n,k", [(128, 8192, 4096), (100, 4096, 4096), (128, 6000, 4096), (64, 12288, 4096),
-                                   (128, 12288, 4096), (128, 8192, 1024)])
+@pytest.mark.parametrize("m,n,k,waves", [(128, 8192, 4096, 8), (100, 4096, 4096, 8), (128, 6000, 4096, 8),
+                                         (64, 12288, 4096, 8), (128, 12288, 4096, 12), (100, 11900, 4096, 12),
+                                         (128, 16384, 4096, 16), (128, 8192, 1024, 8)])
 @pytest.mark.parametrize("out_f32", [False, True])
-def test_prefill_k_quarters(cuda, m, n, k, out_f32):
+def test_prefill_k_quarters(cuda, m, n, k, waves, out_f32):
     """Shapes the planner gives four in-block K parts (64-token tiles, k <= 4096,
-    one block per CU or fewer): 8 waves over 64 rows, or 16 over 128 rows
-    (12288 rows at M = 128); ragged tokens (100) and rows (6000); quarters of
-    256 columns (k = 1024).  GPU-packed GF4 weights, AWQ; 32 sampled token rows
-    against the oracle, to the same bars as every prefill output.  fp32
-    activations of 32..64 tokens take the same quarters (64 staged rows)."""
+    one block per CU or fewer): 8 waves over 64 rows, 12 over 96 (12288 rows at
+    M = 128; 11900 rows end in a partial tile) or 16 over 128 (16384 rows);
+    ragged tokens (100) and rows (6000); quarters of 256 columns (k = 1024).
+    GPU-packed GF4 weights, AWQ; 32 sampled token rows against the oracle, to
+    the same bars as every prefill output.  fp32 activations of half the
+    tokens stage two rows per token and take the same quarters."""
     import torch
 
     rt = _rt()
     hw, wdq, g = _gpu_gf4(rt, cuda, n, k, m + n + k)
+    c_dt = torch.float32 if out_f32 else torch.bfloat16
+    for tokens, a_dt in ((m, torch.bfloat16), (m // 2, torch.float32)):
+        desc = rt.prefill_kernel(hw, tokens, a_dt, awq=True, out_dtype=c_dt)
+        assert desc["name"].startswith(f"gf4_prefill_f16_kernel<64, {waves}, 1, 4,"), (tokens, a_dt, desc)
     a = torch.randn((m, k), generator=g, device=cuda).to(torch.bfloat16)
     awq = torch.rand((k,), generator=g, device=cuda) * 1.5 + 0.5
     out = rt.matmul_prefill(hw, a, awq=awq, out_dtype=torch.float32 if out_f32 else torch.bfloat16)
