@@ -43,6 +43,11 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kBK = 64;                 // k per pipeline step: 8 GF4 words per W row
 constexpr int kLdsRow = kBK * 2 + 16;   // bytes per staged row: 64 bf16 + 16 B pad
+// Token-tile LDS buffers per K part of the staged kernel: four (a barrier
+// every second step) for tiles of up to 128 staged rows, two (a barrier every
+// step) for the 256-row tiles, whose register allocation is at its limit.
+template <int BM>
+constexpr int token_buffers() { return BM <= 128 ? 4 : 2; }
 constexpr int kXcds = 8;
 
 struct PrefillArgs {
@@ -777,43 +782,70 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         }
     };
 
-    // Pipeline, per step kt: the step's tokens were written to LDS at the end
-    // of step kt-1 and its weight words loaded at step kt-2.  A step first
-    // issues the loads of step kt+2 (tokens into the register set the previous
-    // step emptied into LDS, words into the ring slot two ahead), then runs its
-    // MFMAs, then writes the tokens of step kt+1 to the other LDS buffer.  The
-    // words ring has four slots and the loop body covers four steps, so every
-    // register set is loaded and consumed under one static name and nothing
-    // loaded is copied across the loop back-edge (a copy would wait for the
-    // load).  Each split covers a multiple of 4 * kBK columns (the host checks
-    // k_len % 256 == 0); the prefetches past the last step re-read it instead
-    // of branching.
+    // Pipeline, per step kt: the step's weight words were loaded at step kt-2
+    // into a four-slot register ring, and its tokens sit in an LDS buffer.  A
+    // step first issues its prefetches (words into the ring slot two ahead,
+    // tokens into the register set the previous step emptied into LDS), then
+    // runs its MFMAs, then writes tokens loaded one step earlier to LDS.
+    // * Two buffers (NBUF = 2): tokens of step kt+2 are loaded, those of kt+1
+    //   written to the other buffer, and every step ends in a barrier.
+    // * Four buffers: tokens of step kt+3 are loaded, those of kt+2 written to
+    //   buffer (kt+2) mod 4, and a barrier ends every odd step.  A buffer is
+    //   read two steps after it is written, and written two steps after it
+    //   was last read, with a barrier between each pair.  Same-box A/B (us,
+    //   two -> four, bit-identical): GF4 12288x4096 fp32 M = 128 42.1 ->
+    //   40.3, 4096x12288 fp32 M = 48 29.5 -> 28.7, bf16 M = 2048 201 -> 197;
+    //   the 9B 128-token chunk 6213 -> 6148.
+    // The words ring and the loop body cover four steps, so every register
+    // set is loaded and consumed under one static name and nothing loaded is
+    // copied across the loop back-edge (a copy would wait for the load).  Each
+    // split covers a multiple of 4 * kBK columns (the host checks k_len % 256
+    // == 0); the prefetches past the last step re-read it instead of branching.
+    constexpr int NBUF = token_buffers<BM>();
+    static_assert(NBUF * KH * BUF <= 160 * 1024, "token buffers fit the CU's LDS");
     const int KT = k_len / kBK;
-    uint8_t* buf0 = smem + kh * 2 * BUF;
-    uint8_t* buf1 = buf0 + BUF;
+    uint8_t* const tbuf = smem + kh * NBUF * BUF;
     Tokens t0, t1;
     Words w0, w1, w2, w3;
     load_tokens(0, t0);
     load_words(0, w0);
     load_tokens(1, t1);
     load_words(1, w1);
-    store_tokens(t0, buf0);
+    store_tokens(t0, tbuf);
+    if constexpr (NBUF == 4) {
+        store_tokens(t1, tbuf + BUF);
+        load_tokens(min(2, KT - 1), t0);
+    }
     __syncthreads();
-    auto step = [&](int kt, Tokens& t_next, Words& w_next, const Words& w_cur, const uint8_t* cur,
-                    const Tokens& t_fill, uint8_t* fill, auto SPAN) {
-        const int ahead = min(kt + 2, KT - 1);
-        load_tokens(ahead, t_next);
-        load_words(ahead, w_next);
+    // SPAN: kt mod 4 (the unrolled position; Q8W's span offset and the buffer)
+    auto step = [&](int kt, Tokens& t_next, Words& w_next, const Words& w_cur, const Tokens& t_fill, auto SPAN) {
+        constexpr int s4 = decltype(SPAN)::value;
+        load_tokens(min(kt + NBUF / 2 + 1, KT - 1), t_next);
+        load_words(min(kt + 2, KT - 1), w_next);
         __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this step's math
-        compute(w_cur, cur, SPAN);
-        store_tokens(t_fill, fill);
-        __syncthreads();
+        compute(w_cur, tbuf + (s4 % NBUF) * BUF, SPAN);
+        store_tokens(t_fill, tbuf + ((s4 + NBUF / 2) % NBUF) * BUF);
+        if constexpr (NBUF == 2 || s4 % 2 == 1)
+            __syncthreads();
+        else
+            __builtin_amdgcn_sched_barrier(0);  // the step boundary stays a scheduling fence
     };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
     for (int kt = 0; kt < KT; kt += 4) {
-        step(kt, t0, w2, w0, buf0, t1, buf1, std::integral_constant<int, 0>{});
-        step(kt + 1, t1, w3, w1, buf1, t0, buf0, std::integral_constant<int, 1>{});
-        step(kt + 2, t0, w0, w2, buf0, t1, buf1, std::integral_constant<int, 2>{});
-        step(kt + 3, t1, w1, w3, buf1, t0, buf0, std::integral_constant<int, 3>{});
+        if constexpr (NBUF == 4) {
+            step(kt, t1, w2, w0, t0, S0{});
+            step(kt + 1, t0, w3, w1, t1, S1{});
+            step(kt + 2, t1, w0, w2, t0, S2{});
+            step(kt + 3, t0, w1, w3, t1, S3{});
+        } else {
+            step(kt, t0, w2, w0, t1, S0{});
+            step(kt + 1, t1, w3, w1, t0, S1{});
+            step(kt + 2, t0, w0, w2, t1, S2{});
+            step(kt + 3, t1, w1, w3, t0, S3{});
+        }
     }
 
     if constexpr (KH > 1) {
@@ -1091,7 +1123,7 @@ template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, 
           bool SWI = false>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
     constexpr int BN = 32 * (SWI ? 1 : FN) * NW / KH;
-    const size_t lds = 2 * (size_t)KH * BM * kLdsRow;
+    const size_t lds = (size_t)token_buffers<BM>() * KH * BM * kLdsRow;
     if ((a.k_len / KH) % 256 != 0) return hipErrorInvalidValue;  // whole four-step loop bodies per half
     PrefillArgs p = a;
     p.tiles_m = (a.m + BM - 1) / BM;
