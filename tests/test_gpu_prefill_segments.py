@@ -227,6 +227,45 @@ def test_merged_delta_mixer_full_size(cuda, n):
         check_prefill(g[:, sel], x32, None, img, w_exact=om.dequant(rt.TYPE_Q8_0, sub, len(sel), k))
 
 
+@pytest.mark.parametrize("name", ["q8_0", "gf4"])
+@pytest.mark.parametrize("room", ["planned", "staging_only"])
+def test_more_mergeable_ops_than_segments(cuda, name, room):
+    """Six mergeable ops run as launches of at most four segments (four, then
+    two), each output within 2^-20 rel-L2 of its single call and passing the
+    oracle bars.  With a workspace of only the staging bytes (room for no K
+    split, less than a merged launch would plan) the launches run unsplit and
+    give the same results."""
+    import torch
+
+    rt = _rt()
+    t = {"q8_0": rt.TYPE_Q8_0, "gf4": rt.TYPE_GF4}[name]
+    rows, k, n = [256, 128, 64, 32, 512, 96], 1024, 64
+    print(f"prefill segments {name} six ops rows={rows} workspace={room}", flush=True)
+    rng = np.random.default_rng(61 + len(name) + len(room))
+    raws, ws_list = [], []
+    for i, r in enumerate(rows):
+        raw, deq = make_weight(t, r, k, seed=900 + 11 * i)
+        raws.append((raw, deq))
+        ws_list.append(rt.HipWeight.upload(raw, t, r, k, device=cuda))
+    x32 = activations(rng, n, k)
+    x = _t(x32, cuda)
+    if room == "planned":
+        ws = _workspace(ws_list, n, cuda, merged_rows=max(sum(rows[:4]), sum(rows[4:])))
+    else:
+        staged_rows = 64 * ((n + 31) // 32)  # fp32 tokens: a hi and a lo row each, 32-token groups
+        ws = torch.empty((staged_rows * k * 2 + 255) // 256 * 256 + (n * 4 + 255) // 256 * 256, dtype=torch.uint8,
+                         device=cuda)
+    outs = [torch.full((n, r), float("nan"), dtype=torch.float32, device=cuda) for r in rows]
+    got = _run_plan(ws_list, x, outs, ws)
+    big = _workspace(ws_list, n, cuda)
+    for (raw, deq), w, g, r in zip(raws, ws_list, got, rows):
+        single = rt.matmul_prefill(w, x, out_dtype=torch.float32, workspace=big)
+        torch.cuda.synchronize()
+        assert om.rel_l2(g.cpu().numpy().astype(np.float64), single.cpu().numpy().astype(np.float64)) <= MERGED_REL_L2
+        img = om.prefill_image(t, raw, r, k).astype(np.float32) if t != rt.TYPE_GF4 else deq
+        check_prefill(g, x32, None, img, w_exact=deq if t != rt.TYPE_GF4 else None)
+
+
 @pytest.mark.parametrize("rows,k,n", [(12288, 4096, 128), (12288, 4096, 9), (12288, 4096, 32), (12288, 4096, 48),
                                       (1024, 2048, 100), (512, 1024, 40), (2048, 4096, 64), (12288, 4096, 200),
                                       (12288, 4096, 256), (520, 1024, 77), (4096, 4096, 20)])
