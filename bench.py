@@ -118,15 +118,29 @@ class Bench:
                 c(self.stream)
         return g
 
+    # Windows of up to this many launches issue them one by one behind the
+    # warm-up work; longer ones replay one graph holding all of them.
+    DIRECT_MAX = 64
+    # GPU time the warm-up replays queue ahead of the window's start event.
+    BACKLOG_MS = 4.0
+
     def time_launches(self, calls, launches: int, warmup: int):
         """Time exactly ``launches`` launches, rotating over ``calls`` (one launch
-        each), replayed from graphs; returns (ms per launch, launches).
+        each); returns (ms per launch, launches).
 
-        Both graphs (the full rotation and the remainder) are replayed before
-        the timed window, and the window's start event is queued behind
-        warm-up replays still running on the GPU: the window then holds the
-        kernels back to back, not the latency of a first or an idle-GPU graph
-        launch (which a short window, e.g. 20 launches, would otherwise carry)."""
+        The window's start event is queued behind at least BACKLOG_MS of
+        warm-up replays still running on the GPU, so the window holds kernels
+        back to back: not an idle GPU's first launch, and not the host's time
+        to submit the timed work (a graph launch prepares its nodes before the
+        first one runs; a 200-launch window behind 0.45 ms of warm-up measured
+        7.41 us per headline launch against 6.85 behind 2.8 ms).  A graph
+        replay boundary inside the window costs about 5-20 us (about 0.14 us
+        per launch when a 32-launch rotation graph is replayed 125 times,
+        0.2-1 us per launch of a 20-launch window), so the window holds none:
+        up to DIRECT_MAX launches are issued one by one (the backlog also
+        covers about 0.1 ms of host time per call), longer windows are one
+        graph of exactly that many launches, whose one boundary is spread over
+        all of them."""
         torch = self.torch
         n = len(calls)
         launches = max(1, int(launches))
@@ -134,23 +148,28 @@ class Bench:
             for c in calls:  # first touch and code-object load outside the capture
                 c(self.stream)
         torch.cuda.synchronize()
-        full = self._graph(calls)
-        reps, rem = divmod(launches, n)
-        part = self._graph(calls[:rem]) if rem else None
+        direct = launches <= self.DIRECT_MAX
+        warm = self._graph([calls[i % n] for i in range(max(int(warmup), 2 * n))])
+        timed = None if direct else self._graph([calls[i % n] for i in range(launches)])
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(self.stream):  # replays and events on the same stream
-            if part is not None:
-                part.replay()
-            full.replay()
-            torch.cuda.synchronize()
-            for _ in range(max(2, -(-warmup // n))):  # keeps the GPU busy while the window is queued
-                full.replay()
+        with torch.cuda.stream(self.stream):  # replays, launches and events on the same stream
+            if timed is not None:
+                timed.replay()
             ev0.record(self.stream)
-            for _ in range(reps):
-                full.replay()
-            if part is not None:
-                part.replay()
+            warm.replay()
+            ev1.record(self.stream)
+            torch.cuda.synchronize()
+            warm_ms = max(ev0.elapsed_time(ev1), 1e-3)
+            backlog_ms = self.BACKLOG_MS + (0.1 * launches if direct else 0.0)
+            for _ in range(max(2, -(-int(backlog_ms * 1000) // int(warm_ms * 1000 + 1)))):
+                warm.replay()  # still running while the window is queued
+            ev0.record(self.stream)
+            if timed is not None:
+                timed.replay()
+            else:
+                for i in range(launches):
+                    calls[i % n](self.stream)
             ev1.record(self.stream)
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) / launches, launches
