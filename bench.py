@@ -122,7 +122,7 @@ class Bench:
     # warm-up work; longer ones replay one graph holding all of them.
     DIRECT_MAX = 64
     # GPU time the warm-up replays queue ahead of the window's start event.
-    BACKLOG_MS = 4.0
+    BACKLOG_MS = 20.0
 
     def time_launches(self, calls, launches: int, warmup: int):
         """Time exactly ``launches`` launches, rotating over ``calls`` (one launch
@@ -133,7 +133,10 @@ class Bench:
         back to back: not an idle GPU's first launch, and not the host's time
         to submit the timed work (a graph launch prepares its nodes before the
         first one runs; a 200-launch window behind 0.45 ms of warm-up measured
-        7.41 us per headline launch against 6.85 behind 2.8 ms).  A graph
+        7.41 us per headline launch against 6.85 behind 2.8 ms).  The first
+        window of a process also ran slow behind 4 ms (20 headline launches:
+        7.32-7.56 us) and not behind 20 ms (6.99-7.02, against 6.82 for 4000
+        launches).  A graph
         replay boundary inside the window costs about 5-20 us (about 0.14 us
         per launch when a 32-launch rotation graph is replayed 125 times,
         0.2-1 us per launch of a 20-launch window), so the window holds none:
