@@ -136,14 +136,13 @@ class Bench:
         7.41 us per headline launch against 6.85 behind 2.8 ms).  The first
         window of a process also ran slow behind 4 ms (20 headline launches:
         7.32-7.56 us) and not behind 20 ms (6.99-7.02, against 6.82 for 4000
-        launches).  A graph
-        replay boundary inside the window costs about 5-20 us (about 0.14 us
-        per launch when a 32-launch rotation graph is replayed 125 times,
-        0.2-1 us per launch of a 20-launch window), so the window holds none:
-        up to DIRECT_MAX launches are issued one by one (the backlog also
-        covers about 0.1 ms of host time per call), longer windows are one
-        graph of exactly that many launches, whose one boundary is spread over
-        all of them."""
+        launches).  A graph replay boundary inside the window costs about
+        5-20 us (about 0.14 us per launch when a 32-launch rotation graph is
+        replayed 125 times, 0.2-1 us per launch of a 20-launch window), so the
+        window holds none: up to DIRECT_MAX launches are issued one by one
+        (the backlog also covers about 0.1 ms of host time per call), longer
+        windows are one graph of exactly that many launches, whose one
+        boundary is spread over all of them."""
         torch = self.torch
         n = len(calls)
         launches = max(1, int(launches))
