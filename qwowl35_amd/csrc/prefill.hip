@@ -527,16 +527,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 //   the epilogue writes silu(g) * u, g and u each the fp32 value the gate
 //   launch (STORE) and the up launch (SWIGLU epilogue) of the same plan would
 //   form -- the same K partition and MFMA order per tile, so the same bits.
+//   FN = 1 (mixed tiles): a wave's one tile holds 16 rows of the gate (rows
+//   0..15) and the same 16 rows of the up projection (rows 16..31); a lane's
+//   accumulators hold rows 8 g + 4 h + r, so gate row c and up row c pair up
+//   in the same lane (g and g + 2).  A block then covers 16 rows per wave of
+//   a K part, e.g. 96 rows on 6 waves: 12288 rows in 128 column tiles.
 template <int BM, int NW, int FN, int WPE, bool OUT_F32, bool F16W = false, bool Q8W = false, int KH = 1,
           bool Q4W = false, bool SWI = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gf4_prefill_f16_kernel(
     PrefillArgs p) {
-    static_assert(!SWI || (FN == 2 && OUT_F32 && !F16W && !Q8W && !Q4W),
-                  "fused gate/up: GF4 words, a gate and an up tile per wave");
+    static_assert(!SWI || ((FN == 1 || FN == 2) && OUT_F32 && !F16W && !Q8W && !Q4W),
+                  "fused gate/up: GF4 words, a gate and an up tile per wave or one mixed tile");
+    constexpr bool MIX = SWI && FN == 1;    // one tile of 16 gate and 16 up rows per wave
     constexpr int NWG = NW / KH;            // waves per K half
     constexpr int NTG = 64 * NWG;           // threads per K half
     constexpr int TPW = SWI ? 1 : FN;       // distinct 32-row output tiles per wave
-    constexpr int BN = 32 * TPW * NWG;
+    constexpr int BN = (MIX ? 16 : 32 * TPW) * NWG;  // output rows (columns of C) per block
     constexpr int FM = BM / 32;             // 32-token MFMA tiles per wave; FN: 32-row weight tiles per wave
     // 16-byte token chunks per thread per step: BM * 8 over the part's
     // threads, the last one only where the split is uneven (three waves per part)
@@ -546,7 +552,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     static_assert(BM % 32 == 0 && A_CHUNKS >= 1, "token tile rows in whole MFMA tiles");
     static_assert((KH == 1 || KH == 2 || KH == 4) && NW % KH == 0, "one, two or four K parts of equal wave counts");
     // (the fused gate/up kernel hands its gate and up sums over in two passes)
-    static_assert(KH == 1 || (KH / 2) * NWG * FM * (SWI ? 1 : FN) * 16 * 64 * 4 <= 2 * KH * BUF,
+    static_assert(KH == 1 || (KH / 2) * NWG * FM * (SWI ? 1 : FN) * 16 * 64 * 4 <= token_buffers<BM>() * KH * BUF,
                   "K-part partial sums fit the token buffers");
     typedef float float16_t __attribute__((ext_vector_type(16)));
     typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
@@ -594,7 +600,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     // own token tile; the parts are summed in LDS at the end.
     const int kh = KH > 1 ? wave / NWG : 0;
     const int tg = tid - kh * NTG;
-    const int n0 = tn * BN + (wave - kh * NWG) * 32 * TPW;
+    const int n0 = tn * BN + (wave - kh * NWG) * (MIX ? 16 : 32 * TPW);
     const int K = p.k;
     const int k_len = p.k_len / KH;
     const int k_begin = split * p.k_len + kh * k_len;
@@ -619,7 +625,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
     const uint8_t* w_src[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const size_t row = (size_t)min(n0 + (SWI ? 0 : 32 * j) + l32, N - 1);
+        const size_t row = (size_t)min(n0 + (MIX ? (l32 & 15) : (SWI ? 0 : 32 * j) + l32), N - 1);
         if constexpr (Q4W)
             w_src[j] = reinterpret_cast<const uint8_t*>(W) + row * (size_t)(K / 256 * 144) + (k_begin / 256) * 144;
         else if constexpr (Q8W)
@@ -627,7 +633,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
                        32 * half;
         else
             w_src[j] = F16W ? reinterpret_cast<const uint8_t*>(W) + (row * K + k_begin + 32 * half) * 2
-                            : reinterpret_cast<const uint8_t*>((SWI && j == 1 ? p.w_up : W) + row * words_per_row +
+                            : reinterpret_cast<const uint8_t*>(((MIX ? l32 >= 16 : SWI && j == 1) ? p.w_up : W) +
+                                                               row * words_per_row +
                                                                (k_begin >> 3) + 4 * half);
     }
     // Q8W: byte selectors for this lane half (span dword i -> q dword i; d -> (d, d))
@@ -935,12 +942,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WP
         float* const cf = static_cast<float*>(C);
         const bool vec = (ld & 3) == 0 && ((uintptr_t)C & 15) == 0;
         auto put_row = [&](int gm, float rs, auto v_of) {
+            // two tiles: row 8 g + 4 h + r of tile 0 (gate) and tile 1 (up);
+            // mixed: that row (g < 2) and row 16 + that row of tile 0
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+            for (int g = 0; g < (MIX ? 2 : 4); ++g) {
                 const int gn = n0 + 8 * g + 4 * half;
                 float d[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) d[r] = epilogue(kEpiSwiglu, v_of(0, g, r) * rs, v_of(1, g, r) * rs);
+                for (int r = 0; r < 4; ++r)
+                    d[r] = MIX ? epilogue(kEpiSwiglu, v_of(0, g, r) * rs, v_of(0, g + 2, r) * rs)
+                               : epilogue(kEpiSwiglu, v_of(0, g, r) * rs, v_of(FN - 1, g, r) * rs);
                 float* const dst = cf + (size_t)gm * ld + gn;
                 if (vec && gn + 3 < N) {
                     *reinterpret_cast<float4_t*>(dst) = float4_t{d[0], d[1], d[2], d[3]};
@@ -1128,7 +1139,7 @@ __global__ __launch_bounds__(kReduceThreads) void prefill_split_reduce(const flo
 template <int BM, int NW, int FN, int WPE, bool F16W = false, bool Q8W = false, int KH = 1, bool Q4W = false,
           bool SWI = false>
 hipError_t launch_f16_tile(const PrefillArgs& a, bool out_f32, hipStream_t s) {
-    constexpr int BN = 32 * (SWI ? 1 : FN) * NW / KH;
+    constexpr int BN = (SWI && FN == 1 ? 16 : 32 * (SWI ? 1 : FN)) * NW / KH;
     const size_t lds = (size_t)token_buffers<BM>() * KH * BM * kLdsRow;
     if ((a.k_len / KH) % 256 != 0) return hipErrorInvalidValue;  // whole four-step loop bodies per half
     PrefillArgs p = a;
@@ -1443,7 +1454,9 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 // the same (same box, 12288x4096: 43-44 us against 44-45 for the 8-wave K
 // halves at 48-64 tokens, 79 against 68-70 at 128 tokens) and is not built.
 bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
-    if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2 || cfg.waves != 8) return false;
+    if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2) return false;
+    if (cfg.waves == 12) return cfg.bm == 128 && cfg.kh == 2;  // mixed tiles
+    if (cfg.waves != 8) return false;
     if (cfg.kh == 4) return cfg.bm == 64;
     return (cfg.kh == 1 || cfg.kh == 2) && (cfg.bm == 64 || cfg.bm == 128);
 }
@@ -1463,7 +1476,17 @@ bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
 bool plan_swiglu(int wkind, int m, int rows, int k, bool a_f32, size_t workspace_bytes, PrefillCfg& cfg) {
     cfg = plan_prefill_kind(m, rows, k, wkind, a_f32);
     fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32);
-    if (swiglu_cfg_ok(wkind, cfg)) return true;
+    if (swiglu_cfg_ok(wkind, cfg)) {
+        // The gate's 128-token tile with K halves: as mixed tiles (96 rows
+        // per block, three waves per SIMD) where that grid fills more CUs in
+        // one round; the same K partition, so the same bits.
+        if (cfg.bm == 128 && cfg.kh == 2 && cfg.waves == 8) {
+            const long tm = (staged_rows(m, a_f32) + 127) / 128;
+            const long b96 = tm * ((rows + 95) / 96), b128 = tm * ((rows + 127) / 128);
+            if (b96 > b128 && b96 <= num_cus()) cfg.waves = 12;
+        }
+        return true;
+    }
     if (wkind != 0 || !a_f32) return false;
     const int ms = staged_rows(m, a_f32);
     PrefillCfg alt{64, 2, 1};
@@ -1543,7 +1566,8 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         // fp32 input: hi and lo tiles pair up inside a wave's token tiles
         if (af && cfg.bm < 64) return hipErrorInvalidValue;
         // K halves exist for the 8-wave 64- and 128-token tiles of GF4 and q8_0 weights only
-        if (cfg.kh == 2 && (f16w || cfg.waves != 8 || cfg.fn != 2 || (cfg.bm != 64 && cfg.bm != 128)))
+        if (cfg.kh == 2 && (f16w || (cfg.waves != 8 && !(w_up && cfg.waves == 12)) || cfg.fn != 2 ||
+                            (cfg.bm != 64 && cfg.bm != 128)))
             return hipErrorInvalidValue;
         // K quarters: the 64-token GF4 tile on 16 waves (128 rows), 12 (96) or 8 (64)
         if (cfg.kh == 4 &&
@@ -1586,6 +1610,8 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         if (split) p.c = partial;
         const bool kf32 = of || split;
         if (w_up) {
+            if (cfg.bm == 128 && cfg.waves == 12)  // mixed tiles, K halves: three waves per SIMD
+                return launch_f16_tile<128, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
             if (cfg.bm == 128)
                 return cfg.kh == 2 ? launch_f16_tile<128, 8, 2, 2, false, false, 2, false, true>(p, true, stream)
                                    : launch_f16_tile<128, 8, 2, 2, false, false, 1, false, true>(p, true, stream);
