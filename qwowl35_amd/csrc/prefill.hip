@@ -1453,12 +1453,19 @@ void fit_prefill_workspace(int m, int rows, int k, PrefillCfg& cfg, size_t works
 // load ring.  The 16-wave quarters would spill; a fused 12-wave form ran about
 // the same (same box, 12288x4096: 43-44 us against 44-45 for the 8-wave K
 // halves at 48-64 tokens, 79 against 68-70 at 128 tokens) and is not built.
-bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
-    if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2) return false;
-    if (cfg.waves == 12) return cfg.bm == 128 && cfg.kh == 2;  // mixed tiles
-    if (cfg.waves != 8) return false;
+bool swiglu_tile_ok(int wkind, const PrefillCfg& cfg) {
+    if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2 || cfg.waves != 8) return false;
     if (cfg.kh == 4) return cfg.bm == 64;
     return (cfg.kh == 1 || cfg.kh == 2) && (cfg.bm == 64 || cfg.bm == 128);
+}
+
+// A fused launch's configuration: those tiles, or their mixed form (12 waves;
+// the 12-wave K quarters of an unfused plan are not one).
+bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
+    if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2) return false;
+    if (cfg.waves == 12)
+        return (cfg.bm == 128 && cfg.kh == 2) || (cfg.bm == 64 && (cfg.kh == 2 || cfg.kh == 4));
+    return swiglu_tile_ok(wkind, cfg);
 }
 
 // The fused gate/up launch of m tokens (fp32 input: the runtime's chunks):
@@ -1476,15 +1483,19 @@ bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
 bool plan_swiglu(int wkind, int m, int rows, int k, bool a_f32, size_t workspace_bytes, PrefillCfg& cfg) {
     cfg = plan_prefill_kind(m, rows, k, wkind, a_f32);
     fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32);
-    if (swiglu_cfg_ok(wkind, cfg)) {
-        // The gate's 128-token tile with K halves: as mixed tiles (96 rows
-        // per block, three waves per SIMD) where that grid fills more CUs in
-        // one round; the same K partition, so the same bits.
-        if (cfg.bm == 128 && cfg.kh == 2 && cfg.waves == 8) {
-            const long tm = (staged_rows(m, a_f32) + 127) / 128;
-            const long b96 = tm * ((rows + 95) / 96), b128 = tm * ((rows + 127) / 128);
-            if (b96 > b128 && b96 <= num_cus()) cfg.waves = 12;
-        }
+    // An 8-wave fused tile as mixed tiles (three waves per SIMD, 16 rows per
+    // wave of a K part: 96 rows per block with K halves, 48 with quarters)
+    // where that grid fills more CUs in one round; the same K partition, so
+    // the same bits.
+    auto mixed = [&](PrefillCfg& c) {
+        if (c.waves != 8 || c.splits != 1 || (c.kh != 2 && c.kh != 4) || (c.kh == 4 && c.bm != 64)) return;
+        const long tm = (staged_rows(m, a_f32) + c.bm - 1) / c.bm;
+        const int rows_mixed = c.kh == 4 ? 48 : 96, rows_two = c.kh == 4 ? 64 : 128;
+        const long b_mixed = tm * ((rows + rows_mixed - 1) / rows_mixed), b_two = tm * ((rows + rows_two - 1) / rows_two);
+        if (b_mixed > b_two && b_mixed <= num_cus()) c.waves = 12;
+    };
+    if (swiglu_tile_ok(wkind, cfg)) {
+        mixed(cfg);
         return true;
     }
     if (wkind != 0 || !a_f32) return false;
@@ -1501,6 +1512,7 @@ bool plan_swiglu(int wkind, int m, int rows, int k, bool a_f32, size_t workspace
     }
     if (2 * blocks < num_cus()) return false;
     cfg = alt;
+    mixed(cfg);
     return true;
 }
 
@@ -1610,8 +1622,11 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         if (split) p.c = partial;
         const bool kf32 = of || split;
         if (w_up) {
-            if (cfg.bm == 128 && cfg.waves == 12)  // mixed tiles, K halves: three waves per SIMD
-                return launch_f16_tile<128, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
+            if (cfg.waves == 12) {  // mixed tiles: three waves per SIMD
+                if (cfg.bm == 128) return launch_f16_tile<128, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
+                return cfg.kh == 4 ? launch_f16_tile<64, 12, 1, 3, false, false, 4, false, true>(p, true, stream)
+                                   : launch_f16_tile<64, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
+            }
             if (cfg.bm == 128)
                 return cfg.kh == 2 ? launch_f16_tile<128, 8, 2, 2, false, false, 2, false, true>(p, true, stream)
                                    : launch_f16_tile<128, 8, 2, 2, false, false, 1, false, true>(p, true, stream);
