@@ -1464,7 +1464,7 @@ bool swiglu_tile_ok(int wkind, const PrefillCfg& cfg) {
 bool swiglu_cfg_ok(int wkind, const PrefillCfg& cfg) {
     if (wkind != 0 || cfg.splits != 1 || cfg.fn != 2) return false;
     if (cfg.waves == 12)
-        return (cfg.bm == 128 && cfg.kh == 2) || (cfg.bm == 64 && (cfg.kh == 2 || cfg.kh == 4));
+        return (cfg.bm == 128 && (cfg.kh == 1 || cfg.kh == 2)) || (cfg.bm == 64 && (cfg.kh == 2 || cfg.kh == 4));
     return swiglu_tile_ok(wkind, cfg);
 }
 
@@ -1484,13 +1484,18 @@ bool plan_swiglu(int wkind, int m, int rows, int k, bool a_f32, size_t workspace
     cfg = plan_prefill_kind(m, rows, k, wkind, a_f32);
     fit_prefill_workspace(m, rows, k, cfg, workspace_bytes, a_f32);
     // An 8-wave fused tile as mixed tiles (three waves per SIMD, 16 rows per
-    // wave of a K part: 96 rows per block with K halves, 48 with quarters)
-    // where that grid fills more CUs in one round; the same K partition, so
-    // the same bits.
+    // wave of a K part: 192 rows per block without K parts, 96 with K halves,
+    // 48 with quarters) where that grid fills more CUs in one round; the same
+    // K partition, so the same bits.
     auto mixed = [&](PrefillCfg& c) {
-        if (c.waves != 8 || c.splits != 1 || (c.kh != 2 && c.kh != 4) || (c.kh == 4 && c.bm != 64)) return;
+        if (c.waves != 8 || c.splits != 1 || (c.kh == 4 && c.bm != 64) || (c.kh == 1 && c.bm != 128)) return;
         const long tm = (staged_rows(m, a_f32) + c.bm - 1) / c.bm;
-        const int rows_mixed = c.kh == 4 ? 48 : 96, rows_two = c.kh == 4 ? 64 : 128;
+        const int rows_mixed = 192 / c.kh, rows_two = 256 / c.kh;
+        // without K parts only up to three token tiles: at four (193..256
+        // tokens) the mixed form was 0.5-1% slower (same box, gate/up op at
+        // 224 / 256 tokens 103.7 / 105.8 -> 104.2 / 106.7 us; 129 / 192
+        // tokens 87.7 / 90.7 -> 80.1 / 88.3)
+        if (c.kh == 1 && tm > 3) return;
         const long b_mixed = tm * ((rows + rows_mixed - 1) / rows_mixed), b_two = tm * ((rows + rows_two - 1) / rows_two);
         if (b_mixed > b_two && b_mixed <= num_cus()) c.waves = 12;
     };
@@ -1623,7 +1628,9 @@ hipError_t launch_gf4_prefill_cfg(const void* w, int rows, int k, const void* a,
         const bool kf32 = of || split;
         if (w_up) {
             if (cfg.waves == 12) {  // mixed tiles: three waves per SIMD
-                if (cfg.bm == 128) return launch_f16_tile<128, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
+                if (cfg.bm == 128)
+                    return cfg.kh == 1 ? launch_f16_tile<128, 12, 1, 3, false, false, 1, false, true>(p, true, stream)
+                                       : launch_f16_tile<128, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
                 return cfg.kh == 4 ? launch_f16_tile<64, 12, 1, 3, false, false, 4, false, true>(p, true, stream)
                                    : launch_f16_tile<64, 12, 1, 3, false, false, 2, false, true>(p, true, stream);
             }
